@@ -1,0 +1,155 @@
+/* wxx_hip.h — C ABI of libwxx_hip.so, the MI355X (gfx950) backend of wxx.
+ *
+ * Each entry point replaces one WGSL dispatch (or one runtime service) of the
+ * reference's WebGPU backend; the comment on each names the reference
+ * interface it stands in for (paths under the reference's src/wxx/).
+ *
+ * Conventions:
+ *  - all functions return 0 on success or a negative WXX_E_* code; the text
+ *    of the last failure (per host thread) is wxx_last_error();
+ *  - pointers are device addresses from wxx_alloc (already advanced to the
+ *    first element of a view); sizes, shapes and strides are int64 element
+ *    counts; f32 data is IEEE binary32, u32 indices are uint32, c64 is
+ *    interleaved (re, im) binary32 pairs;
+ *  - every call enqueues on the library's single in-order HIP stream (the
+ *    reference's single shared compute pass); only wxx_d2h, wxx_sync and
+ *    wxx_timer_elapsed wait for the device.
+ */
+#ifndef WXX_HIP_H
+#define WXX_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  WXX_OK = 0,
+  WXX_E_HIP = -1,
+  WXX_E_ARG = -2,
+  WXX_E_OOM = -3,
+  WXX_E_INIT = -4,
+  WXX_E_RANGE = -5,
+  WXX_E_UNSUPPORTED = -6
+};
+
+/* ---- runtime: replaces WebGPUContext / GPUBufferPool / GPUCommandBuffer
+ *      (backend/device.py:9-273) and Tensor storage I/O (Tensor.py:66-90,
+ *      522-569) ---------------------------------------------------------- */
+const char* wxx_last_error(void);
+int wxx_device_count(int* count);
+/* device.py:11-13 (adapter + device request) */
+int wxx_init(int device);
+int wxx_device_info(int* compute_units, char* name, int name_len, size_t* total_mem);
+/* GPUBufferPool.create_buffer / release (device.py:53-61, 88-113) */
+void* wxx_alloc(size_t bytes);
+int wxx_free(void* ptr);
+/* GPUBufferPool.clear_cache (device.py:135-141) */
+int wxx_empty_cache(void);
+/* GPUBufferPool.get_memory_snapshot (device.py:115-133) */
+int wxx_mem_stats(size_t* live, size_t* cached, size_t* peak, size_t* n_malloc);
+/* create_buffer_with_data upload (device.py:63-86) */
+int wxx_h2d(void* dst, const void* src, size_t bytes);
+/* Tensor.read_buffer readback (Tensor.py:552-569) */
+int wxx_d2h(void* dst, const void* src, size_t bytes);
+int wxx_d2d(void* dst, const void* src, size_t bytes);
+/* Tensor(value=...) fill (Tensor.py:66-78) */
+int wxx_fill_u32(void* dst, int64_t n, uint32_t bits);
+/* GPUCommandBuffer.flush(wait=True) (device.py:208-224) */
+int wxx_sync(void);
+void* wxx_stream(void);
+int wxx_timer_record(int slot);
+int wxx_timer_elapsed(int start, int stop, float* ms);
+
+/* ---- A: GEMM — functional.matmul_add (functional/utils.py:378-499) +
+ *      shaders/matmul.wgsl.  sA/sB = batch strides (0 = unbatched);
+ *      bias_mode 0 none, 1 (N,), 2 (M,N), 3 (batch,M,N); tile 0 = auto. ---- */
+int wxx_matmul_add(const float* A, const float* B, const float* bias, float* C, int64_t M,
+                   int64_t N, int64_t K, int64_t batch, int64_t sA, int64_t sB, int64_t sBias,
+                   int bias_mode, int transpose_A, int transpose_B, int tile);
+
+/* ---- D: reductions over (outer, reduce, inner) ------------------------- */
+/* functional.sum / mean / sumsq (functional/reductions.py:27-197); mode 0/1/2 */
+int wxx_reduce(const float* x, float* out, int64_t outer, int64_t reduce, int64_t inner,
+               int mode);
+/* functional.max / min (functional/reductions.py:241-312); op 0 max, 1 min */
+int wxx_reduce_minmax(const float* x, float* vals, uint32_t* idx, int64_t outer,
+                      int64_t reduce, int64_t inner, int op);
+/* functional.maxmin_backward (functional/reductions.py:200-237) */
+int wxx_maxmin_backward(const float* g, const uint32_t* idx, float* out, int64_t outer,
+                        int64_t reduce, int64_t inner);
+/* functional.softmax (functional/activations.py:126-173) */
+int wxx_softmax(const float* x, float* y, int64_t outer, int64_t C, int64_t inner);
+/* functional.meanvarnorm (functional/normalization.py:82-145); row_cap 0 = all rows */
+int wxx_meanvarnorm(const float* x, const float* gamma, const float* beta, float* y,
+                    float* mean, float* inv_std, int64_t outer, int64_t reduce, int64_t inner,
+                    float eps, int64_t row_cap);
+/* functional.meanvarnormdx (functional/normalization.py:308-359) */
+int wxx_meanvarnormdx(const float* dy, const float* x, const float* gamma, const float* mean,
+                      const float* inv_std, float* dx, int64_t outer, int64_t reduce,
+                      int64_t inner, int64_t row_cap);
+/* functional.meanvarnormdg (functional/normalization.py:362-412) */
+int wxx_meanvarnormdg(const float* dy, const float* x, const float* mean, const float* inv_std,
+                      float* dgamma, float* dbeta, int64_t outer, int64_t reduce,
+                      int64_t inner);
+/* functional.rmsnorm (functional/normalization.py:24-79) */
+int wxx_rmsnorm(const float* x, const float* gamma, float* y, float* inv_rms, int64_t outer,
+                int64_t reduce, int64_t inner, float eps, int64_t row_cap);
+/* functional.rmsnormdx (functional/normalization.py:415-463) */
+int wxx_rmsnormdx(const float* dy, const float* x, const float* gamma, const float* inv_rms,
+                  float* dx, int64_t outer, int64_t reduce, int64_t inner);
+/* functional.rmsnormdg (functional/normalization.py:466-513) */
+int wxx_rmsnormdg(const float* dy, const float* x, const float* inv_rms, float* dgamma,
+                  int64_t outer, int64_t reduce, int64_t inner);
+/* functional.batchnorm (functional/normalization.py:148-206); HW = H*W */
+int wxx_batchnorm(const float* x, const float* gamma, const float* beta, float* running_mean,
+                  float* running_var, float* y, float* saved_mean, float* inv_std, int64_t B,
+                  int64_t C, int64_t HW, float eps, float momentum, int training);
+/* functional.batchnormdg (functional/normalization.py:260-305) */
+int wxx_batchnormdg(const float* dy, const float* x, const float* saved_mean,
+                    const float* inv_std, float* dgamma, float* dbeta, int64_t B, int64_t C,
+                    int64_t HW);
+/* functional.batchnormdx (functional/normalization.py:209-257) */
+int wxx_batchnormdx(const float* dy, const float* x, const float* gamma, const float* dgamma,
+                    const float* dbeta, const float* saved_mean, const float* inv_std,
+                    float* dx, int64_t B, int64_t C, int64_t HW);
+
+/* ---- E: elementwise / layout -------------------------------------------- */
+/* functional.pointwise (functional/pointwise.py:29-98) and, with out == a,
+ * functional._pointwise (pointwise.py:231-289); op 0 add 1 sub 2 mul 3 div */
+int wxx_pointwise(float* out, const float* a, const float* b, int rank, const int64_t* shape,
+                  const int64_t* s_out, const int64_t* s_a, const int64_t* s_b, int op);
+/* functional.scalarpointwise (functional/pointwise.py:101-146) */
+int wxx_scalarpointwise(const float* x, float* y, int64_t n, int op, float c, int reverse);
+/* backend/dispatch.py:_unary_op (:59-89) for the activation and unary math
+ * kernels of functional/activations.py:22-124 and pointwise.py:293-354 */
+int wxx_unary(const float* x, float* y, int64_t n, int op);
+/* functional.clamp / clampbackwards (pointwise.py:149-228), masked_fill
+ * (functional/utils.py:558-597); mode 0/1/2 */
+int wxx_clamp(const float* x, float* y, int64_t n, float lo, float hi, int mode);
+/* functional.equal / equal_number (functional/utils.py:502-556) */
+int wxx_equal(const void* a, const void* b, float* out, int64_t n, int mode, uint32_t number);
+/* functional.mul_backward (functional/pointwise.py:460-502) */
+int wxx_mul_backward(const float* g, const float* a, const float* b, float* da, float* db,
+                     int64_t n);
+/* functional.contiguous (functional/utils.py:316-369), complex_contiguous
+ * (functional/fft.py:295-342), assign from a tensor (utils.py:29-101) */
+int wxx_copy_strided(void* dst, const void* src, int itemsize, int rank, const int64_t* shape,
+                     const int64_t* s_dst, const int64_t* s_src);
+/* functional.assign with a scalar (functional/utils.py:29-101) */
+int wxx_fill_strided(void* dst, int rank, const int64_t* shape, const int64_t* s_dst,
+                     uint32_t bits);
+/* functional.scatter_zeros (functional/utils.py:760-827) */
+int wxx_scatter_zeros(float* out, const float* grad, int rank, const int64_t* shape,
+                      const int64_t* s_grad, int dim, int64_t start, int64_t length);
+/* functional.unfolddx (functional/utils.py:239-287) */
+int wxx_unfolddx(const float* dy, float* dx, int64_t prefix, int64_t length, int64_t suffix,
+                 int64_t windows, int64_t size, int64_t step);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WXX_HIP_H */

@@ -1,0 +1,47 @@
+"""Test configuration.
+
+Markers: ``gpu`` tests need a HIP device and call the C ABI of
+``libwxx_hip.so``; everything else runs on the CPU (oracle pinning, host
+logic, library exports).  GPU tests never skip for a missing device: on a
+GPU box a missing device or library is a failure.
+"""
+
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (HIP device) and libwxx_hip.so")
+
+
+@pytest.fixture(scope="session")
+def device():
+    """Open the HIP device once (fails loudly when unavailable)."""
+    from wxx_amd.backend import device as dev
+
+    dev.ensure_device()
+    return dev
+
+
+def rng(seed=0):
+    return np.random.default_rng(seed)
+
+
+def assert_close(actual, expected, rtol=1e-4, atol=1e-5, msg=""):
+    actual = np.asarray(actual)
+    expected = np.asarray(expected)
+    assert actual.shape == expected.shape, f"{msg} shape {actual.shape} != {expected.shape}"
+    if not np.allclose(actual, expected, rtol=rtol, atol=atol, equal_nan=True):
+        err = np.abs(actual.astype(np.float64) - expected.astype(np.float64))
+        bad = ~np.isclose(actual, expected, rtol=rtol, atol=atol, equal_nan=True)
+        raise AssertionError(
+            f"{msg} max abs err {np.nanmax(err):.3g}; {int(bad.sum())} of {bad.size} "
+            f"elements outside rtol={rtol} atol={atol}"
+        )

@@ -1,0 +1,140 @@
+"""GPU parity: elementwise, scalar, unary and layout kernels vs the oracle."""
+
+import numpy as np
+import pytest
+
+from conftest import assert_close, rng
+from oracle import activations as oa
+from oracle import elementwise as oe
+
+pytestmark = pytest.mark.gpu
+
+
+def F():
+    from wxx_amd import functional
+
+    return functional
+
+
+def up(a):
+    return F().from_numpy(np.asarray(a, np.float32))
+
+
+@pytest.mark.parametrize("op", [0, 1, 2, 3])
+@pytest.mark.parametrize("sa,sb", [((5, 7), (5, 7)), ((3, 1), (1, 4)), ((8, 1024, 768), (768,)),
+                                   ((96, 128, 128), (128, 128)), ((2, 3, 4, 5), (3, 1, 5)),
+                                   ((1,), (6,)), ((4097,), (4097,))])
+def test_pointwise_broadcast(device, op, sa, sb):
+    a = rng(1).standard_normal(sa).astype(np.float32)
+    b = rng(2).standard_normal(sb).astype(np.float32) + (3.0 if op == 3 else 0.0)
+    got = F().pointwise(up(a), up(b), op).numpy()
+    assert_close(got, oe.pointwise(a, b, op), rtol=1e-6, atol=1e-6)
+
+
+def test_pointwise_strided_views(device):
+    # reference tests/test_pointwise.py:90-112
+    x = rng(4).standard_normal((4, 6, 8)).astype(np.float32)
+    y = rng(5).standard_normal((4, 6, 8)).astype(np.float32)
+    xt = F().permute(up(x), 0, 2, 1)
+    yt = F().permute(up(y), 0, 2, 1)
+    assert not xt.is_contiguous()
+    assert_close(F().pointwise(xt, yt, 2).numpy(), np.transpose(x, (0, 2, 1)) * np.transpose(y, (0, 2, 1)))
+    X, Y = up(x), up(y)
+    assert_close(F().pointwise(X[1:], Y[1:], 0).numpy(), x[1:] + y[1:])
+    assert_close(F().scalarpointwise(X[:, ::2, :], 3.0, 2).numpy(), x[:, ::2, :] * 3.0)
+    col = F().permute(X, 0, 2, 1)[:, :, :1]
+    assert_close(F().pointwise(col, F().permute(Y, 0, 2, 1), 0).numpy(),
+                 np.transpose(x, (0, 2, 1))[:, :, :1] + np.transpose(y, (0, 2, 1)))
+
+
+def test_pointwise_inplace_and_alias(device):
+    a = rng(6).standard_normal((3, 4)).astype(np.float32)
+    b = rng(7).standard_normal((4,)).astype(np.float32)
+    ta = up(a)
+    F()._pointwise(ta, up(b), 0)
+    assert_close(ta.numpy(), a + b)
+    c = up(np.array([1.0, 2.0, 3.0]))
+    F()._pointwise(c, c, 0)
+    assert np.array_equal(c.numpy(), np.array([2.0, 4.0, 6.0], np.float32))
+
+
+@pytest.mark.parametrize("op,c,rev", [(0, 2.5, 0), (1, 2.5, 0), (1, 2.5, 1), (2, -1.5, 0),
+                                      (3, 3.0, 0), (3, -1.0, 0), (3, 2.0, 0), (3, 0.5, 0),
+                                      (3, 2.5, 1), (4, 2.0, 0), (4, 2.0, 1)])
+def test_scalarpointwise(device, op, c, rev):
+    x = np.array([[-2.0, -0.5, 0.5, 2.0], [0.25, 1.5, 3.0, 4.0], [-3.0, -2.0, 2.0, 3.0]],
+                 np.float32)
+    x = np.concatenate([x, rng(8).standard_normal((5, 4)).astype(np.float32)])
+    got = F().scalarpointwise(up(x), c, op, rev).numpy()
+    assert_close(got, oe.scalarpointwise(x, c, op, rev), rtol=2e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("name", sorted(oa.UNARY))
+def test_unary(device, name):
+    from wxx_amd.functional import activations as fa
+
+    x = (rng(9).standard_normal(10001) * 4).astype(np.float32)
+    x[:4] = [0.0, 10.5, -10.5, 100.0]
+    if name in ("log", "sqrt", "rsqrt"):
+        x = np.abs(x) + 0.1
+    if name == "sigmoidbackwards":
+        x = oa.sigmoid(x)
+    got = fa.unary(up(x), name).numpy()
+    assert_close(got, oa.UNARY[name](x), rtol=2e-6, atol=2e-6)
+
+
+def test_clamp_equal_masked_fill(device):
+    x = rng(10).standard_normal(1000).astype(np.float32)
+    x[:3] = 0.0
+    assert np.array_equal(F().clamp(up(x), -0.5, 0.7).numpy(), oe.clamp(x, -0.5, 0.7))
+    assert np.array_equal(F().clampbackwards(up(x), -0.5, 0.7).numpy(),
+                          oe.clampbackwards(x, -0.5, 0.7))
+    assert np.array_equal(F().masked_fill(up(x), -1e9).numpy(), oe.masked_fill(x, -1e9))
+    assert np.array_equal(F().equal(up(x), up(x)).numpy(), np.ones(1000, np.float32))
+    assert np.array_equal(F().equal_number(up(x), 0.0).numpy(), oe.equal(x, 0.0))
+    u = F().from_numpy(np.arange(10) % 3, dtype=np.uint32)
+    assert np.array_equal(F().equal_number(u, 2).numpy(), (np.arange(10) % 3 == 2).astype(np.float32))
+
+
+def test_mul_backward(device):
+    g, a, b = (rng(i).standard_normal((7, 9)).astype(np.float32) for i in (11, 12, 13))
+    da, db = F().mul_backward(up(g), up(a), up(b))
+    ea, eb = oe.mul_backward(g, a, b)
+    assert np.array_equal(da.numpy(), ea) and np.array_equal(db.numpy(), eb)
+
+
+@pytest.mark.parametrize("shape,perm", [((4, 6, 8), (0, 2, 1)), ((8, 1024, 12, 64), (0, 2, 1, 3)),
+                                        ((64, 96), (1, 0)), ((2, 3, 4, 5, 6), (4, 2, 0, 3, 1)),
+                                        ((1000, 3), (1, 0))])
+def test_contiguous_bit_exact(device, shape, perm):
+    x = rng(14).standard_normal(shape).astype(np.float32)
+    got = F().contiguous(F().permute(up(x), *perm)).numpy()
+    assert np.array_equal(got, np.ascontiguousarray(np.transpose(x, perm)))
+
+
+def test_assign_and_scatter_and_unfold(device):
+    x = np.zeros((5, 6), np.float32)
+    t = up(x)
+    F().assign(t[1:4, ::2], 7.0)
+    x[1:4, ::2] = 7.0
+    assert np.array_equal(t.numpy(), x)
+    src = rng(15).standard_normal((3, 3)).astype(np.float32)
+    F().assign(t[1:4, ::2], up(src))
+    x[1:4, ::2] = src
+    assert np.array_equal(t.numpy(), x)
+    g = rng(16).standard_normal((2, 3, 4)).astype(np.float32)
+    out = F().scatter_zeros(up(g), (2, 7, 4), 1, 2).numpy()
+    ref = np.zeros((2, 7, 4), np.float32)
+    ref[:, 2:5] = g
+    assert np.array_equal(out, ref)
+    # unfold backward: scatter-add of overlapping windows
+    inp = (2, 10, 3)
+    size, step = 4, 2
+    windows = (10 - size) // step + 1
+    dy = rng(17).standard_normal((2, windows, 3, size)).astype(np.float32)
+    dx = F().unfolddx(up(dy), inp, 1, size, step).numpy()
+    ref = np.zeros(inp, np.float64)
+    for l in range(windows):
+        for w in range(size):
+            ref[:, l * step + w, :] += dy[:, l, :, w]
+    assert_close(dx, ref, atol=1e-6)

@@ -1,0 +1,99 @@
+"""GPU parity: the fp32 MFMA GEMM (functional.matmul_add) against the oracle.
+
+Small and ragged shapes are compared in full against the float64 oracle;
+the BASELINE config-2 sizes are compared on row samples against the
+exact-order fp32 restatement of the reference kernel (oracle/csrc/gemm_ref.c)
+plus a full-matrix linearity identity."""
+
+import numpy as np
+import pytest
+
+from conftest import assert_close, rng
+from oracle import gemm as og
+
+pytestmark = pytest.mark.gpu
+
+
+def F():
+    from wxx_amd import functional
+
+    return functional
+
+
+def up(a):
+    return F().from_numpy(np.asarray(a, np.float32))
+
+
+def tol(K):
+    # fp32 dot products of length K with N(0,1) entries: |C| ~ sqrt(K)
+    return dict(rtol=1e-4, atol=1e-5 * max(1.0, np.sqrt(K)))
+
+
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (7, 5, 9), (64, 64, 16), (128, 128, 128),
+                                   (130, 67, 33), (256, 384, 96), (17, 682, 256),
+                                   (300, 200, 1000), (64, 1024, 17), (5, 3, 0)])
+def test_matmul_transposes_ragged(device, ta, tb, M, N, K):
+    r = rng(M * 7 + N * 3 + K)
+    A = r.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    B = r.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    got = F().matmul_add(up(A), up(B), None, transpose_A=ta, transpose_B=tb).numpy()
+    assert_close(got, og.matmul_add(A, B, None, ta, tb), **tol(K))
+
+
+@pytest.mark.parametrize("bias_kind", ["none", "vec", "mat", "batched"])
+@pytest.mark.parametrize("layout", ["A_batched", "both_batched", "B_batched"])
+def test_matmul_batch_and_bias_modes(device, bias_kind, layout):
+    r = rng(11)
+    b, M, K, N = 3, 37, 20, 45
+    A = r.standard_normal((b, M, K) if layout != "B_batched" else (M, K)).astype(np.float32)
+    B = r.standard_normal((b, K, N) if layout != "A_batched" else (K, N)).astype(np.float32)
+    bias = {"none": None, "vec": r.standard_normal(N), "mat": r.standard_normal((M, N)),
+            "batched": r.standard_normal((b, M, N))}[bias_kind]
+    bt = None if bias is None else up(bias)
+    got = F().matmul_add(up(A), up(B), bt).numpy()
+    assert_close(got, og.matmul_add(A, B, bias), **tol(K))
+
+
+def test_matmul_attention_shapes(device):
+    r = rng(12)
+    q = r.standard_normal((12, 128, 64)).astype(np.float32)
+    k = r.standard_normal((12, 128, 64)).astype(np.float32)
+    s = F().matmul_add(up(q), up(k), None, transpose_B=True).numpy()
+    assert_close(s, og.matmul_add(q, k, None, False, True), **tol(64))
+    p = r.standard_normal((12, 128, 128)).astype(np.float32)
+    o = F().matmul_add(up(p), up(k), None).numpy()
+    assert_close(o, og.matmul_add(p, k), **tol(128))
+    # weight-gradient shape: A^T @ g with batch
+    g = r.standard_normal((12, 128, 64)).astype(np.float32)
+    dw = F().matmul_add(up(q), up(g), None, transpose_A=True).numpy()
+    assert_close(dw, og.matmul_add(q, g, None, True, False), **tol(128))
+
+
+@pytest.mark.parametrize("M,N,K", [(1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096),
+                                   (8192, 3072, 768), (8192, 768, 3072)])
+def test_matmul_config2_sizes(device, M, N, K):
+    r = rng(10 + M % 7)
+    A = r.standard_normal((M, K)).astype(np.float32)
+    B = r.standard_normal((K, N)).astype(np.float32)
+    tA, tB = up(A), up(B)
+    C = F().matmul_add(tA, tB, None).numpy()
+    rows = r.integers(0, M - 8)
+    ref = og.matmul_add_fma(A, B, rows=(rows, rows + 8))[rows:rows + 8]
+    assert_close(C[rows:rows + 8], ref, **tol(K))
+    # full-matrix identity: A @ (B 1) == (A @ B) 1, checked in float64
+    ones = np.ones(N)
+    lhs = C.astype(np.float64) @ ones
+    rhs = A.astype(np.float64) @ (B.astype(np.float64) @ ones)
+    assert_close(lhs, rhs, rtol=1e-4, atol=1e-3 * np.sqrt(K * N))
+
+
+def test_matmul_errors(device):
+    a = up(np.ones((3, 4)))
+    with pytest.raises(ValueError):
+        F().matmul_add(a, up(np.ones((5, 2))), None)
+    with pytest.raises(ValueError):
+        F().matmul_add(up(np.ones((2, 3, 4))), up(np.ones((3, 4, 2))), None)
+    with pytest.raises(ValueError):
+        F().matmul_add(a, up(np.ones((4, 2))), up(np.ones(3)))

@@ -1,0 +1,127 @@
+"""GPU parity: LayerNorm, RMSNorm and BatchNorm forward/backward vs the oracle."""
+
+import numpy as np
+import pytest
+
+from conftest import assert_close, rng
+from oracle import norms as on
+
+pytestmark = pytest.mark.gpu
+
+
+def F():
+    from wxx_amd import functional
+
+    return functional
+
+
+def up(a):
+    return F().from_numpy(np.asarray(a, np.float32))
+
+
+SHAPES = [((2, 3, 4), -1), ((8192, 4096), -1), ((8, 1024, 768), -1), ((4, 128, 256), -1),
+          ((5, 100), -1), ((3, 7, 5), 1), ((6, 20000), -1), ((9, 130), -1), ((2, 3), 0)]
+
+
+@pytest.mark.parametrize("shape,axis", SHAPES)
+def test_layernorm_fwd_bwd(device, shape, axis):
+    r = rng(len(shape) * 10 + shape[-1] % 97)
+    x = (r.standard_normal(shape) * 2 + 0.5).astype(np.float32)
+    red = shape[axis]
+    g = r.standard_normal(red).astype(np.float32)
+    b = r.standard_normal(red).astype(np.float32)
+    y, mu, inv = F().meanvarnorm(up(x), up(g), up(b), axis=axis)
+    ey, emu, einv = on.meanvarnorm(x, g, b, axis=axis)
+    assert_close(mu.numpy(), emu, atol=1e-5)
+    assert_close(inv.numpy(), einv, rtol=1e-4)
+    assert_close(y.numpy(), ey, rtol=1e-4, atol=1e-4)
+    dy = r.standard_normal(shape).astype(np.float32)
+    dx = F().meanvarnormdx(up(dy), up(x), up(g), mu, inv, axis=axis)
+    assert_close(dx.numpy(), on.meanvarnormdx(dy, x, g, emu, einv, axis=axis), rtol=1e-4,
+                 atol=1e-4)
+    dg, db = F().meanvarnormdg(up(dy), up(x), mu, inv, axis=axis)
+    edg, edb = on.meanvarnormdg(dy, x, emu, einv, axis=axis)
+    n = x.size // red
+    assert_close(dg.numpy(), edg, rtol=1e-4, atol=1e-5 * np.sqrt(n) * 10)
+    assert_close(db.numpy(), edb, rtol=1e-4, atol=1e-5 * np.sqrt(n) * 10)
+
+
+def test_layernorm_reference_test_case(device):
+    x = rng(0).standard_normal((2, 3, 4)).astype(np.float32)
+    y, _, _ = F().meanvarnorm(up(x), up(np.ones(4)), up(np.zeros(4)), axis=-1)
+    ref = (x - x.mean(axis=-1, keepdims=True)) / np.sqrt(x.var(axis=-1, keepdims=True) + 1e-5)
+    assert_close(y.numpy(), ref, atol=1e-4)
+
+
+def test_norm_zero_rows_and_row_cap(device):
+    from wxx_amd.backend import compat
+
+    x = rng(1).standard_normal((65537, 8)).astype(np.float32)
+    x[3] = 0.0
+    g = rng(2).standard_normal(8).astype(np.float32)
+    b = rng(3).standard_normal(8).astype(np.float32)
+    y, mu, inv = F().meanvarnorm(up(x), up(g), up(b))
+    assert inv.numpy()[3] == 0.0
+    assert_close(y.numpy()[3], b)
+    assert np.any(y.numpy()[65535:] != 0)  # default: every row computed
+    yr, rr = F().rmsnorm(up(x), up(g))
+    assert rr.numpy()[3] == 0.0
+    compat.REFERENCE_ROW_CAP = True
+    try:
+        yc, muc, invc = F().meanvarnorm(up(x), up(g), up(b))
+        ey, emu, einv = on.meanvarnorm(x, g, b, row_cap=65535)
+        assert np.all(yc.numpy()[65535:] == 0) and np.all(invc.numpy()[65535:] == 0)
+        assert_close(yc.numpy(), ey, atol=1e-4)
+        yrc, rrc = F().rmsnorm(up(x), up(g))
+        assert np.all(yrc.numpy()[65535:] == 0) and np.all(rrc.numpy()[65535:] == 0)
+    finally:
+        compat.REFERENCE_ROW_CAP = False
+
+
+@pytest.mark.parametrize("shape,axis", [((2, 4), -1), ((8, 8192, 256), -1), ((3, 5, 7), 1),
+                                        ((4, 3000), -1)])
+def test_rmsnorm_fwd_bwd(device, shape, axis):
+    r = rng(50 + shape[-1] % 13)
+    x = r.standard_normal(shape).astype(np.float32)
+    red = shape[axis]
+    g = r.standard_normal(red).astype(np.float32)
+    y, irms = F().rmsnorm(up(x), up(g), axis=axis)
+    ey, er = on.rmsnorm(x, g, axis=axis)
+    assert_close(irms.numpy(), er, rtol=1e-4)
+    assert_close(y.numpy(), ey, rtol=1e-4, atol=1e-4)
+    dy = r.standard_normal(shape).astype(np.float32)
+    dx = F().rmsnormdx(up(dy), up(x), up(g), irms, axis=axis)
+    assert_close(dx.numpy(), on.rmsnormdx(dy, x, g, er, axis=axis), rtol=1e-4, atol=1e-4)
+    dg = F().rmsnormdg(up(dy), up(x), up(g), irms, axis=axis)
+    n = x.size // red
+    assert_close(dg.numpy(), on.rmsnormdg(dy, x, er, axis=axis), rtol=1e-4,
+                 atol=1e-5 * np.sqrt(n) * 10)
+
+
+@pytest.mark.parametrize("shape", [(4, 3, 2, 2), (128, 64, 16, 16), (128, 512, 1, 1),
+                                   (2, 5, 7, 3)])
+@pytest.mark.parametrize("training", [True, False])
+def test_batchnorm(device, shape, training):
+    r = rng(60)
+    C = shape[1]
+    x = r.standard_normal(shape).astype(np.float32)
+    g = r.standard_normal(C).astype(np.float32)
+    b = r.standard_normal(C).astype(np.float32)
+    rm0 = r.standard_normal(C).astype(np.float32)
+    rv0 = (r.random(C) + 0.5).astype(np.float32)
+    rm, rv = up(rm0), up(rv0)
+    y, mu, inv = F().batchnorm(up(x), up(g), up(b), rm, rv, training=training)
+    ey, emu, einv, erm, erv = on.batchnorm(x, g, b, rm0, rv0, training)
+    assert_close(mu.numpy(), emu, atol=1e-5)
+    assert_close(inv.numpy(), einv, rtol=1e-4)
+    assert_close(y.numpy(), ey, rtol=1e-4, atol=1e-4)
+    assert_close(rm.numpy(), erm, atol=1e-5)
+    assert_close(rv.numpy(), erv, rtol=1e-4, atol=1e-5)
+    dy = r.standard_normal(shape).astype(np.float32)
+    dg, db = F().batchnormdg(up(dy), up(x), mu, inv)
+    edg, edb = on.batchnormdg(dy, x, emu, einv)
+    n = x.size // C
+    assert_close(dg.numpy(), edg, rtol=1e-4, atol=1e-5 * np.sqrt(n) * 10)
+    assert_close(db.numpy(), edb, rtol=1e-4, atol=1e-5 * np.sqrt(n) * 10)
+    dx = F().batchnormdx(up(dy), up(x), up(g), dg, db, mu, inv)
+    assert_close(dx.numpy(), on.batchnormdx(dy, x, g, edg, edb, emu, einv), rtol=1e-3, atol=1e-4)

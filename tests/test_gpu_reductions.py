@@ -1,0 +1,113 @@
+"""GPU parity: reductions and softmax against the oracle (via the C ABI)."""
+
+import numpy as np
+import pytest
+
+from conftest import assert_close, rng
+from oracle import activations as oa
+from oracle import reductions as orr
+
+pytestmark = pytest.mark.gpu
+
+
+def F():
+    from wxx_amd import functional
+
+    return functional
+
+
+def up(a):
+    return F().from_numpy(np.asarray(a, np.float32))
+
+
+@pytest.mark.parametrize("shape,axis,keepdims", [
+    ((4, 5), None, False), ((4, 5), 0, False), ((4, 5), 1, True), ((4, 5), -1, False),
+    ((2, 3, 4, 5), (1, 2), False), ((7,), 0, False), ((3, 100000), 1, False),
+    ((1, 10_000_000), None, False), ((8, 589824), 0, False), ((1000, 3, 7), 1, True),
+    ((5, 1, 9), 1, False), ((2, 4097, 3), 1, False),
+])
+@pytest.mark.parametrize("mode", [0, 1, 2])
+def test_reduce_modes(device, shape, axis, keepdims, mode):
+    x = rng(sum(shape) + mode).standard_normal(shape).astype(np.float32)
+    fn = [F().sum, F().mean, F().sumsq][mode]
+    got = fn(up(x), axis=axis, keepdims=keepdims).numpy()
+    exp = orr.reduce(x, axis=axis, keepdims=keepdims, mode=mode)
+    # fp32 summation in a different order than the float64 oracle: allow
+    # 1e-6 of each output's L1 mass (a wrong index or a dropped block is off
+    # by O(sqrt(n)) times more).
+    mass = orr.reduce(np.abs(x), axis=axis, keepdims=keepdims, mode=2 if mode == 2 else mode)
+    atol = 1e-5 + 1e-6 * np.abs(mass).astype(np.float64)
+    err = np.abs(got.astype(np.float64) - exp)
+    assert got.shape == exp.shape
+    assert np.all(err <= atol + 1e-4 * np.abs(exp)), float(np.max(err - atol))
+
+
+def test_reduce_reference_test_case(device):
+    # reference tests/test_reductions.py:10-15
+    a = rng(0).standard_normal((4, 5)).astype(np.float32)
+    t = up(a)
+    assert_close(F().sum(t).numpy(), a.sum(keepdims=False).reshape(1), atol=1e-4)
+    assert_close(F().sum(t, axis=0).numpy(), a.sum(axis=0), atol=1e-4)
+    assert_close(F().sum(t, axis=1, keepdims=True).numpy(), a.sum(axis=1, keepdims=True), atol=1e-4)
+    assert_close(F().mean(t, axis=-1).numpy(), a.mean(axis=-1), atol=1e-4)
+
+
+@pytest.mark.parametrize("op", [0, 1])
+@pytest.mark.parametrize("shape,axis", [((3, 4), 1), ((3, 4), 0), ((5, 700), 1), ((2, 600, 3), 1),
+                                        ((1, 100000), None), ((64, 1024), -1)])
+def test_minmax_bit_exact(device, op, shape, axis):
+    r = rng(40 + op)
+    x = r.integers(-3, 4, size=shape).astype(np.float32)  # many ties: exercises the tie rule
+    fn = F().max if op == 0 else F().min
+    v, i = fn(up(x), axis=axis)
+    ev, ei = orr.minmax(x, axis=axis, op=op)
+    assert np.array_equal(v.numpy(), ev)
+    assert i.type == "u32"
+    assert np.array_equal(i.numpy(), ei)
+
+
+def test_minmax_special_values(device):
+    x = np.array([[0.0, 5.0, 5.0, 1.0], [-np.inf, -np.inf, -np.inf, -np.inf],
+                  [np.nan, 2.0, np.nan, 2.0], [-1e38, -1e38, -2e38, -1e38]], np.float32)
+    v, i = F().max(up(x), axis=1)
+    ev, ei = orr.minmax(x, axis=1, op=0)
+    assert np.array_equal(i.numpy(), ei) and np.array_equal(v.numpy(), ev)
+    assert list(ei) == [2, 0, 1, 0]
+
+
+def test_maxmin_backward(device):
+    x = rng(5).standard_normal((6, 33)).astype(np.float32)
+    g = rng(6).standard_normal(6).astype(np.float32)
+    _, i = F().max(up(x), axis=1)
+    d = F().maxmin_backward(up(g), i, x.shape, axis=1).numpy()
+    assert np.array_equal(d, orr.maxmin_backward(g, i.numpy(), x.shape, axis=1))
+
+
+@pytest.mark.parametrize("shape,dim", [((3, 5), -1), ((8192, 4096), -1), ((96, 1024, 1024), -1),
+                                       ((512, 128), -1), ((7, 3000), 1), ((4, 20000), -1),
+                                       ((2, 50304), -1), ((4, 6, 3), 1), ((5, 7), 0),
+                                       ((33, 1), -1), ((10, 10), -1)])
+def test_softmax(device, shape, dim):
+    x = (rng(7).standard_normal(shape) * 3).astype(np.float32)
+    got = F().softmax(up(x), dim).numpy()
+    if np.prod(shape) > 20_000_000:
+        # large case: check invariants on all rows, values on a row sample
+        assert_close(got.sum(axis=dim), np.ones(got.sum(axis=dim).shape, np.float32), atol=2e-5)
+        idx = rng(8).integers(0, shape[0], 4)
+        assert_close(got[idx], oa.softmax(x[idx], dim))
+    else:
+        assert_close(got, oa.softmax(x, dim))
+
+
+def test_softmax_reference_test_case(device):
+    a = rng(3).standard_normal((3, 5)).astype(np.float32)
+    ref = np.exp(a) / np.exp(a).sum(axis=-1, keepdims=True)
+    assert_close(F().softmax(up(a), dim=-1).numpy(), ref, atol=1e-5)
+
+
+def test_softmax_masked_rows(device):
+    x = rng(9).standard_normal((4, 64)).astype(np.float32)
+    x[:, 10:] += -1e9  # additive causal-mask style
+    got = F().softmax(up(x), -1).numpy()
+    assert_close(got, oa.softmax(x, -1))
+    assert np.all(got[:, 10:] == 0)

@@ -1,0 +1,383 @@
+"""Pin the CPU oracle before trusting it (CPU-only).
+
+Each oracle function is checked against something independent of its own
+formula: the closed forms in the reference's tests (same seeds and shapes),
+brute-force simulations of the reference kernels on small inputs, finite
+differences for every backward, and identities.  Each check is chosen so a
+plausible slip (dropped term, wrong tie rule, wrong eps, transposed operand)
+fails it.
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+from conftest import assert_close, rng
+from oracle import activations as oa
+from oracle import elementwise as oe
+from oracle import gemm as og
+from oracle import norms as on
+from oracle import reductions as orr
+
+# ---------------------------------------------------------------- reductions
+
+
+def test_reduce_matches_reference_test_closed_forms():
+    # reference tests/test_reductions.py:10-15
+    a = rng(0).standard_normal((4, 5)).astype(np.float32)
+    assert_close(orr.reduce(a), np.array([a.sum()], np.float32), atol=1e-5)
+    assert_close(orr.reduce(a, axis=0), a.sum(axis=0), atol=1e-5)
+    assert_close(orr.reduce(a, axis=1, keepdims=True), a.sum(axis=1, keepdims=True), atol=1e-5)
+    assert_close(orr.reduce(a, axis=-1, mode=1), a.mean(axis=-1), atol=1e-5)
+    assert_close(orr.reduce(a, axis=1, mode=2), (a.astype(np.float64) ** 2).sum(axis=1), atol=1e-5)
+
+
+def _simulate_minmax_row(row, op):
+    """Literal scalar simulation of reduce_minmax.wgsl for one output."""
+    init = -1e38 if op == 0 else 1e38
+
+    def better(c, cur):
+        return c > cur if op == 0 else c < cur
+
+    vals, idxs = [], []
+    for t in range(256):
+        bv, bi = np.float32(init), 0
+        r = t
+        while r < len(row):
+            if better(row[r], bv):
+                bv, bi = row[r], r
+            r += 256
+        vals.append(bv)
+        idxs.append(bi)
+    s = 128
+    while s >= 1:
+        for i in range(s):
+            if better(vals[i + s], vals[i]):
+                vals[i], idxs[i] = vals[i + s], idxs[i + s]
+        s //= 2
+    return vals[0], idxs[0]
+
+
+def test_minmax_matches_reference_test():
+    # reference tests/test_reductions.py:18-24
+    a = rng(1).standard_normal((3, 4)).astype(np.float32)
+    v, i = orr.minmax(a, axis=1, op=0)
+    assert_close(v, a.max(axis=1))
+    assert np.array_equal(i.astype(np.int64), a.argmax(axis=1))
+    v2, _ = orr.minmax(a, axis=0, op=1)
+    assert_close(v2, a.min(axis=0))
+
+
+@pytest.mark.parametrize("op", [0, 1])
+def test_minmax_tie_rule_brute_force(op):
+    r = rng(7)
+    cases = [
+        np.where(np.arange(600) % 7 == 3, 5.0, 0.0),   # many ties across lanes and chunks
+        np.array([0.0, 5.0, 5.0] + [0.0] * 10),        # lanes 1 and 2 tie: lane 2 wins
+        np.full(300, -1e38),                            # never strictly better than init
+        np.full(10, -np.inf),
+        np.array([np.nan, 1.0, np.nan, 1.0]),
+        r.integers(-2, 3, size=1000).astype(np.float64),
+    ]
+    for row in cases:
+        row = (row if op == 0 else -row).astype(np.float32)
+        ev, ei = _simulate_minmax_row(row, op)
+        v, i = orr.minmax(row, axis=None, op=op)
+        assert int(i[0]) == ei, (row[:8], int(i[0]), ei)
+        assert np.float32(v[0]) == np.float32(ev)
+    # the reference rule is not numpy's first occurrence
+    _, i = orr.minmax(np.array([0.0, 5.0, 5.0], np.float32), axis=None, op=0)
+    assert int(i[0]) == 2
+
+
+def test_minmax_inner_axis_brute_force():
+    x = rng(8).integers(0, 3, size=(3, 300, 4)).astype(np.float32)
+    v, i = orr.minmax(x, axis=1, op=0)
+    for o in range(3):
+        for k in range(4):
+            ev, ei = _simulate_minmax_row(x[o, :, k], 0)
+            assert int(i[o, k]) == ei and v[o, k] == ev
+
+
+def test_maxmin_backward_routes_to_index():
+    x = rng(9).standard_normal((4, 6)).astype(np.float32)
+    v, i = orr.minmax(x, axis=1, op=0)
+    g = rng(10).standard_normal(4).astype(np.float32)
+    d = orr.maxmin_backward(g, i, x.shape, axis=1)
+    expect = np.zeros_like(x)
+    expect[np.arange(4), x.argmax(axis=1)] = g
+    assert np.array_equal(d, expect)
+
+
+# ---------------------------------------------------------------- softmax / unary
+
+
+def test_softmax_matches_reference_test_closed_form():
+    # reference tests/test_activations.py:34-38
+    a = rng(3).standard_normal((3, 5)).astype(np.float32)
+    ref = np.exp(a) / np.exp(a).sum(axis=-1, keepdims=True)
+    assert_close(oa.softmax(a, -1), ref, atol=1e-5)
+    # along another axis, and shift invariance
+    b = rng(4).standard_normal((4, 6, 3)).astype(np.float32)
+    assert_close(oa.softmax(b, 1), oa.softmax(b + 100.0, 1), atol=1e-5)
+    assert_close(oa.softmax(b, 1).sum(axis=1), np.ones((4, 3), np.float32), atol=1e-6)
+
+
+def test_activations_match_reference_tests():
+    # reference tests/test_activations.py:9-31
+    a = rng(0).standard_normal((5, 7)).astype(np.float32)
+    tanh_gelu = a * 0.5 * (1 + np.tanh(np.sqrt(2 / np.pi) * (a + 0.044715 * a ** 3)))
+    assert_close(oa.gelu(a), tanh_gelu, atol=1e-3)
+    assert_close(oa.sigmoid(a), 1 / (1 + np.exp(-a)), atol=1e-5)
+    assert_close(oa.UNARY["relu"](a), np.maximum(a, 0))
+    b = (rng(1).standard_normal((4, 6)) * 0.5).astype(np.float32)
+    assert_close(oa.UNARY["sin"](b), np.sin(b), atol=1e-6)
+    assert_close(oa.UNARY["cos"](b), np.cos(b), atol=1e-6)
+    # clamps of the reference kernels
+    assert oa.gelu(np.float32(11.0)) == np.float32(11.0)
+    assert oa.gelu(np.float32(-11.0)) == 0.0
+    assert oa.gelubackwards(np.float32(12.0)) == 1.0
+    assert oa.sigmoid(np.float32(-1000.0)) > 0.0  # clamped at -88, not 0
+
+
+@pytest.mark.parametrize("name,fwd", [("gelubackwards", "gelu"), ("selubackwards", "selu"),
+                                      ("relubackwards", "relu"), ("sinback", "sin"),
+                                      ("cosback", "cos")])
+def test_local_derivatives_by_finite_differences(name, fwd):
+    # h = 1e-3 keeps float32 output rounding (~1e-4 here) below the
+    # tolerance while a wrong derivative constant is off by > 1e-2.
+    x = np.linspace(-3.0, 3.0, 61) + 0.013  # avoid the kink of relu at 0
+    h = 1e-3
+    f = oa.UNARY[fwd]
+    num = (f(x + h).astype(np.float64) - f(x - h)) / (2 * h)
+    assert_close(oa.UNARY[name](x), num, rtol=2e-3, atol=2e-3)
+
+
+def test_sigmoid_derivative_from_output():
+    x = np.linspace(-4, 4, 17)
+    y = oa.sigmoid(x)
+    num = (oa.sigmoid(x + 1e-3).astype(np.float64) - oa.sigmoid(x - 1e-3)) / 2e-3
+    assert_close(oa.sigmoidbackwards(y), num, rtol=1e-3, atol=1e-4)
+
+
+# ---------------------------------------------------------------- norms
+
+
+def test_layernorm_matches_reference_test():
+    # reference tests/test_normalization.py:12-21
+    x = rng(0).standard_normal((2, 3, 4)).astype(np.float32)
+    y, mu, inv = on.meanvarnorm(x, np.ones(4), np.zeros(4), axis=-1)
+    ref = (x - x.mean(axis=-1, keepdims=True)) / np.sqrt(x.var(axis=-1, keepdims=True) + 1e-5)
+    assert_close(y, ref, atol=1e-4)
+    assert_close(mu, x.mean(axis=-1))
+
+
+def test_rmsnorm_matches_reference_test():
+    # reference tests/test_normalization.py:24-30
+    x = rng(1).standard_normal((2, 4)).astype(np.float32)
+    y, r = on.rmsnorm(x, np.ones(4), axis=-1)
+    ref = x / np.sqrt((x ** 2).mean(axis=-1, keepdims=True) + 1e-6)
+    assert_close(y, ref, atol=1e-4)
+
+
+def test_norm_zero_rules_and_row_cap():
+    x = np.zeros((3, 8), np.float32)
+    x[1] = rng(2).standard_normal(8)
+    g = rng(3).standard_normal(8).astype(np.float32)
+    b = rng(4).standard_normal(8).astype(np.float32)
+    y, mu, inv = on.meanvarnorm(x, g, b)
+    assert inv[0] == 0.0 and inv[2] == 0.0 and inv[1] > 0
+    assert_close(y[0], b)  # zero-variance row: inv_std = 0 -> y = beta
+    y2, r = on.rmsnorm(x, g)
+    assert r[0] == 0.0 and np.all(y2[0] == 0.0)
+    yc, _, ic = on.meanvarnorm(x, g, b, row_cap=2)
+    assert np.all(yc[2] == 0.0) and ic[2] == 0.0 and np.array_equal(yc[:2], y[:2])
+
+
+def _fd_grad(f, x, eps=1e-5):
+    g = np.zeros_like(x, dtype=np.float64)
+    flat = x.reshape(-1)
+    for k in range(flat.size):
+        old = flat[k]
+        flat[k] = old + eps
+        fp = f(x)
+        flat[k] = old - eps
+        fm = f(x)
+        flat[k] = old
+        g.reshape(-1)[k] = (fp - fm) / (2 * eps)
+    return g
+
+
+def test_layernorm_backward_by_finite_differences():
+    r = rng(5)
+    x = r.standard_normal((3, 6))
+    g = r.standard_normal(6)
+    b = r.standard_normal(6)
+    dy = r.standard_normal((3, 6))
+
+    def ln64(xx, gg=g, bb=b):
+        mu = xx.mean(axis=-1, keepdims=True)
+        var = (xx * xx).mean(axis=-1, keepdims=True) - mu * mu
+        return (xx - mu) / np.sqrt(var + 1e-5) * gg + bb
+
+    _, mu, inv = on.meanvarnorm(x.astype(np.float32), g, b)
+    dx = on.meanvarnormdx(dy, x, g, mu, inv)
+    num = _fd_grad(lambda xx: float((ln64(xx) * dy).sum()), x.copy())
+    assert_close(dx, num, rtol=1e-3, atol=1e-4)
+    dg, db = on.meanvarnormdg(dy, x, mu, inv)
+    num_g = _fd_grad(lambda gg: float((ln64(x, gg=gg) * dy).sum()), g.copy())
+    assert_close(dg, num_g, rtol=1e-3, atol=1e-4)
+    assert_close(db, dy.sum(axis=0), atol=1e-5)
+
+
+def test_rmsnorm_backward_by_finite_differences():
+    r = rng(6)
+    x = r.standard_normal((2, 5))
+    g = r.standard_normal(5)
+    dy = r.standard_normal((2, 5))
+
+    def rms64(xx, gg=g):
+        return xx / np.sqrt((xx * xx).mean(axis=-1, keepdims=True) + 1e-6) * gg
+
+    _, irms = on.rmsnorm(x.astype(np.float32), g)
+    dx = on.rmsnormdx(dy, x, g, irms)
+    assert_close(dx, _fd_grad(lambda xx: float((rms64(xx) * dy).sum()), x.copy()),
+                 rtol=1e-3, atol=1e-4)
+    dg = on.rmsnormdg(dy, x, irms)
+    assert_close(dg, _fd_grad(lambda gg: float((rms64(x, gg) * dy).sum()), g.copy()),
+                 rtol=1e-3, atol=1e-4)
+
+
+def test_layernorm_inner_axis_equals_transposed_last_axis():
+    x = rng(11).standard_normal((2, 5, 3)).astype(np.float32)
+    g = rng(12).standard_normal(5)
+    b = rng(13).standard_normal(5)
+    y, mu, inv = on.meanvarnorm(x, g, b, axis=1)
+    yt, mut, invt = on.meanvarnorm(np.ascontiguousarray(x.transpose(0, 2, 1)), g, b, axis=-1)
+    assert_close(y, yt.transpose(0, 2, 1), atol=1e-6)
+    assert_close(mu, mut, atol=1e-6)
+
+
+def test_batchnorm_statistics_and_backward():
+    r = rng(14)
+    x = r.standard_normal((4, 3, 2, 2))
+    g = r.standard_normal(3)
+    b = r.standard_normal(3)
+    y, mu, inv, rm, rv = on.batchnorm(x, g, b, np.zeros(3), np.ones(3), training=True)
+    assert_close(mu, x.mean(axis=(0, 2, 3)), atol=1e-6)
+    assert_close(inv, 1 / np.sqrt(x.var(axis=(0, 2, 3)) + 1e-5), rtol=1e-5)
+    assert_close(rm, 0.1 * x.mean(axis=(0, 2, 3)), atol=1e-6)
+    assert_close(rv, 0.9 + 0.1 * x.var(axis=(0, 2, 3), ddof=1), atol=1e-6)
+    ye, *_ = on.batchnorm(x, g, b, rm, rv, training=False)
+    assert_close(ye, (x - rm.reshape(1, 3, 1, 1)) / np.sqrt(rv.reshape(1, 3, 1, 1) + 1e-5)
+                 * g.reshape(1, 3, 1, 1) + b.reshape(1, 3, 1, 1), atol=1e-5)
+    dy = r.standard_normal(x.shape)
+
+    def bn64(xx):
+        m = xx.mean(axis=(0, 2, 3), keepdims=True)
+        v = xx.var(axis=(0, 2, 3), keepdims=True)
+        return ((xx - m) / np.sqrt(v + 1e-5) * g.reshape(1, 3, 1, 1) + b.reshape(1, 3, 1, 1))
+
+    dg, db = on.batchnormdg(dy, x, mu, inv)
+    dx = on.batchnormdx(dy, x, g, dg, db, mu, inv)
+    assert_close(dx, _fd_grad(lambda xx: float((bn64(xx) * dy).sum()), x.copy()),
+                 rtol=1e-3, atol=1e-4)
+    assert_close(db, dy.sum(axis=(0, 2, 3)), atol=1e-5)
+
+
+# ---------------------------------------------------------------- GEMM
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+def test_gemm_closed_form_and_fma_chain(ta, tb):
+    r = rng(20)
+    M, N, K = 7, 5, 9
+    A = r.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    B = r.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    bias = r.standard_normal(N).astype(np.float32)
+    c = og.matmul_add(A, B, bias, ta, tb)
+    a = A.T if ta else A
+    b = B.T if tb else B
+    brute = np.array([[sum(float(a[i, k]) * float(b[k, j]) for k in range(K)) + bias[j]
+                       for j in range(N)] for i in range(M)])
+    assert_close(c, brute, atol=1e-5)
+    cf = og.matmul_add_fma(A, B, bias, ta, tb)
+    assert_close(cf, brute, rtol=1e-5, atol=1e-5)
+    # the C oracle is the fma chain in ascending k, then one bias add
+    for i in range(M):
+        for j in range(N):
+            acc = np.float32(0.0)
+            for k in range(K):
+                exact = np.float64(a[i, k]) * np.float64(b[k, j]) + np.float64(acc)
+                acc = np.float32(exact)
+            assert abs(float(cf[i, j]) - float(np.float32(acc + bias[j]))) <= 2 * np.spacing(
+                np.float32(abs(cf[i, j]) + 1e-30)
+            )
+
+
+def test_gemm_batch_and_bias_modes():
+    r = rng(21)
+    A = r.standard_normal((3, 4, 6)).astype(np.float32)
+    W = r.standard_normal((6, 5)).astype(np.float32)
+    for bias in (None, r.standard_normal(5), r.standard_normal((4, 5)),
+                 r.standard_normal((3, 4, 5))):
+        c = og.matmul_add(A, W, bias)
+        ref = np.einsum("bik,kj->bij", A.astype(np.float64), W.astype(np.float64))
+        if bias is not None:
+            ref = ref + bias
+        assert_close(c, ref, atol=1e-5)
+        assert_close(og.matmul_add_fma(A, W, None if bias is None else bias.astype(np.float32)),
+                     ref, atol=1e-4)
+    with pytest.raises(ValueError):
+        og.matmul_add(A, r.standard_normal((2, 6, 5)))
+    with pytest.raises(ValueError):
+        og.matmul_add(A, W, r.standard_normal((5, 4)))
+
+
+def test_gemm_fma_row_sample_is_rows_of_full():
+    r = rng(22)
+    A = r.standard_normal((64, 48)).astype(np.float32)
+    B = r.standard_normal((48, 40)).astype(np.float32)
+    full = og.matmul_add_fma(A, B)
+    part = og.matmul_add_fma(A, B, rows=(8, 24))
+    assert np.array_equal(part[8:24], full[8:24])
+    assert np.all(part[:8] == 0) and np.all(part[24:] == 0)
+
+
+# ---------------------------------------------------------------- elementwise
+
+
+def test_pow_rules_match_reference_test():
+    # reference tests/test_pointwise.py:33-68
+    arr = np.array([[-2.0, -0.5, 0.5, 2.0], [0.25, 1.5, 3.0, 4.0]], np.float32)
+    assert_close(oe.scalarpointwise(arr, 3, 3), arr ** 3, atol=1e-5)
+    assert_close(oe.scalarpointwise(arr, -1, 3), arr ** -1, atol=1e-5)
+    assert_close(oe.scalarpointwise(arr, 2, 4, reverse=1), 2.0 / arr, atol=1e-6)
+    assert_close(oe.scalarpointwise(arr, 2.5, 3, reverse=1), 2.5 ** arr, atol=1e-5)
+    neg = np.array([[-2.0, -3.0, 2.0, 3.0]], np.float32)
+    assert_close(oe.scalarpointwise(neg, 3, 3), np.array([[-8.0, -27.0, 8.0, 27.0]]))
+    frac = oe.scalarpointwise(neg, 0.5, 3)
+    assert np.isnan(frac[0, :2]).all()
+    assert_close(frac[0, 2:], np.sqrt(np.array([2.0, 3.0])))
+    assert_close(oe.scalarpointwise(neg, 2, 3), neg ** 2)
+
+
+def test_binary_broadcast_matches_reference_test():
+    # reference tests/test_pointwise.py:81-87 and :16-21
+    a = rng(2).standard_normal((3, 1)).astype(np.float32)
+    b = rng(3).standard_normal((1, 4)).astype(np.float32)
+    assert_close(oe.pointwise(a, b, 2), a * b)
+    x = rng(0).standard_normal((5, 7)).astype(np.float32)
+    y = rng(1).standard_normal((5, 7)).astype(np.float32)
+    for op, f in enumerate([np.add, np.subtract, np.multiply, np.divide]):
+        assert_close(oe.pointwise(x, y, op), f(x, y))
+
+
+def test_clamp_equal_fill():
+    x = np.array([-2.0, -0.5, 0.0, 0.5, 2.0], np.float32)
+    assert np.array_equal(oe.clamp(x, -1, 1), np.clip(x, -1, 1))
+    assert np.array_equal(oe.clampbackwards(x, -1, 1), np.array([0, 1, 1, 1, 0], np.float32))
+    assert np.array_equal(oe.masked_fill(x, -9.0), np.array([-2, -0.5, -9, 0.5, 2], np.float32))
+    assert np.array_equal(oe.equal(x, 0.5), (x == 0.5).astype(np.float32))
+    assert math.isclose(float(oe.mul_backward(x, x, 2 * x)[0][0]), 8.0)

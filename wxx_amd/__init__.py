@@ -1,0 +1,14 @@
+"""wxx_amd: the wxx tensor library on a native MI355X (gfx950) HIP backend.
+
+``import wxx_amd as wxx`` exposes the reference package's surface
+(reference src/wxx/__init__.py:1-17): ``Tensor``, ``Parameter``,
+``functional``, ``autograd``, ``nn``, ``backend``, ``serialization``,
+``save``/``load``.  Importing does not touch the GPU; the device opens on the
+first allocation.
+"""
+
+from .Tensor import Parameter, Tensor
+from . import backend, functional
+from .backend.device import get_device
+
+__all__ = ["Tensor", "Parameter", "functional", "backend", "get_device"]

@@ -1,0 +1,213 @@
+// BatchNorm over NCHW f32 tensors: per-channel statistics across (B, H, W),
+// running-statistic EMA, normalisation, and the backward pair.
+//
+// Reference semantics (src/wxx/shaders/layers/batchnorm.wgsl:30-111,
+// batchnormdx.wgsl:24-50, batchnormdg.wgsl:22-74; host
+// src/wxx/functional/normalization.py:148-305):
+//  * training: mu = S/M, var = max(0, Q/M - mu^2), inv = rsqrt(var + eps)
+//    (no zero-variance special case), running_mean = (1-m) rm + m mu,
+//    running_var = (1-m) rv + m var * M/(M-1) (var itself when M == 1);
+//  * eval: inv = rsqrt(running_var + eps), y uses the running mean;
+//  * dgamma = sum dy xhat, dbeta = sum dy;
+//    dx = (g inv / M) (M dy - dbeta - xhat dgamma).
+//
+// MI355X design: the reference gives each channel one 256-thread workgroup
+// (64-512 workgroups for ResNet18, a quarter of the chip).  Here the
+// per-channel sums run as a (channel, split) grid of partial reductions,
+// a per-channel finalize adds the partials in split order (deterministic),
+// and the normalisation is a separate fully parallel elementwise pass.
+#include "common.h"
+
+namespace {
+
+constexpr int kBlock = 256;
+
+// part[(c * splits + s) * 2 + {0,1}] = sums over this split of (a, b), where
+// (a, b) = (x, x^2) for statistics or (dy * xhat, dy) for the gradient.
+template <bool GRAD>
+__global__ __launch_bounds__(kBlock) void bn_partial_kernel(
+    const float* __restrict__ x, const float* __restrict__ dy, const float* __restrict__ mean,
+    const float* __restrict__ inv, float* __restrict__ part, int64_t B, int64_t Cc, int64_t HW,
+    int splits) {
+  __shared__ float red[4];
+  const int64_t c = blockIdx.x;
+  const int s = blockIdx.y;
+  const int64_t M = B * HW;
+  const int64_t seg = (M + splits - 1) / splits;
+  const int64_t m0 = s * seg;
+  const int64_t m1 = m0 + seg < M ? m0 + seg : M;
+  float mu = 0.f, is = 0.f;
+  if (GRAD) {
+    mu = mean[c];
+    is = inv[c];
+  }
+  float a = 0.f, b = 0.f;
+  for (int64_t m = m0 + threadIdx.x; m < m1; m += kBlock) {
+    const int64_t bb = m / HW, sp = m - bb * HW;
+    const int64_t idx = (bb * Cc + c) * HW + sp;
+    const float v = x[idx];
+    if (GRAD) {
+      const float d = dy[idx];
+      a += d * (v - mu) * is;
+      b += d;
+    } else {
+      a += v;
+      b += v * v;
+    }
+  }
+  a = wxx::block_sum(a, red);
+  b = wxx::block_sum(b, red);
+  if (threadIdx.x == 0) {
+    part[(c * splits + s) * 2 + 0] = a;
+    part[(c * splits + s) * 2 + 1] = b;
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void bn_finalize_kernel(
+    const float* __restrict__ part, float* __restrict__ running_mean,
+    float* __restrict__ running_var, float* __restrict__ saved_mean, float* __restrict__ inv_std,
+    int64_t Cc, int64_t M, int splits, float eps, float momentum, int training) {
+  const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (c >= Cc) return;
+  if (!training) {
+    saved_mean[c] = running_mean[c];
+    inv_std[c] = rsqrtf(running_var[c] + eps);
+    return;
+  }
+  float S = 0.f, Q = 0.f;
+  for (int s = 0; s < splits; ++s) {
+    S += part[(c * splits + s) * 2 + 0];
+    Q += part[(c * splits + s) * 2 + 1];
+  }
+  const float mf = (float)M;
+  const float mu = S / mf;
+  const float var = fmaxf(0.f, Q / mf - mu * mu);
+  saved_mean[c] = mu;
+  inv_std[c] = rsqrtf(var + eps);
+  running_mean[c] = (1.f - momentum) * running_mean[c] + momentum * mu;
+  const float unbiased = M > 1 ? var * (mf / (mf - 1.f)) : var;
+  running_var[c] = (1.f - momentum) * running_var[c] + momentum * unbiased;
+}
+
+__global__ __launch_bounds__(kBlock) void bn_grad_finalize_kernel(const float* __restrict__ part,
+                                                                  float* __restrict__ dg,
+                                                                  float* __restrict__ db,
+                                                                  int64_t Cc, int splits) {
+  const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (c >= Cc) return;
+  float a = 0.f, b = 0.f;
+  for (int s = 0; s < splits; ++s) {
+    a += part[(c * splits + s) * 2 + 0];
+    b += part[(c * splits + s) * 2 + 1];
+  }
+  dg[c] = a;
+  db[c] = b;
+}
+
+__global__ __launch_bounds__(kBlock) void bn_apply_kernel(
+    const float* __restrict__ x, const float* __restrict__ g, const float* __restrict__ b,
+    const float* __restrict__ mean, const float* __restrict__ inv, float* __restrict__ y,
+    int64_t n, int64_t Cc, int64_t HW) {
+  int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t step = (int64_t)gridDim.x * kBlock;
+  for (; i < n; i += step) {
+    const int64_t c = (i / HW) % Cc;
+    y[i] = (x[i] - mean[c]) * inv[c] * g[c] + b[c];
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void bn_dx_kernel(
+    const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ g,
+    const float* __restrict__ dg, const float* __restrict__ db, const float* __restrict__ mean,
+    const float* __restrict__ inv, float* __restrict__ dx, int64_t n, int64_t Cc, int64_t HW,
+    float mf) {
+  int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t step = (int64_t)gridDim.x * kBlock;
+  for (; i < n; i += step) {
+    const int64_t c = (i / HW) % Cc;
+    const float is = inv[c];
+    const float xh = (x[i] - mean[c]) * is;
+    dx[i] = (g[c] * is / mf) * (mf * dy[i] - db[c] - xh * dg[c]);
+  }
+}
+
+int pick_splits(int64_t Cc, int64_t M) {
+  const int64_t target = (int64_t)wxx::num_cus() * 8;
+  int64_t s = (target + Cc - 1) / Cc;
+  s = std::min<int64_t>(s, std::max<int64_t>(1, M / 1024));
+  return (int)std::max<int64_t>(1, std::min<int64_t>(s, 1024));
+}
+
+}  // namespace
+
+// Replaces functional.batchnorm (reference src/wxx/functional/normalization.py:148-206).
+WXX_API int wxx_batchnorm(const float* x, const float* gamma, const float* beta,
+                          float* running_mean, float* running_var, float* y, float* saved_mean,
+                          float* inv_std, int64_t B, int64_t C, int64_t HW, float eps,
+                          float momentum, int training) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(x && gamma && beta && running_mean && running_var && y && saved_mean && inv_std,
+              "null pointer");
+  WXX_REQUIRE(B >= 0 && C >= 1 && HW >= 0, "bad batchnorm dims");
+  hipStream_t s = wxx::stream();
+  const int64_t M = B * HW;
+  int splits = 1;
+  float* part = nullptr;
+  if (training) {
+    splits = pick_splits(C, M);
+    part = (float*)wxx::scratch_alloc(sizeof(float) * 2 * C * splits);
+    if (!part) return wxx::set_error(WXX_E_OOM, "batchnorm partials");
+    hipLaunchKernelGGL(bn_partial_kernel<false>, dim3((unsigned)C, splits), dim3(kBlock), 0, s, x,
+                       nullptr, nullptr, nullptr, part, B, C, HW, splits);
+    WXX_LAUNCHED();
+  }
+  hipLaunchKernelGGL(bn_finalize_kernel, dim3(wxx::grid_1d(C, kBlock)), dim3(kBlock), 0, s, part,
+                     running_mean, running_var, saved_mean, inv_std, C, M, splits, eps, momentum,
+                     training);
+  WXX_LAUNCHED();
+  if (part) wxx::scratch_free(part);
+  const int64_t n = M * C;
+  if (n > 0) {
+    hipLaunchKernelGGL(bn_apply_kernel, dim3(wxx::grid_1d(n, kBlock, 16384)), dim3(kBlock), 0, s,
+                       x, gamma, beta, saved_mean, inv_std, y, n, C, HW);
+    WXX_LAUNCHED();
+  }
+  return WXX_OK;
+}
+
+// Replaces functional.batchnormdg (reference normalization.py:260-305).
+WXX_API int wxx_batchnormdg(const float* dy, const float* x, const float* saved_mean,
+                            const float* inv_std, float* dgamma, float* dbeta, int64_t B,
+                            int64_t C, int64_t HW) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(dy && x && saved_mean && inv_std && dgamma && dbeta, "null pointer");
+  WXX_REQUIRE(B >= 0 && C >= 1 && HW >= 0, "bad batchnorm dims");
+  hipStream_t s = wxx::stream();
+  const int64_t M = B * HW;
+  const int splits = pick_splits(C, M);
+  float* part = (float*)wxx::scratch_alloc(sizeof(float) * 2 * C * splits);
+  if (!part) return wxx::set_error(WXX_E_OOM, "batchnorm partials");
+  hipLaunchKernelGGL(bn_partial_kernel<true>, dim3((unsigned)C, splits), dim3(kBlock), 0, s, x, dy,
+                     saved_mean, inv_std, part, B, C, HW, splits);
+  WXX_LAUNCHED();
+  hipLaunchKernelGGL(bn_grad_finalize_kernel, dim3(wxx::grid_1d(C, kBlock)), dim3(kBlock), 0, s,
+                     part, dgamma, dbeta, C, splits);
+  WXX_LAUNCHED();
+  wxx::scratch_free(part);
+  return WXX_OK;
+}
+
+// Replaces functional.batchnormdx (reference normalization.py:209-257).
+WXX_API int wxx_batchnormdx(const float* dy, const float* x, const float* gamma,
+                            const float* dgamma, const float* dbeta, const float* saved_mean,
+                            const float* inv_std, float* dx, int64_t B, int64_t C, int64_t HW) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(dy && x && gamma && dgamma && dbeta && saved_mean && inv_std && dx, "null pointer");
+  const int64_t n = B * C * HW;
+  if (n <= 0) return WXX_OK;
+  hipLaunchKernelGGL(bn_dx_kernel, dim3(wxx::grid_1d(n, kBlock, 16384)), dim3(kBlock), 0,
+                     wxx::stream(), dy, x, gamma, dgamma, dbeta, saved_mean, inv_std, dx, n, C,
+                     HW, (float)(B * HW));
+  WXX_LAUNCHED();
+  return WXX_OK;
+}

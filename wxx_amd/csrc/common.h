@@ -1,0 +1,130 @@
+// Shared definitions for the gfx950 kernels of libwxx_hip.so.
+//
+// Every extern "C" entry point returns 0 on success or a negative WXX_E_*
+// code; the message of the last failure is kept per host thread and read
+// back with wxx_last_error().  All work is enqueued on the one in-order
+// stream owned by the runtime (runtime.hip), which gives the same ordering
+// guarantees as the reference's single shared compute pass.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <cstddef>
+#include <cstdio>
+#include <cstdarg>
+#include <algorithm>
+
+#define WXX_API extern "C" __attribute__((visibility("default")))
+
+WXX_API int wxx_fill_u32(void* dst, int64_t n, uint32_t bits);
+
+enum {
+  WXX_OK = 0,
+  WXX_E_HIP = -1,        // a HIP runtime call failed
+  WXX_E_ARG = -2,        // invalid argument (null pointer, bad enum, bad size)
+  WXX_E_OOM = -3,        // device allocation failed
+  WXX_E_INIT = -4,       // runtime not initialised / no device
+  WXX_E_RANGE = -5,      // index data out of range (e.g. CCE target >= K)
+  WXX_E_UNSUPPORTED = -6 // shape/layout outside what a kernel supports
+};
+
+namespace wxx {
+
+// Runtime state (runtime.hip).
+hipStream_t stream();
+bool initialised();
+int set_error(int code, const char* fmt, ...);
+void* scratch_alloc(size_t bytes);   // stream-ordered temporary from the cache
+void scratch_free(void* p);
+int num_cus();
+
+constexpr int kMaxRank = 6;
+
+struct Shape6 {
+  int64_t d[kMaxRank];
+};
+
+}  // namespace wxx
+
+#define WXX_CHECK_INIT()                                                   \
+  do {                                                                     \
+    if (!wxx::initialised())                                               \
+      return wxx::set_error(WXX_E_INIT, "wxx_init() has not been called"); \
+  } while (0)
+
+#define WXX_HIP(call)                                                      \
+  do {                                                                     \
+    hipError_t e_ = (call);                                                \
+    if (e_ != hipSuccess)                                                  \
+      return wxx::set_error(WXX_E_HIP, "%s failed: %s", #call,             \
+                            hipGetErrorString(e_));                        \
+  } while (0)
+
+#define WXX_REQUIRE(cond, ...)                                             \
+  do {                                                                     \
+    if (!(cond)) return wxx::set_error(WXX_E_ARG, __VA_ARGS__);            \
+  } while (0)
+
+// Check the launch that was just enqueued.
+#define WXX_LAUNCHED()                                                     \
+  do {                                                                     \
+    hipError_t e_ = hipGetLastError();                                     \
+    if (e_ != hipSuccess)                                                  \
+      return wxx::set_error(WXX_E_HIP, "kernel launch failed: %s",         \
+                            hipGetErrorString(e_));                        \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// Device helpers
+// ---------------------------------------------------------------------------
+namespace wxx {
+
+__device__ __forceinline__ float warp_sum(float v) {
+  // 64-wide wavefront butterfly; __shfl_xor lowers to ds_swizzle/DPP moves.
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float warp_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Block-wide sum of one value per thread; every thread gets the result.
+// `red` must hold at least blockDim.x / 64 floats.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  v = warp_sum(v);
+  __syncthreads();  // protect `red` from a previous use
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < nw; ++i) t += red[i];
+  return t;
+}
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  v = warp_max(v);
+  __syncthreads();
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  float t = red[0];
+  for (int i = 1; i < nw; ++i) t = fmaxf(t, red[i]);
+  return t;
+}
+
+inline unsigned int grid_1d(int64_t n, int block, int64_t cap = 1 << 20) {
+  int64_t g = (n + block - 1) / block;
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return (unsigned int)g;
+}
+
+}  // namespace wxx

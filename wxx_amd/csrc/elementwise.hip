@@ -1,0 +1,655 @@
+// Elementwise and layout kernels: broadcast binary ops (out-of-place and in
+// place), scalar ops, unary math / activation (+ local derivative) ops,
+// clamp, equality, masked fill, the fused mul backward, strided gather
+// ("contiguous"), strided assign / fill, scatter_zeros and unfold backward.
+//
+// Reference kernels and hosts:
+//   pointwise/pointwise.wgsl:19-61, pointwise/_pointwise.wgsl:17-60,
+//   pointwise/scalarpointwise.wgsl:17-72, pointwise/{abs,exp,log,negate,
+//   rsqrt,sign,sqrt,square}.wgsl, activations/{relu,gelu,sigmoid,selu,sin,
+//   cos}*.wgsl, helpers/{clamp,clampbackwards,equal,maskedfill,mul_backward,
+//   contiguous,assign,scatter_zeros,unfolddx}.wgsl; hosts in
+//   src/wxx/functional/pointwise.py, activations.py and utils.py.
+//
+// MI355X design: the reference decomposes every linear index with a div/mod
+// per dimension.  Here the host first coalesces dimensions that are
+// contiguous in every operand and drops size-1 dimensions, so the common
+// cases (same-shape contiguous tensors, row/column broadcast, a permuted
+// view) run as rank-1/2/3 loops; rank-1 unit-stride operands use float4
+// accesses.  Index arithmetic is 32-bit whenever the tensor has fewer than
+// 2^31 elements.
+#include "common.h"
+
+#include <cmath>
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kMaxOps = 3;
+
+struct ND {
+  int rank;
+  int64_t shape[wxx::kMaxRank];
+  int64_t stride[kMaxOps][wxx::kMaxRank];
+};
+
+// Merge dimensions that are contiguous in every operand, drop size-1 dims.
+ND collapse(int rank, const int64_t* shape, const int64_t* const* strides, int nops) {
+  ND r;
+  r.rank = 0;
+  for (int d = 0; d < rank; ++d) {
+    if (shape[d] == 1) continue;
+    if (r.rank > 0) {
+      const int p = r.rank - 1;
+      bool merge = true;
+      for (int o = 0; o < nops; ++o)
+        if (r.stride[o][p] != strides[o][d] * shape[d]) merge = false;
+      if (merge) {
+        r.shape[p] *= shape[d];
+        for (int o = 0; o < nops; ++o) r.stride[o][p] = strides[o][d];
+        continue;
+      }
+    }
+    r.shape[r.rank] = shape[d];
+    for (int o = 0; o < nops; ++o) r.stride[o][r.rank] = strides[o][d];
+    ++r.rank;
+  }
+  if (r.rank == 0) {
+    r.rank = 1;
+    r.shape[0] = 1;
+    for (int o = 0; o < nops; ++o) r.stride[o][0] = 0;
+  }
+  return r;
+}
+
+template <int NOPS>
+__device__ __forceinline__ void offsets(const ND& nd, int64_t idx, int64_t* off) {
+#pragma unroll
+  for (int o = 0; o < NOPS; ++o) off[o] = 0;
+  if (nd.rank == 1) {
+#pragma unroll
+    for (int o = 0; o < NOPS; ++o) off[o] = idx * nd.stride[o][0];
+    return;
+  }
+  // 32-bit decomposition when possible (AMD has no hardware 64-bit divide).
+  uint32_t rem = (uint32_t)idx;
+  for (int d = nd.rank - 1; d >= 0; --d) {
+    const uint32_t n = (uint32_t)nd.shape[d];
+    const uint32_t q = rem / n;
+    const uint32_t c = rem - q * n;
+    rem = q;
+#pragma unroll
+    for (int o = 0; o < NOPS; ++o) off[o] += (int64_t)c * nd.stride[o][d];
+  }
+}
+
+template <int NOPS>
+__device__ __forceinline__ void offsets64(const ND& nd, int64_t idx, int64_t* off) {
+#pragma unroll
+  for (int o = 0; o < NOPS; ++o) off[o] = 0;
+  for (int d = nd.rank - 1; d >= 0; --d) {
+    const int64_t n = nd.shape[d];
+    const int64_t q = idx / n;
+    const int64_t c = idx - q * n;
+    idx = q;
+#pragma unroll
+    for (int o = 0; o < NOPS; ++o) off[o] += c * nd.stride[o][d];
+  }
+}
+
+// ---- binary ----------------------------------------------------------------
+__device__ __forceinline__ float binop(int op, float a, float b) {
+  switch (op) {
+    case 1: return a - b;
+    case 2: return a * b;
+    case 3: return a / b;
+    default: return a + b;
+  }
+}
+
+// operands: 0 = out, 1 = a, 2 = b
+template <bool BIG>
+__global__ __launch_bounds__(kBlock) void binary_kernel(float* __restrict__ out,
+                                                        const float* __restrict__ a,
+                                                        const float* __restrict__ b, ND nd,
+                                                        int64_t n, int op) {
+  int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t step = (int64_t)gridDim.x * kBlock;
+  for (; i < n; i += step) {
+    int64_t off[3];
+    if (BIG)
+      offsets64<3>(nd, i, off);
+    else
+      offsets<3>(nd, i, off);
+    out[off[0]] = binop(op, a[off[1]], b[off[2]]);
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void binary_flat4_kernel(float4* __restrict__ out,
+                                                              const float4* __restrict__ a,
+                                                              const float4* __restrict__ b,
+                                                              int64_t n4, int op) {
+  int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t step = (int64_t)gridDim.x * kBlock;
+  for (; i < n4; i += step) {
+    float4 x = a[i], y = b[i];
+    out[i] = make_float4(binop(op, x.x, y.x), binop(op, x.y, y.y), binop(op, x.z, y.z),
+                         binop(op, x.w, y.w));
+  }
+}
+
+// ---- scalar / unary ----------------------------------------------------------
+__device__ __forceinline__ float scalar_op(int op, float x, float c, int rev) {
+  switch (op) {
+    case 0: return x + c;
+    case 1: return rev ? c - x : x - c;
+    case 2: return x * c;
+    case 3: {
+      if (rev) return powf(c, x);
+      if (x < 0.f) {
+        if (c == truncf(c)) {
+          const float mag = powf(-x, c);
+          const bool odd = fmodf(fabsf(c) * 0.5f, 1.0f) > 0.25f;
+          return odd ? -mag : mag;
+        }
+        return __int_as_float(0x7fc00000);
+      }
+      return powf(x, c);
+    }
+    case 4: return rev ? c / x : x / c;
+    default: return x;
+  }
+}
+
+enum Unary {
+  U_RELU = 0, U_RELU_BWD, U_GELU, U_GELU_BWD, U_SIGMOID, U_SIGMOID_BWD, U_SELU, U_SELU_BWD,
+  U_SIN, U_SIN_BWD, U_COS, U_COS_BWD, U_ABS, U_EXP, U_LOG, U_NEG, U_RSQRT, U_SIGN, U_SQRT,
+  U_SQUARE, U_COUNT
+};
+
+constexpr float kSqrt2OverPi = 0.7978845608f;
+constexpr float kGeluC = 0.044715f;
+constexpr float kGeluDC = 0.134145f;
+constexpr float kSeluAlpha = 1.6732632423543772848170429916717f;
+constexpr float kSeluScale = 1.0507009873554804934193349852946f;
+
+__device__ __forceinline__ float unary_op(int op, float x) {
+  switch (op) {
+    case U_RELU: return fmaxf(0.f, x);
+    case U_RELU_BWD: return x > 0.f ? 1.f : 0.f;
+    case U_GELU: {
+      if (x > 10.f) return x;
+      if (x < -10.f) return 0.f;
+      const float u = kSqrt2OverPi * (x + kGeluC * x * x * x);
+      return 0.5f * x * (1.f + tanhf(u));
+    }
+    case U_GELU_BWD: {
+      if (x > 10.f) return 1.f;
+      if (x < -10.f) return 0.f;
+      const float u = kSqrt2OverPi * (x + kGeluC * x * x * x);
+      const float t = tanhf(u);
+      const float du = kSqrt2OverPi * (1.f + kGeluDC * x * x);
+      return 0.5f * (1.f + t) + 0.5f * x * (1.f - t * t) * du;
+    }
+    case U_SIGMOID: {
+      const float xc = fminf(fmaxf(x, -88.f), 88.f);
+      return 1.f / (1.f + expf(-xc));
+    }
+    case U_SIGMOID_BWD: return x * (1.f - x);
+    case U_SELU: return x > 0.f ? kSeluScale * x : kSeluScale * kSeluAlpha * (expf(x) - 1.f);
+    case U_SELU_BWD: return x > 0.f ? kSeluScale : kSeluScale * kSeluAlpha * expf(x);
+    case U_SIN: return sinf(x);
+    case U_SIN_BWD: return cosf(x);
+    case U_COS: return cosf(x);
+    case U_COS_BWD: return -sinf(x);
+    case U_ABS: return fabsf(x);
+    case U_EXP: return expf(x);
+    case U_LOG: return logf(x);
+    case U_NEG: return -x;
+    case U_RSQRT: return rsqrtf(x);
+    case U_SIGN: return x > 0.f ? 1.f : (x < 0.f ? -1.f : 0.f);
+    case U_SQRT: return sqrtf(x);
+    case U_SQUARE: return x * x;
+    default: return x;
+  }
+}
+
+template <int OP>
+__global__ __launch_bounds__(kBlock) void unary_kernel(const float* __restrict__ x,
+                                                       float* __restrict__ y, int64_t n,
+                                                       int vec) {
+  const int64_t n4 = vec ? n >> 2 : 0;
+  const int64_t step = (int64_t)gridDim.x * kBlock;
+  const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  float4* y4 = reinterpret_cast<float4*>(y);
+  for (int64_t i = t; i < n4; i += step) {
+    float4 v = x4[i];
+    y4[i] = make_float4(unary_op(OP, v.x), unary_op(OP, v.y), unary_op(OP, v.z),
+                        unary_op(OP, v.w));
+  }
+  for (int64_t i = (n4 << 2) + t; i < n; i += step) y[i] = unary_op(OP, x[i]);
+}
+
+__global__ __launch_bounds__(kBlock) void scalar_kernel(const float* __restrict__ x,
+                                                        float* __restrict__ y, int64_t n, int op,
+                                                        float c, int rev, int vec) {
+  const int64_t n4 = vec ? n >> 2 : 0;
+  const int64_t step = (int64_t)gridDim.x * kBlock;
+  const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  float4* y4 = reinterpret_cast<float4*>(y);
+  for (int64_t i = t; i < n4; i += step) {
+    float4 v = x4[i];
+    y4[i] = make_float4(scalar_op(op, v.x, c, rev), scalar_op(op, v.y, c, rev),
+                        scalar_op(op, v.z, c, rev), scalar_op(op, v.w, c, rev));
+  }
+  for (int64_t i = (n4 << 2) + t; i < n; i += step) y[i] = scalar_op(op, x[i], c, rev);
+}
+
+// mode 0: clamp; 1: clamp backward mask; 2: masked fill (x != 0 ? x : lo)
+__global__ __launch_bounds__(kBlock) void clamp_kernel(const float* __restrict__ x,
+                                                       float* __restrict__ y, int64_t n, float lo,
+                                                       float hi, int mode) {
+  int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t step = (int64_t)gridDim.x * kBlock;
+  for (; i < n; i += step) {
+    const float v = x[i];
+    float r;
+    if (mode == 0)
+      r = fminf(fmaxf(v, lo), hi);
+    else if (mode == 1)
+      r = (v >= lo && v <= hi) ? 1.f : 0.f;
+    else
+      r = v != 0.f ? v : lo;
+    y[i] = r;
+  }
+}
+
+// mode 0: f32 == f32, 1: u32 == u32, 2: f32 == scalar bits, 3: u32 == scalar
+__global__ __launch_bounds__(kBlock) void equal_kernel(const uint32_t* __restrict__ a,
+                                                       const uint32_t* __restrict__ b,
+                                                       float* __restrict__ out, int64_t n,
+                                                       int mode, uint32_t number) {
+  int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t step = (int64_t)gridDim.x * kBlock;
+  for (; i < n; i += step) {
+    const uint32_t x = a[i];
+    bool eq;
+    switch (mode) {
+      case 0: eq = __uint_as_float(x) == __uint_as_float(b[i]); break;
+      case 1: eq = x == b[i]; break;
+      case 2: eq = __uint_as_float(x) == __uint_as_float(number); break;
+      default: eq = x == number; break;
+    }
+    out[i] = eq ? 1.f : 0.f;
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void mul_backward_kernel(const float* __restrict__ g,
+                                                              const float* __restrict__ a,
+                                                              const float* __restrict__ b,
+                                                              float* __restrict__ da,
+                                                              float* __restrict__ db, int64_t n) {
+  int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t step = (int64_t)gridDim.x * kBlock;
+  for (; i < n; i += step) {
+    const float gv = g[i];
+    da[i] = gv * b[i];
+    db[i] = gv * a[i];
+  }
+}
+
+// ---- layout -------------------------------------------------------------------
+// dst (operand 0) and src (operand 1) both strided; element type T.
+template <typename T, bool BIG>
+__global__ __launch_bounds__(kBlock) void copy_strided_kernel(T* __restrict__ dst,
+                                                              const T* __restrict__ src, ND nd,
+                                                              int64_t n) {
+  int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t step = (int64_t)gridDim.x * kBlock;
+  for (; i < n; i += step) {
+    int64_t off[2];
+    if (BIG)
+      offsets64<2>(nd, i, off);
+    else
+      offsets<2>(nd, i, off);
+    dst[off[0]] = src[off[1]];
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void fill_strided_kernel(T* __restrict__ dst, ND nd,
+                                                              int64_t n, T v) {
+  int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t step = (int64_t)gridDim.x * kBlock;
+  for (; i < n; i += step) {
+    int64_t off[1];
+    offsets64<1>(nd, i, off);
+    dst[off[0]] = v;
+  }
+}
+
+// Tiled transpose of the two innermost collapsed dims (gather case where the
+// source's innermost stride is not 1): read 64x64 tiles coalesced, write
+// coalesced through LDS.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void transpose_tile_kernel(T* __restrict__ dst,
+                                                                const T* __restrict__ src,
+                                                                int64_t batch, int64_t rows,
+                                                                int64_t cols, int64_t sb,
+                                                                int64_t sr, int64_t sc) {
+  // dst[b][r][c] = src[b*sb + r*sr + c*sc], with sr == 1 expected (fast read
+  // along r).  Tile: 64 (r) x 64 (c).
+  __shared__ T tile[64][65];
+  const int64_t b = blockIdx.z;
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // 64 x 4
+  for (int k = ty; k < 64; k += 4) {
+    const int64_t c = c0 + k, r = r0 + tx;
+    if (c < cols && r < rows) tile[k][tx] = src[b * sb + r * sr + c * sc];
+  }
+  __syncthreads();
+  for (int k = ty; k < 64; k += 4) {
+    const int64_t r = r0 + k, c = c0 + tx;
+    if (r < rows && c < cols) dst[(b * rows + r) * cols + c] = tile[tx][k];
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void scatter_zeros_kernel(float* __restrict__ out,
+                                                               const float* __restrict__ grad,
+                                                               ND nd, int64_t n, int dim,
+                                                               int64_t start, int64_t length) {
+  // nd.shape = output shape (uncollapsed), nd.stride[0] = grad strides.
+  int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t step = (int64_t)gridDim.x * kBlock;
+  for (; i < n; i += step) {
+    int64_t rem = i, off = 0;
+    bool in = true;
+    for (int d = nd.rank - 1; d >= 0; --d) {
+      const int64_t sz = nd.shape[d];
+      const int64_t q = rem / sz;
+      int64_t c = rem - q * sz;
+      rem = q;
+      if (d == dim) {
+        if (c < start || c >= start + length) {
+          in = false;
+        } else {
+          c -= start;
+        }
+      }
+      off += c * nd.stride[0][d];
+    }
+    float v = 0.f;
+    if (in) v = grad[off];
+    out[i] = v;
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void unfolddx_kernel(const float* __restrict__ dy,
+                                                          float* __restrict__ dx, int64_t prefix,
+                                                          int64_t length, int64_t suffix,
+                                                          int64_t windows, int64_t size,
+                                                          int64_t stepw) {
+  const int64_t total = prefix * length * suffix;
+  int64_t idx = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t gstep = (int64_t)gridDim.x * kBlock;
+  for (; idx < total; idx += gstep) {
+    const int64_t s = idx % suffix;
+    const int64_t nn = (idx / suffix) % length;
+    const int64_t p = idx / (suffix * length);
+    float acc = 0.f;
+    for (int64_t w = 0; w < size; ++w) {
+      if (nn >= w) {
+        const int64_t pos = nn - w;
+        if (pos % stepw == 0) {
+          const int64_t l = pos / stepw;
+          if (l < windows) acc += dy[((p * windows + l) * suffix + s) * size + w];
+        }
+      }
+    }
+    dx[idx] = acc;
+  }
+}
+
+inline unsigned grid_for(int64_t n) { return wxx::grid_1d(n, kBlock, 16384); }
+
+bool fits32(const ND& nd, int64_t n) {
+  if (n >= (int64_t(1) << 31)) return false;
+  for (int d = 0; d < nd.rank; ++d)
+    if (nd.shape[d] >= (int64_t(1) << 31)) return false;
+  return true;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+
+// out = a op b with broadcasting; a/b/out strides in elements over the
+// output shape (0 for broadcast dims).  op: 0 add, 1 sub, 2 mul, 3 div.
+// Replaces functional.pointwise (reference src/wxx/functional/pointwise.py:29-98)
+// and, with out == a, functional._pointwise (pointwise.py:231-289).
+WXX_API int wxx_pointwise(float* out, const float* a, const float* b, int rank,
+                          const int64_t* shape, const int64_t* s_out, const int64_t* s_a,
+                          const int64_t* s_b, int op) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(out && a && b && shape && s_out && s_a && s_b, "null pointer");
+  WXX_REQUIRE(rank >= 0 && rank <= wxx::kMaxRank, "rank %d unsupported", rank);
+  int64_t n = 1;
+  for (int d = 0; d < rank; ++d) n *= shape[d];
+  if (n == 0) return WXX_OK;
+  const int64_t* ss[3] = {s_out, s_a, s_b};
+  ND nd = collapse(rank, shape, ss, 3);
+  hipStream_t s = wxx::stream();
+  if (nd.rank == 1 && nd.stride[0][0] == 1 && nd.stride[1][0] == 1 && nd.stride[2][0] == 1 &&
+      n % 4 == 0 && ((uintptr_t)out | (uintptr_t)a | (uintptr_t)b) % 16 == 0) {
+    hipLaunchKernelGGL(binary_flat4_kernel, dim3(grid_for(n / 4)), dim3(kBlock), 0, s,
+                       (float4*)out, (const float4*)a, (const float4*)b, n / 4, op);
+  } else if (fits32(nd, n)) {
+    hipLaunchKernelGGL(binary_kernel<false>, dim3(grid_for(n)), dim3(kBlock), 0, s, out, a, b,
+                       nd, n, op);
+  } else {
+    hipLaunchKernelGGL(binary_kernel<true>, dim3(grid_for(n)), dim3(kBlock), 0, s, out, a, b, nd,
+                       n, op);
+  }
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// y = x op c (or c op x when reverse); op: 0 add, 1 sub, 2 mul, 3 pow, 4 div.
+// Replaces functional.scalarpointwise (reference pointwise.py:101-146).
+WXX_API int wxx_scalarpointwise(const float* x, float* y, int64_t n, int op, float c,
+                                int reverse) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(x && y, "null pointer");
+  WXX_REQUIRE(op >= 0 && op <= 4, "bad scalar op %d", op);
+  if (n <= 0) return WXX_OK;
+  const int vec = ((uintptr_t)x | (uintptr_t)y) % 16 == 0;
+  hipLaunchKernelGGL(scalar_kernel, dim3(grid_for((n + 3) / 4)), dim3(kBlock), 0, wxx::stream(),
+                     x, y, n, op, c, reverse, vec);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// Unary op on a contiguous tensor; op numbering in the Unary enum above
+// (relu, relu', gelu, gelu', sigmoid, sigmoid'(from y), selu, selu', sin,
+// sin', cos, cos', abs, exp, log, neg, rsqrt, sign, sqrt, square).
+// Replaces the _unary_op family (reference src/wxx/backend/dispatch.py:59-89,
+// functional/activations.py:22-124, functional/pointwise.py:293-354).
+WXX_API int wxx_unary(const float* x, float* y, int64_t n, int op) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(x && y, "null pointer");
+  WXX_REQUIRE(op >= 0 && op < U_COUNT, "bad unary op %d", op);
+  if (n <= 0) return WXX_OK;
+  const int vec = ((uintptr_t)x | (uintptr_t)y) % 16 == 0;
+  dim3 grid(grid_for((n + 3) / 4));
+  hipStream_t s = wxx::stream();
+#define WXX_UCASE(OP) \
+  case OP: hipLaunchKernelGGL(unary_kernel<OP>, grid, dim3(kBlock), 0, s, x, y, n, vec); break;
+  switch (op) {
+    WXX_UCASE(U_RELU) WXX_UCASE(U_RELU_BWD) WXX_UCASE(U_GELU) WXX_UCASE(U_GELU_BWD)
+    WXX_UCASE(U_SIGMOID) WXX_UCASE(U_SIGMOID_BWD) WXX_UCASE(U_SELU) WXX_UCASE(U_SELU_BWD)
+    WXX_UCASE(U_SIN) WXX_UCASE(U_SIN_BWD) WXX_UCASE(U_COS) WXX_UCASE(U_COS_BWD)
+    WXX_UCASE(U_ABS) WXX_UCASE(U_EXP) WXX_UCASE(U_LOG) WXX_UCASE(U_NEG) WXX_UCASE(U_RSQRT)
+    WXX_UCASE(U_SIGN) WXX_UCASE(U_SQRT) WXX_UCASE(U_SQUARE)
+    default: break;
+  }
+#undef WXX_UCASE
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// mode 0: clamp (reference helpers/clamp.wgsl); 1: clamp backward mask
+// (clampbackwards.wgsl); 2: masked fill with `lo` (maskedfill.wgsl).
+WXX_API int wxx_clamp(const float* x, float* y, int64_t n, float lo, float hi, int mode) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(x && y, "null pointer");
+  WXX_REQUIRE(mode >= 0 && mode <= 2, "bad clamp mode %d", mode);
+  if (n <= 0) return WXX_OK;
+  hipLaunchKernelGGL(clamp_kernel, dim3(grid_for(n)), dim3(kBlock), 0, wxx::stream(), x, y, n,
+                     lo, hi, mode);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// Replaces functional.equal / equal_number (reference functional/utils.py:502-556).
+WXX_API int wxx_equal(const void* a, const void* b, float* out, int64_t n, int mode,
+                      uint32_t number) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(a && out && (mode >= 2 || b), "null pointer");
+  WXX_REQUIRE(mode >= 0 && mode <= 3, "bad equal mode %d", mode);
+  if (n <= 0) return WXX_OK;
+  hipLaunchKernelGGL(equal_kernel, dim3(grid_for(n)), dim3(kBlock), 0, wxx::stream(),
+                     (const uint32_t*)a, (const uint32_t*)(b ? b : a), out, n, mode, number);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// Replaces functional.mul_backward (reference pointwise.py:460-502).
+WXX_API int wxx_mul_backward(const float* g, const float* a, const float* b, float* da,
+                             float* db, int64_t n) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(g && a && b && da && db, "null pointer");
+  if (n <= 0) return WXX_OK;
+  hipLaunchKernelGGL(mul_backward_kernel, dim3(grid_for(n)), dim3(kBlock), 0, wxx::stream(), g,
+                     a, b, da, db, n);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// dst (strided view) <- src (strided view), element size 4 or 8 bytes.
+// With s_dst row-major this is functional.contiguous (reference
+// functional/utils.py:316-369, fft.py:295-342); otherwise functional.assign
+// from a tensor (utils.py:29-101).
+WXX_API int wxx_copy_strided(void* dst, const void* src, int itemsize, int rank,
+                             const int64_t* shape, const int64_t* s_dst, const int64_t* s_src) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(dst && src && shape && s_dst && s_src, "null pointer");
+  WXX_REQUIRE(itemsize == 4 || itemsize == 8, "itemsize %d unsupported", itemsize);
+  WXX_REQUIRE(rank >= 0 && rank <= wxx::kMaxRank, "rank %d unsupported", rank);
+  int64_t n = 1;
+  for (int d = 0; d < rank; ++d) n *= shape[d];
+  if (n == 0) return WXX_OK;
+  const int64_t* ss[2] = {s_dst, s_src};
+  ND nd = collapse(rank, shape, ss, 2);
+  hipStream_t s = wxx::stream();
+  // Transpose-shaped gather: destination dense, source innermost stride != 1
+  // but unit stride on the next dim -> LDS-tiled transpose.
+  if (nd.rank >= 2 && nd.rank <= 3 && nd.stride[0][nd.rank - 1] == 1 &&
+      nd.stride[1][nd.rank - 2] == 1 && nd.stride[1][nd.rank - 1] != 1 &&
+      nd.stride[0][nd.rank - 2] == nd.shape[nd.rank - 1] &&
+      (nd.rank == 2 || nd.stride[0][0] == nd.shape[1] * nd.shape[2])) {
+    const int64_t rows = nd.shape[nd.rank - 2], cols = nd.shape[nd.rank - 1];
+    const int64_t batch = nd.rank == 3 ? nd.shape[0] : 1;
+    const int64_t sb = nd.rank == 3 ? nd.stride[1][0] : 0;
+    if (batch <= 65535 && (rows + 63) / 64 <= 65535) {
+      dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64), (unsigned)batch);
+      if (itemsize == 4)
+        hipLaunchKernelGGL(transpose_tile_kernel<uint32_t>, grid, dim3(kBlock), 0, s,
+                           (uint32_t*)dst, (const uint32_t*)src, batch, rows, cols, sb,
+                           nd.stride[1][nd.rank - 2], nd.stride[1][nd.rank - 1]);
+      else
+        hipLaunchKernelGGL(transpose_tile_kernel<uint64_t>, grid, dim3(kBlock), 0, s,
+                           (uint64_t*)dst, (const uint64_t*)src, batch, rows, cols, sb,
+                           nd.stride[1][nd.rank - 2], nd.stride[1][nd.rank - 1]);
+      WXX_LAUNCHED();
+      return WXX_OK;
+    }
+  }
+  const bool big = !fits32(nd, n);
+  if (itemsize == 4) {
+    if (big)
+      hipLaunchKernelGGL((copy_strided_kernel<uint32_t, true>), dim3(grid_for(n)), dim3(kBlock),
+                         0, s, (uint32_t*)dst, (const uint32_t*)src, nd, n);
+    else
+      hipLaunchKernelGGL((copy_strided_kernel<uint32_t, false>), dim3(grid_for(n)), dim3(kBlock),
+                         0, s, (uint32_t*)dst, (const uint32_t*)src, nd, n);
+  } else {
+    if (big)
+      hipLaunchKernelGGL((copy_strided_kernel<uint64_t, true>), dim3(grid_for(n)), dim3(kBlock),
+                         0, s, (uint64_t*)dst, (const uint64_t*)src, nd, n);
+    else
+      hipLaunchKernelGGL((copy_strided_kernel<uint64_t, false>), dim3(grid_for(n)), dim3(kBlock),
+                         0, s, (uint64_t*)dst, (const uint64_t*)src, nd, n);
+  }
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// Fill a strided view with a 32-bit pattern (functional.assign with a
+// scalar, reference functional/utils.py:29-101).
+WXX_API int wxx_fill_strided(void* dst, int rank, const int64_t* shape, const int64_t* s_dst,
+                             uint32_t bits) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(dst && shape && s_dst, "null pointer");
+  WXX_REQUIRE(rank >= 0 && rank <= wxx::kMaxRank, "rank %d unsupported", rank);
+  int64_t n = 1;
+  for (int d = 0; d < rank; ++d) n *= shape[d];
+  if (n == 0) return WXX_OK;
+  const int64_t* ss[1] = {s_dst};
+  ND nd = collapse(rank, shape, ss, 1);
+  if (nd.rank == 1 && nd.stride[0][0] == 1) return wxx_fill_u32(dst, n, bits);
+  hipLaunchKernelGGL(fill_strided_kernel<uint32_t>, dim3(grid_for(n)), dim3(kBlock), 0,
+                     wxx::stream(), (uint32_t*)dst, nd, n, bits);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// out (dense, shape `shape`) = zeros with `grad` (strided) placed at
+// [start, start+length) along `dim`.  Replaces functional.scatter_zeros
+// (reference functional/utils.py:760-827).
+WXX_API int wxx_scatter_zeros(float* out, const float* grad, int rank, const int64_t* shape,
+                              const int64_t* s_grad, int dim, int64_t start, int64_t length) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(out && grad && shape && s_grad, "null pointer");
+  WXX_REQUIRE(rank >= 1 && rank <= wxx::kMaxRank && dim >= 0 && dim < rank, "bad rank/dim");
+  ND nd;
+  nd.rank = rank;
+  int64_t n = 1;
+  for (int d = 0; d < rank; ++d) {
+    nd.shape[d] = shape[d];
+    nd.stride[0][d] = s_grad[d];
+    n *= shape[d];
+  }
+  if (n == 0) return WXX_OK;
+  hipLaunchKernelGGL(scatter_zeros_kernel, dim3(grid_for(n)), dim3(kBlock), 0, wxx::stream(), out,
+                     grad, nd, n, dim, start, length);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// Replaces functional.unfolddx (reference functional/utils.py:239-287).
+WXX_API int wxx_unfolddx(const float* dy, float* dx, int64_t prefix, int64_t length,
+                         int64_t suffix, int64_t windows, int64_t size, int64_t step) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(dy && dx, "null pointer");
+  WXX_REQUIRE(size >= 1 && step >= 1 && suffix >= 1, "bad unfold parameters");
+  const int64_t n = prefix * length * suffix;
+  if (n <= 0) return WXX_OK;
+  hipLaunchKernelGGL(unfolddx_kernel, dim3(grid_for(n)), dim3(kBlock), 0, wxx::stream(), dy, dx,
+                     prefix, length, suffix, windows, size, step);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}

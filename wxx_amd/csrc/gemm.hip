@@ -1,0 +1,378 @@
+// Batched fp32 GEMM with fused bias on the CDNA4 fp32 matrix cores:
+//     C[b] = op(A[b]) . op(B[b]) + bias
+//
+// Reference semantics (src/wxx/shaders/matmul.wgsl:1-151, host
+// src/wxx/functional/utils.py:378-499):
+//  * A is (M, K) row-major, or (K, M) when transpose_A; B is (K, N), or
+//    (N, K) when transpose_B; an unbatched operand has batch stride 0;
+//  * bias_mode 0 = none, 1 = (N,), 2 = (M, N) shared by every batch,
+//    3 = (batch, M, N);
+//  * every output element is sum_k A[i,k] B[k,j] accumulated in fp32.
+//
+// MI355X design (not a translation of the reference's 16x16-thread,
+// 4x4-register scalar tile):
+//  * 256-thread workgroups (4 wavefronts) own a BM x BN tile; each wave owns
+//    a WM x WN sub-tile computed with v_mfma_f32_32x32x2f32 (64 FLOP/clk per
+//    SIMD, the fp32 matrix peak of 157.3 TFLOP/s at 256 CUs);
+//  * A and B tiles are staged k-major in LDS ([BK][BM] and [BK][BN]) and
+//    double buffered: the global loads of chunk k+1 are in flight while the
+//    MFMAs of chunk k run, one barrier per chunk;
+//  * within an MFMA the two K lanes (lane / 32) take k and k + BK/2 of the
+//    chunk, so a lane's A/B fragment is one conflict-free ds_read_b32;
+//  * tile ids are remapped so that consecutive tiles land on the same XCD
+//    (each of the 8 XCDs has its own L2) and walked in GROUP_M row groups;
+//  * full interior tiles use float4 global loads without bounds checks,
+//    edge tiles and ragged K fall back to guarded scalar loads.
+#include "common.h"
+
+namespace {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+struct GemmArgs {
+  const float* A;
+  const float* B;
+  const float* bias;
+  float* C;
+  int64_t M, N, K;
+  int64_t lda, ldb, ldc;
+  int64_t sA, sB, sC, sBias;
+  int64_t bias_rows;  // mode 2: rows of the bias matrix (row index taken modulo)
+  int bias_mode;
+  int tiles_m, tiles_n;
+  int vec_ok;  // all leading dims, batch strides and base pointers allow float4
+};
+
+constexpr int kGroupM = 8;
+constexpr int kPad = 4;
+
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB>
+struct GemmCfg {
+  static constexpr int kThreads = 256;
+  static constexpr int kWavesM = BM / WM;
+  static constexpr int kWavesN = BN / WN;
+  static_assert(kWavesM * kWavesN == 4, "4 waves per workgroup");
+  static constexpr int TM = WM / 32;
+  static constexpr int TN = WN / 32;
+  static constexpr int LDA_S = BM + kPad;  // LDS row stride (floats) of the A tile
+  static constexpr int LDB_S = BN + kPad;
+  // global -> register loads, in float4 units per thread
+  static constexpr int PA = (BM * BK) / (4 * kThreads);
+  static constexpr int PB = (BN * BK) / (4 * kThreads);
+  static_assert(PA >= 1 && PB >= 1, "tile too small for 256 threads");
+};
+
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB>
+__global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
+  using Cfg = GemmCfg<BM, BN, BK, WM, WN, TA, TB>;
+  constexpr int TM = Cfg::TM, TN = Cfg::TN;
+  constexpr int LDA_S = Cfg::LDA_S, LDB_S = Cfg::LDB_S;
+  constexpr int PA = Cfg::PA, PB = Cfg::PB;
+
+  __shared__ __attribute__((aligned(16))) float As[2][BK * LDA_S];
+  __shared__ __attribute__((aligned(16))) float Bs[2][BK * LDB_S];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / Cfg::kWavesN;
+  const int wn = wave % Cfg::kWavesN;
+
+  // ---- tile id: XCD-contiguous remap, then GROUP_M swizzle -------------
+  const int ntiles = g.tiles_m * g.tiles_n;
+  int bid = blockIdx.x;
+  if ((ntiles & 7) == 0) bid = (bid & 7) * (ntiles >> 3) + (bid >> 3);
+  const int group_size = kGroupM * g.tiles_n;
+  const int group = bid / group_size;
+  const int first_m = group * kGroupM;
+  const int gm = min(g.tiles_m - first_m, kGroupM);
+  const int tile_m = first_m + (bid % group_size) % gm;
+  const int tile_n = (bid % group_size) / gm;
+
+  const int64_t batch = blockIdx.y;
+  const float* __restrict__ A = g.A + batch * g.sA;
+  const float* __restrict__ B = g.B + batch * g.sB;
+  float* __restrict__ C = g.C + batch * g.sC;
+
+  const int64_t m0 = (int64_t)tile_m * BM;
+  const int64_t n0 = (int64_t)tile_n * BN;
+  const int64_t M = g.M, N = g.N, K = g.K;
+  const bool full_mn = g.vec_ok && (m0 + BM <= M) && (n0 + BN <= N);
+
+  float4 ra[PA], rb[PB];
+
+  // ---- global -> registers for the K chunk starting at k0 ---------------
+  auto load_chunk = [&](int64_t k0, bool fast) {
+#pragma unroll
+    for (int p = 0; p < PA; ++p) {
+      const int f = p * 256 + tid;  // float4 index within the A tile
+      int64_t i, k;
+      if (!TA) {
+        constexpr int KV = BK / 4;
+        i = m0 + f / KV;
+        k = k0 + (f % KV) * 4;
+        const float* src = A + i * g.lda + k;
+        if (fast) {
+          ra[p] = *reinterpret_cast<const float4*>(src);
+        } else {
+          float v[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) v[c] = (i < M && k + c < K) ? src[c] : 0.f;
+          ra[p] = make_float4(v[0], v[1], v[2], v[3]);
+        }
+      } else {
+        constexpr int IV = BM / 4;
+        i = m0 + (f % IV) * 4;
+        k = k0 + f / IV;
+        const float* src = A + k * g.lda + i;
+        if (fast) {
+          ra[p] = *reinterpret_cast<const float4*>(src);
+        } else {
+          float v[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) v[c] = (k < K && i + c < M) ? src[c] : 0.f;
+          ra[p] = make_float4(v[0], v[1], v[2], v[3]);
+        }
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < PB; ++p) {
+      const int f = p * 256 + tid;
+      int64_t j, k;
+      if (!TB) {
+        constexpr int JV = BN / 4;
+        j = n0 + (f % JV) * 4;
+        k = k0 + f / JV;
+        const float* src = B + k * g.ldb + j;
+        if (fast) {
+          rb[p] = *reinterpret_cast<const float4*>(src);
+        } else {
+          float v[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) v[c] = (k < K && j + c < N) ? src[c] : 0.f;
+          rb[p] = make_float4(v[0], v[1], v[2], v[3]);
+        }
+      } else {
+        constexpr int KV = BK / 4;
+        j = n0 + f / KV;
+        k = k0 + (f % KV) * 4;
+        const float* src = B + j * g.ldb + k;
+        if (fast) {
+          rb[p] = *reinterpret_cast<const float4*>(src);
+        } else {
+          float v[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) v[c] = (j < N && k + c < K) ? src[c] : 0.f;
+          rb[p] = make_float4(v[0], v[1], v[2], v[3]);
+        }
+      }
+    }
+  };
+
+  // ---- registers -> LDS (k-major tiles) ----------------------------------
+  auto store_chunk = [&](int buf) {
+    float* as = As[buf];
+    float* bs = Bs[buf];
+#pragma unroll
+    for (int p = 0; p < PA; ++p) {
+      const int f = p * 256 + tid;
+      if (!TA) {
+        constexpr int KV = BK / 4;
+        const int i = f / KV, k = (f % KV) * 4;
+        as[(k + 0) * LDA_S + i] = ra[p].x;
+        as[(k + 1) * LDA_S + i] = ra[p].y;
+        as[(k + 2) * LDA_S + i] = ra[p].z;
+        as[(k + 3) * LDA_S + i] = ra[p].w;
+      } else {
+        constexpr int IV = BM / 4;
+        const int i = (f % IV) * 4, k = f / IV;
+        *reinterpret_cast<float4*>(&as[k * LDA_S + i]) = ra[p];
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < PB; ++p) {
+      const int f = p * 256 + tid;
+      if (!TB) {
+        constexpr int JV = BN / 4;
+        const int j = (f % JV) * 4, k = f / JV;
+        *reinterpret_cast<float4*>(&bs[k * LDB_S + j]) = rb[p];
+      } else {
+        constexpr int KV = BK / 4;
+        const int j = f / KV, k = (f % KV) * 4;
+        bs[(k + 0) * LDB_S + j] = rb[p].x;
+        bs[(k + 1) * LDB_S + j] = rb[p].y;
+        bs[(k + 2) * LDB_S + j] = rb[p].z;
+        bs[(k + 3) * LDB_S + j] = rb[p].w;
+      }
+    }
+  };
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int b = 0; b < TN; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+
+  const int half = lane >> 5;  // which K lane of the MFMA this lane feeds
+  const int l32 = lane & 31;
+  const int a_off = wm * WM + l32;
+  const int b_off = wn * WN + l32;
+
+  const int64_t nk = (K + BK - 1) / BK;
+  load_chunk(0, full_mn && BK <= K);
+  store_chunk(0);
+  __syncthreads();
+
+  for (int64_t kc = 0; kc < nk; ++kc) {
+    const int cur = (int)(kc & 1);
+    if (kc + 1 < nk) {
+      const int64_t k1 = (kc + 1) * BK;
+      load_chunk(k1, full_mn && k1 + BK <= K);
+    }
+    const float* as = As[cur];
+    const float* bs = Bs[cur];
+#pragma unroll
+    for (int s = 0; s < BK / 2; ++s) {
+      const int kk = s + half * (BK / 2);
+      float af[TM], bf[TN];
+#pragma unroll
+      for (int a = 0; a < TM; ++a) af[a] = as[kk * LDA_S + a_off + 32 * a];
+#pragma unroll
+      for (int b = 0; b < TN; ++b) bf[b] = bs[kk * LDB_S + b_off + 32 * b];
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a], bf[b], acc[a][b], 0, 0, 0);
+    }
+    if (kc + 1 < nk) store_chunk(cur ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: D[i][j] of a 32x32 tile sits in lane j + 32*((i/4)%2),
+  //      register (i%4) + 4*(i/8) --------------------------------------------
+  const float* __restrict__ bias = g.bias;
+#pragma unroll
+  for (int a = 0; a < TM; ++a) {
+#pragma unroll
+    for (int b = 0; b < TN; ++b) {
+      const int64_t col = n0 + wn * WN + 32 * b + l32;
+      if (col >= N) continue;
+      float bias1 = 0.f;
+      if (g.bias_mode == 1) bias1 = bias[col];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm * WM + 32 * a + 8 * (r >> 2) + 4 * half + (r & 3);
+        if (row < M) {
+          float v = acc[a][b][r];
+          if (g.bias_mode == 1)
+            v += bias1;
+          else if (g.bias_mode == 2)
+            v += bias[(row % g.bias_rows) * N + col];
+          else if (g.bias_mode == 3)
+            v += bias[batch * g.sBias + row * N + col];
+          C[row * g.ldc + col] = v;
+        }
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int BK, int WM, int WN>
+int launch_cfg(GemmArgs& g, int64_t batch, bool ta, bool tb) {
+  g.tiles_m = (int)((g.M + BM - 1) / BM);
+  g.tiles_n = (int)((g.N + BN - 1) / BN);
+  dim3 grid((unsigned)(g.tiles_m * g.tiles_n), (unsigned)batch);
+  hipStream_t s = wxx::stream();
+  if (!ta && !tb)
+    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, false>), grid, dim3(256),
+                       0, s, g);
+  else if (!ta && tb)
+    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, true>), grid, dim3(256),
+                       0, s, g);
+  else if (ta && !tb)
+    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, false>), grid, dim3(256),
+                       0, s, g);
+  else
+    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, true>), grid, dim3(256),
+                       0, s, g);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+inline bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+// Replaces functional.matmul_add (reference src/wxx/functional/utils.py:378-499).
+// Strides are in elements; sA / sB == 0 marks an unbatched operand.
+// tile: 0 = choose automatically, 1 = 64x64, 2 = 128x128, 3 = 256x128.
+WXX_API int wxx_matmul_add(const float* A, const float* B, const float* bias, float* C,
+                           int64_t M, int64_t N, int64_t K, int64_t batch, int64_t sA,
+                           int64_t sB, int64_t sBias, int bias_mode, int transpose_A,
+                           int transpose_B, int tile) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(A && B && C, "null pointer");
+  WXX_REQUIRE(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "negative GEMM dims");
+  WXX_REQUIRE(bias_mode >= 0 && bias_mode <= 3, "bad bias_mode %d", bias_mode);
+  WXX_REQUIRE(bias_mode == 0 || bias, "bias pointer is null for bias_mode %d", bias_mode);
+  WXX_REQUIRE(batch <= 65535, "batch %lld exceeds 65535", (long long)batch);
+  if (M == 0 || N == 0 || batch == 0) return WXX_OK;
+
+  GemmArgs g;
+  g.A = A;
+  g.B = B;
+  g.bias = bias;
+  g.C = C;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.lda = transpose_A ? M : K;
+  g.ldb = transpose_B ? K : N;
+  g.ldc = N;
+  g.sA = sA;
+  g.sB = sB;
+  g.sC = M * N;
+  g.sBias = sBias;
+  g.bias_mode = bias_mode;
+  g.bias_rows = M;
+  int64_t nb = batch;
+  // Fold the batch into M when B is shared and A's rows are contiguous across
+  // batches: one larger GEMM fills the GPU better than `batch` small ones.
+  if (batch > 1 && sB == 0 && !transpose_A && sA == M * K) {
+    g.M = M * batch;
+    g.sA = 0;
+    g.sC = 0;
+    if (bias_mode == 3) {
+      g.bias_mode = 2;
+      g.bias_rows = M * batch;
+    }
+    nb = 1;
+  }
+  g.vec_ok = (g.lda % 4 == 0) && (g.ldb % 4 == 0) && (g.sA % 4 == 0) && (g.sB % 4 == 0) &&
+             al16(A) && al16(B);
+
+  if (K == 0) {
+    // Empty contraction: C = bias (or 0).  Reuse the kernel with K = 0: the
+    // k-loop is skipped and the epilogue writes the bias.
+  }
+  if (tile == 0) {
+    const int64_t cus = wxx::num_cus() > 0 ? wxx::num_cus() : 256;
+    const int64_t t128 = ((g.M + 127) / 128) * ((g.N + 127) / 128) * nb;
+    const int64_t t256 = ((g.M + 255) / 256) * ((g.N + 127) / 128) * nb;
+    if (t256 >= 2 * cus && g.K >= 256)
+      tile = 3;
+    else if (t128 >= cus)
+      tile = 2;
+    else
+      tile = 1;
+  }
+  switch (tile) {
+    case 1: return launch_cfg<64, 64, 16, 32, 32>(g, nb, transpose_A, transpose_B);
+    case 2: return launch_cfg<128, 128, 16, 64, 64>(g, nb, transpose_A, transpose_B);
+    case 3: return launch_cfg<256, 128, 16, 128, 64>(g, nb, transpose_A, transpose_B);
+    default: return wxx::set_error(WXX_E_ARG, "bad tile %d", tile);
+  }
+}

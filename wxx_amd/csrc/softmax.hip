@@ -1,0 +1,136 @@
+// Softmax along one axis of a contiguous f32 tensor viewed as
+// (outer, C, inner).
+//
+// Reference semantics (src/wxx/shaders/activations/softmax.wgsl:25-77,
+// host src/wxx/functional/activations.py:126-173): m = max(-1e38, max_c x),
+// s = sum_c exp(x - m), y = exp(x - m) * (1 / s).
+//
+// MI355X design: the reference runs one thread per row with three serial,
+// uncoalesced passes.  Here a row (inner == 1) lives in VGPRs of one wave
+// (C <= 2048) or one workgroup (C <= 16384): one HBM read, one HBM write,
+// wave-shuffle reductions.  Longer rows use an online (max, sum) pass and a
+// write pass.  inner > 1 gives each thread one column so lanes read
+// consecutive addresses.
+#include "rows.h"
+
+namespace {
+
+template <int TPR, int NCH, bool VEC>
+__global__ __launch_bounds__(256) void softmax_rows_kernel(const float* __restrict__ x,
+                                                            float* __restrict__ y, int64_t rows,
+                                                            int C) {
+  __shared__ float red[4];
+  constexpr int RPB = 256 / TPR;
+  const int t = threadIdx.x % TPR;
+  const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;
+  if (TPR == 64 && row >= rows) return;
+  const float* xr = x + row * C;
+  wxx::RowRegs<TPR, NCH, VEC> r;
+  r.load(xr, C, t, -INFINITY);
+  float m = -1e38f;
+#pragma unroll
+  for (int e = 0; e < NCH * 4; ++e) m = fmaxf(m, r.v[e]);
+  m = wxx::RowReduce<TPR>::max(m, red);
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < NCH * 4; ++e) {
+    float ev = r.valid(e, t, C) ? expf(r.v[e] - m) : 0.f;
+    r.v[e] = ev;
+    s += ev;
+  }
+  s = wxx::RowReduce<TPR>::sum(s, red);
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int e = 0; e < NCH * 4; ++e) r.v[e] *= inv;
+  r.store(y + row * C, C, t);
+}
+
+// Rows longer than 16384: online max/sum in one pass, then a write pass.
+__global__ __launch_bounds__(256) void softmax_rows_looped_kernel(const float* __restrict__ x,
+                                                                   float* __restrict__ y,
+                                                                   int64_t C) {
+  __shared__ float sm[4], ss[4];
+  const int64_t row = blockIdx.x;
+  const float* xr = x + row * C;
+  float m = -1e38f, s = 0.f;
+  for (int64_t c = threadIdx.x; c < C; c += 256) {
+    float v = xr[c];
+    if (v > m) {
+      s = s * expf(m - v) + 1.f;
+      m = v;
+    } else {
+      s += expf(v - m);
+    }
+  }
+  // Combine (m, s) pairs: first within the wave, then across the 4 waves.
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    float om = __shfl_xor(m, off, 64), os = __shfl_xor(s, off, 64);
+    float nm = fmaxf(m, om);
+    s = s * expf(m - nm) + os * expf(om - nm);
+    m = nm;
+  }
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (lane == 0) {
+    sm[w] = m;
+    ss[w] = s;
+  }
+  __syncthreads();
+  float M = sm[0];
+  for (int i = 1; i < 4; ++i) M = fmaxf(M, sm[i]);
+  float S = 0.f;
+  for (int i = 0; i < 4; ++i) S += ss[i] * expf(sm[i] - M);
+  const float inv = 1.0f / S;
+  float* yr = y + row * C;
+  for (int64_t c = threadIdx.x; c < C; c += 256) yr[c] = expf(xr[c] - M) * inv;
+}
+
+// inner > 1: thread per (outer, inner) column, three passes over C.
+__global__ __launch_bounds__(256) void softmax_cols_kernel(const float* __restrict__ x,
+                                                            float* __restrict__ y, int64_t outer,
+                                                            int64_t C, int64_t inner) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= outer * inner) return;
+  const int64_t o = t / inner, i = t - o * inner;
+  const float* p = x + o * C * inner + i;
+  float* q = y + o * C * inner + i;
+  float m = -1e38f;
+  for (int64_t c = 0; c < C; ++c) m = fmaxf(m, p[c * inner]);
+  float s = 0.f;
+  for (int64_t c = 0; c < C; ++c) s += expf(p[c * inner] - m);
+  const float inv = 1.0f / s;
+  for (int64_t c = 0; c < C; ++c) q[c * inner] = expf(p[c * inner] - m) * inv;
+}
+
+}  // namespace
+
+// Replaces functional.softmax (reference src/wxx/functional/activations.py:126-173).
+WXX_API int wxx_softmax(const float* x, float* y, int64_t outer, int64_t C, int64_t inner) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(x && y, "null pointer");
+  WXX_REQUIRE(outer >= 0 && C >= 1 && inner >= 1, "bad softmax dims");
+  if (outer == 0) return WXX_OK;
+  hipStream_t s = wxx::stream();
+  if (inner == 1) {
+    const bool vec = (C % 4 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0);
+    if (wxx::row_plan(C) == 0) {
+      hipLaunchKernelGGL(softmax_rows_looped_kernel, dim3((unsigned)outer), dim3(256), 0, s, x,
+                         y, C);
+    } else {
+      int rc = wxx::row_dispatch(C, vec, [&](auto tpr, auto nch, auto v) {
+        hipLaunchKernelGGL((softmax_rows_kernel<decltype(tpr)::value, decltype(nch)::value,
+                                                decltype(v)::value>),
+                           wxx::row_grid(decltype(tpr)::value, outer), dim3(256), 0, s, x, y,
+                           outer, (int)C);
+        return 0;
+      });
+      if (rc) return rc;
+    }
+    WXX_LAUNCHED();
+    return WXX_OK;
+  }
+  hipLaunchKernelGGL(softmax_cols_kernel, dim3(wxx::grid_1d(outer * inner, 256)), dim3(256), 0,
+                     s, x, y, outer, C, inner);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}

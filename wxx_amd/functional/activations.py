@@ -1,0 +1,108 @@
+"""Activation functions, their local derivatives and softmax
+(reference src/wxx/functional/activations.py:22-173).
+
+The ``*backwards`` / ``*back`` functions return the local derivative, as in
+the reference; autograd multiplies by the incoming gradient.
+"""
+
+from .. import validation
+from ..backend.dispatch import _get_reduce_dims
+from ._common import call, empty, ptr
+
+# Must match enum Unary in csrc/elementwise.hip.
+UNARY = {
+    "relu": 0,
+    "relubackwards": 1,
+    "gelu": 2,
+    "gelubackwards": 3,
+    "sigmoid": 4,
+    "sigmoidbackwards": 5,
+    "selu": 6,
+    "selubackwards": 7,
+    "sin": 8,
+    "sinback": 9,
+    "cos": 10,
+    "cosback": 11,
+    "abs": 12,
+    "exp": 13,
+    "log": 14,
+    "negate": 15,
+    "rsqrt": 16,
+    "sign": 17,
+    "sqrt": 18,
+    "square": 19,
+}
+
+
+def unary(tensor1, name):
+    """Run unary kernel ``name`` on a contiguous copy of ``tensor1``."""
+    if not tensor1.is_contiguous():
+        tensor1 = tensor1.contiguous()
+    validation.check_rank(tensor1.shape, name="unary op input")
+    out = empty(tensor1.shape, requires_grad=tensor1.requires_grad)
+    call("wxx_unary", ptr(tensor1), ptr(out), validation.numel(tensor1.shape), UNARY[name])
+    return out
+
+
+def relu(tensor1):
+    return unary(tensor1, "relu")
+
+
+def relubackwards(tensor1):
+    return unary(tensor1, "relubackwards")
+
+
+def gelu(tensor1):
+    return unary(tensor1, "gelu")
+
+
+def gelubackwards(tensor1):
+    return unary(tensor1, "gelubackwards")
+
+
+def sigmoid(tensor1):
+    return unary(tensor1, "sigmoid")
+
+
+def sigmoidbackwards(tensor1):
+    """Local derivative from the sigmoid *output* ``y``: ``y (1 - y)``."""
+    return unary(tensor1, "sigmoidbackwards")
+
+
+def selu(tensor1):
+    return unary(tensor1, "selu")
+
+
+def selubackwards(tensor1):
+    return unary(tensor1, "selubackwards")
+
+
+def sin(tensor1):
+    return unary(tensor1, "sin")
+
+
+def sinback(tensor1):
+    return unary(tensor1, "sinback")
+
+
+def cos(tensor1):
+    return unary(tensor1, "cos")
+
+
+def cosback(tensor1):
+    return unary(tensor1, "cosback")
+
+
+def softmax(tensor1, dim):
+    """Softmax along ``dim``."""
+    if not tensor1.is_contiguous():
+        tensor1 = tensor1.contiguous()
+    rank = validation.check_rank(tensor1.shape, name="softmax input")
+    dim = validation.normalize_dim(dim, rank, name="dim")
+    if tensor1.type != "f32":
+        raise TypeError(f"softmax expects f32 input, got {tensor1.type!r}")
+    outer, c, inner, _ = _get_reduce_dims(tensor1.shape, dim)
+    out = empty(tensor1.shape, requires_grad=tensor1.requires_grad)
+    if validation.numel(tensor1.shape):
+        call("wxx_softmax", ptr(tensor1), ptr(out), outer, c, inner)
+    return out

@@ -1,0 +1,124 @@
+"""Normalisation: RMSNorm, LayerNorm ("meanvarnorm") and BatchNorm, forward
+and backward (reference src/wxx/functional/normalization.py:24-513).
+
+Eps values follow the reference: LayerNorm 1e-5 (normalization.py:94),
+RMSNorm 1e-6 (:36), BatchNorm 1e-5 with momentum 0.1 (:157).
+"""
+
+from ..backend import compat
+from ..backend.dispatch import _get_reduce_dims
+from ._common import call, contiguous_f32, empty, ptr
+
+LN_EPS = 1e-5
+RMS_EPS = 1e-6
+BN_EPS = 1e-5
+BN_MOMENTUM = 0.1
+
+
+def rmsnorm(tensor1, gamma, axis=None):
+    """``y = x * r * gamma`` with ``r = rsqrt(mean(x^2) + 1e-6)`` (0 for an all-zero slice)."""
+    tensor1 = contiguous_f32(tensor1)
+    gamma = contiguous_f32(gamma, "gamma")
+    outer, red, inner, out_shape = _get_reduce_dims(tensor1.shape, axis)
+    y = empty(tensor1.shape)
+    irms = empty(out_shape)
+    call("wxx_rmsnorm", ptr(tensor1), ptr(gamma), ptr(y), ptr(irms), outer, red, inner,
+         RMS_EPS, compat.row_cap())
+    return y, irms
+
+
+def meanvarnorm(tensor1, gamma, beta, axis=None):
+    """LayerNorm over ``axis``; returns ``(y, mean, inv_std)``."""
+    tensor1 = contiguous_f32(tensor1)
+    gamma = contiguous_f32(gamma, "gamma")
+    beta = contiguous_f32(beta, "beta")
+    outer, red, inner, out_shape = _get_reduce_dims(tensor1.shape, axis)
+    y = empty(tensor1.shape)
+    mean = empty(out_shape)
+    istd = empty(out_shape)
+    call("wxx_meanvarnorm", ptr(tensor1), ptr(gamma), ptr(beta), ptr(y), ptr(mean), ptr(istd),
+         outer, red, inner, LN_EPS, compat.row_cap())
+    return y, mean, istd
+
+
+def meanvarnormdx(grad, tensor1, gamma, mean, var, axis=None):
+    """LayerNorm input gradient (``var`` is the saved inv_std, as in the reference)."""
+    tensor1 = contiguous_f32(tensor1)
+    gamma = contiguous_f32(gamma, "gamma")
+    grad = contiguous_f32(grad, "grad")
+    outer, red, inner, _ = _get_reduce_dims(tensor1.shape, axis)
+    dx = empty(tensor1.shape)
+    call("wxx_meanvarnormdx", ptr(grad), ptr(tensor1), ptr(gamma), ptr(mean), ptr(var), ptr(dx),
+         outer, red, inner, compat.row_cap())
+    return dx
+
+
+def meanvarnormdg(grad, tensor1, mean, var, axis=None):
+    """LayerNorm ``(dgamma, dbeta)``."""
+    tensor1 = contiguous_f32(tensor1)
+    grad = contiguous_f32(grad, "grad")
+    outer, red, inner, _ = _get_reduce_dims(tensor1.shape, axis)
+    dg = empty((red,))
+    db = empty((red,))
+    call("wxx_meanvarnormdg", ptr(grad), ptr(tensor1), ptr(mean), ptr(var), ptr(dg), ptr(db),
+         outer, red, inner)
+    return dg, db
+
+
+def rmsnormdx(grad, tensor1, gamma, irms, axis=None):
+    tensor1 = contiguous_f32(tensor1)
+    gamma = contiguous_f32(gamma, "gamma")
+    grad = contiguous_f32(grad, "grad")
+    outer, red, inner, _ = _get_reduce_dims(tensor1.shape, axis)
+    dx = empty(tensor1.shape)
+    call("wxx_rmsnormdx", ptr(grad), ptr(tensor1), ptr(gamma), ptr(irms), ptr(dx),
+         outer, red, inner)
+    return dx
+
+
+def rmsnormdg(grad, tensor1, gamma, irms, axis=None):
+    tensor1 = contiguous_f32(tensor1)
+    grad = contiguous_f32(grad, "grad")
+    outer, red, inner, _ = _get_reduce_dims(tensor1.shape, axis)
+    dg = empty(gamma.shape)
+    call("wxx_rmsnormdg", ptr(grad), ptr(tensor1), ptr(irms), ptr(dg), outer, red, inner)
+    return dg
+
+
+def batchnorm(tensor1, gamma, beta, running_mean, running_std, training=False):
+    """Per-channel BatchNorm over (B, H, W) of an NCHW tensor; returns ``(y, mean, inv_std)``.
+
+    ``running_std`` holds the running *variance* (reference naming).
+    """
+    tensor1 = contiguous_f32(tensor1)
+    gamma = contiguous_f32(gamma, "gamma")
+    B, Cc, H, W = tensor1.shape
+    y = empty(tensor1.shape)
+    mean = empty((Cc,))
+    istd = empty((Cc,))
+    call("wxx_batchnorm", ptr(tensor1), ptr(gamma), ptr(beta), ptr(running_mean),
+         ptr(running_std), ptr(y), ptr(mean), ptr(istd), B, Cc, H * W, BN_EPS, BN_MOMENTUM,
+         1 if training else 0)
+    return y, mean, istd
+
+
+def batchnormdx(grad, tensor1, gamma, dgamma, dbeta, saved_mean, saved_std):
+    tensor1 = contiguous_f32(tensor1)
+    gamma = contiguous_f32(gamma, "gamma")
+    grad = contiguous_f32(grad, "grad")
+    B, Cc, H, W = tensor1.shape
+    dx = empty(tensor1.shape)
+    call("wxx_batchnormdx", ptr(grad), ptr(tensor1), ptr(gamma), ptr(dgamma), ptr(dbeta),
+         ptr(saved_mean), ptr(saved_std), ptr(dx), B, Cc, H * W)
+    return dx
+
+
+def batchnormdg(grad, tensor1, saved_mean, saved_std):
+    tensor1 = contiguous_f32(tensor1)
+    grad = contiguous_f32(grad, "grad")
+    B, Cc, H, W = tensor1.shape
+    dg = empty((Cc,))
+    db = empty((Cc,))
+    call("wxx_batchnormdg", ptr(grad), ptr(tensor1), ptr(saved_mean), ptr(saved_std), ptr(dg),
+         ptr(db), B, Cc, H * W)
+    return dg, db
