@@ -82,6 +82,10 @@ int wxx_maxmin_backward(const float* g, const uint32_t* idx, float* out, int64_t
                         int64_t reduce, int64_t inner);
 /* functional.softmax (functional/activations.py:126-173) */
 int wxx_softmax(const float* x, float* y, int64_t outer, int64_t C, int64_t inner);
+/* Softmax backward dx = y * (g - sum(g * y)) along C: the multiply / sum /
+ * subtract / multiply chain of autograd softmax (autograd/reductions.py:25-35) */
+int wxx_softmax_backward(const float* y, const float* g, float* dx, int64_t outer, int64_t C,
+                         int64_t inner);
 /* functional.meanvarnorm (functional/normalization.py:82-145); row_cap 0 = all rows */
 int wxx_meanvarnorm(const float* x, const float* gamma, const float* beta, float* y,
                     float* mean, float* inv_std, int64_t outer, int64_t reduce, int64_t inner,
@@ -126,6 +130,13 @@ int wxx_scalarpointwise(const float* x, float* y, int64_t n, int op, float c, in
 /* backend/dispatch.py:_unary_op (:59-89) for the activation and unary math
  * kernels of functional/activations.py:22-124 and pointwise.py:293-354 */
 int wxx_unary(const float* x, float* y, int64_t n, int op);
+/* f'(x) * g for the activation backwards of autograd/pointwise.py:291-388
+ * (derivative kernel + pointwise multiply in one pass); op = derivative code */
+int wxx_unary_backward(const float* x, const float* g, float* y, int64_t n, int op);
+/* dst (dense over shape) = src (strides s_src, 0 = broadcast) * scale: the
+ * ones_like * grad products of sum/mean backward (autograd/reductions.py:38-95) */
+int wxx_broadcast_scale(float* dst, const float* src, int rank, const int64_t* shape,
+                        const int64_t* s_src, float scale);
 /* functional.clamp / clampbackwards (pointwise.py:149-228), masked_fill
  * (functional/utils.py:558-597); mode 0/1/2 */
 int wxx_clamp(const float* x, float* y, int64_t n, float lo, float hi, int mode);
@@ -147,6 +158,59 @@ int wxx_scatter_zeros(float* out, const float* grad, int rank, const int64_t* sh
 /* functional.unfolddx (functional/utils.py:239-287) */
 int wxx_unfolddx(const float* dy, float* dx, int64_t prefix, int64_t length, int64_t suffix,
                  int64_t windows, int64_t size, int64_t step);
+
+/* ---- C: FFT and complex ops (functional/fft.py).  X/complex pointers are c64. */
+/* functional.rfft (fft.py:484-563): rows x in_len -> rows x (n/2+1); n = 2^k <= 32768 */
+int wxx_rfft(const float* x, void* X, int64_t rows, int64_t in_len, int64_t n);
+/* functional.irfft (fft.py:566-645): rows x in_len -> rows x n; n = 2^k, 2 <= n <= 32768 */
+int wxx_irfft(const void* X, float* x, int64_t rows, int64_t in_len, int64_t n);
+/* functional.complex_mul (fft.py:168-213, op 0) and complex_add_inplace
+ * (fft.py:216-245, op 1); strides in complex elements, 0 = broadcast */
+int wxx_complex_binary(void* out, const void* a, const void* b, int rank, const int64_t* shape,
+                       const int64_t* s_out, const int64_t* s_a, const int64_t* s_b, int op,
+                       int conj_a, int conj_b);
+/* functional.complex_conj (fft.py:248-292) */
+int wxx_complex_conj(void* dst, const void* src, int rank, const int64_t* shape,
+                     const int64_t* s_dst, const int64_t* s_src);
+/* functional.complex_pad (fft.py:345-383) */
+int wxx_complex_pad(const void* src, void* dst, int64_t batch, int64_t in_len, int64_t out_len);
+
+/* ---- D7: loss — functional.cceloss (functional/loss.py:20-101) +
+ *      shaders/loss/cceloss.wgsl.  *bad (device int) is set to 1 when a
+ *      target is >= K; the caller zeroes and reads it. ---- */
+int wxx_cceloss(const float* z, const uint32_t* targets, float* loss, float* dz, int64_t B,
+                int64_t K, int* bad);
+
+/* ---- E8 / D8: optimizer and gradient norm ---------------------------------- */
+/* functional.adamw (functional/layers.py:21-68) */
+int wxx_adamw(float* p, const float* g, float* m, float* v, int64_t n, float lr, float beta1,
+              float beta2, float eps, float weight_decay, float bc1, float bc2);
+/* No reference counterpart: one launch for the whole parameter list of
+ * AdamW.step (nn/optimizer.py:69-84); p/g/m/v/n are host arrays of length count */
+int wxx_adamw_multi(void* const* p, void* const* g, void* const* m, void* const* v,
+                    const int64_t* n, int count, float lr, float beta1, float beta2, float eps,
+                    float weight_decay, float bc1, float bc2);
+/* No reference counterpart: the per-gradient sumsq + accumulate loop of
+ * clip_grad_norm_ (nn/utils.py:82-93) as one reduction into out[0] */
+int wxx_sumsq_multi(void* const* x, const int64_t* n, int count, float* out);
+/* No reference counterpart: the rescale loop of clip_grad_norm_ (nn/utils.py:97-101) */
+int wxx_scale_multi(void* const* x, const int64_t* n, int count, float c);
+
+/* ---- E6 / E7: embedding, dropout; C6: Hyena decay window ------------------ */
+/* functional.embed (functional/layers.py:161-206) */
+int wxx_embed(const uint32_t* ids, const float* W, float* out, int64_t ntok, int64_t D,
+              int64_t V);
+/* functional.embeddx (functional/layers.py:209-254), deterministic */
+int wxx_embeddx(const float* g, const uint32_t* ids, float* grad, int64_t ntok, int64_t D,
+                int64_t V);
+/* functional.dropout / dropoutdx (functional/layers.py:73-158) */
+int wxx_dropout(const float* x, float* y, int64_t n, uint32_t seed, float p, float scale);
+/* functional.decay_window (functional/pointwise.py:357-404) */
+int wxx_decay_window(const float* decay, float* w, int64_t rows, int64_t channels,
+                     int64_t length, int64_t stage);
+/* functional.decay_window_backward (functional/pointwise.py:407-457) */
+int wxx_decay_window_backward(const float* g, const float* decay, float* out, int64_t rows,
+                              int64_t channels, int64_t length, int64_t stage);
 
 #ifdef __cplusplus
 }

@@ -25,6 +25,15 @@ def softmax(x, dim=-1):
     return (e * (1.0 / e.sum(axis=dim, keepdims=True))).astype(np.float32)
 
 
+def softmax_backward(y, g, dim=-1):
+    """Softmax gradient from the output: y * (g - sum(g * y, dim)) (reference
+    src/wxx/autograd/reductions.py:25-35)."""
+    y = np.asarray(y, dtype=np.float64)
+    g = np.asarray(g, dtype=np.float64)
+    dot = (g * y).sum(axis=dim, keepdims=True)
+    return (y * (g - dot)).astype(np.float32)
+
+
 def gelu(x):
     x = np.asarray(x, dtype=np.float64)
     u = SQRT_2_OVER_PI * (x + GELU_C * x ** 3)

@@ -17,8 +17,34 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 
+# Test-only hook: run the GPU tests against the AddressSanitizer CPU build of
+# the kernels (tests/cpu_emu) by pointing the loader at that library.  Never
+# set on a GPU box; the product loader has no fallback of its own.
+_EMU = os.environ.get("WXX_TEST_EMU_LIB")
+if _EMU:
+    from wxx_amd.backend import lib as _wlib
+
+    _wlib.LIB_PATH = _EMU
+
+
+# Cases too large for the CPU emulation (multi-GFLOP GEMMs, 100M-element rows);
+# they run unchanged on the GPU.
+_EMU_HEAVY = ("test_matmul_config2_sizes", "test_softmax[shape2", "test_softmax[shape1-",
+              "test_layernorm_fwd_bwd[shape1-", "test_rmsnorm_fwd_bwd[shape1-",
+              "test_fft_full_size_properties", "test_hyena_shapes")
+
+
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (HIP device) and libwxx_hip.so")
+
+
+def pytest_collection_modifyitems(config, items):
+    if not _EMU:
+        return
+    skip = pytest.mark.skip(reason="too large for the CPU emulation; runs on the GPU")
+    for item in items:
+        if any(item.nodeid.split("::")[-1].startswith(h) for h in _EMU_HEAVY):
+            item.add_marker(skip)
 
 
 @pytest.fixture(scope="session")

@@ -1,0 +1,194 @@
+// CPU emulation of the subset of HIP used by wxx_amd/csrc/*.hip.
+//
+// TEST INFRASTRUCTURE ONLY: it lets the unchanged kernel sources build as
+// ordinary C++ (clang++ -fsanitize=address) so that every global-memory
+// access of every kernel is bounds-checked on the CPU before a kernel ever
+// runs on a GPU.  It is never used by the product library.
+//
+// Execution model: a launch runs its workgroups one after another; each
+// workgroup runs blockDim OS threads.  __syncthreads is a barrier over the
+// workgroup's live threads, __shfl_xor / MFMA exchange through a per-wave
+// slot array guarded by a barrier over the wave's live lanes.  A thread that
+// returns early leaves both barriers (the GPU equivalent: an exited wave no
+// longer counts for s_barrier).  __shared__ becomes static storage, which is
+// safe because workgroups do not overlap in time.
+#pragma once
+#include <cmath>
+#include <condition_variable>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <mutex>
+#include <thread>
+#include <vector>
+#include <algorithm>
+#include <chrono>
+
+#define __global__
+#define __device__
+#define __host__
+#define __forceinline__ inline
+#define __launch_bounds__(...)
+#define __shared__ static
+
+using std::max;
+using std::min;
+
+struct dim3 {
+  unsigned x, y, z;
+  dim3(unsigned a = 1, unsigned b = 1, unsigned c = 1) : x(a), y(b), z(c) {}
+};
+struct uint3_t { unsigned x, y, z; };
+
+struct float4 { float x, y, z, w; };
+inline float4 make_float4(float a, float b, float c, float d) { return float4{a, b, c, d}; }
+struct float2 { float x, y; };
+inline float2 make_float2(float a, float b) { return float2{a, b}; }
+
+namespace wxx_emu {
+extern thread_local uint3_t tl_thread, tl_block;
+extern dim3 g_block_dim, g_grid_dim;
+
+struct Barrier {
+  std::mutex mu;
+  std::condition_variable cv;
+  int expected = 0, arrived = 0;
+  unsigned long gen = 0;
+  void reset(int n) { std::lock_guard<std::mutex> l(mu); expected = n; arrived = 0; }
+  void wait() {
+    std::unique_lock<std::mutex> l(mu);
+    const unsigned long g = gen;
+    if (++arrived >= expected) { arrived = 0; ++gen; cv.notify_all(); return; }
+    cv.wait(l, [&] { return gen != g; });
+  }
+  void leave() {
+    std::lock_guard<std::mutex> l(mu);
+    --expected;
+    if (arrived >= expected && expected >= 0 && arrived > 0) { arrived = 0; ++gen; cv.notify_all(); }
+  }
+};
+
+struct Launch {
+  Barrier block;
+  Barrier wave[16];
+  uint64_t slot[1024][18];  // per-lane exchange: value + MFMA operands
+};
+extern Launch* g_launch;
+
+inline int lane() { return (int)(tl_thread.x + g_block_dim.x * (tl_thread.y + g_block_dim.y * tl_thread.z)) & 63; }
+inline int flat_tid() { return (int)(tl_thread.x + g_block_dim.x * (tl_thread.y + g_block_dim.y * tl_thread.z)); }
+inline int wave_id() { return flat_tid() >> 6; }
+
+void run(const std::function<void()>& body, dim3 grid, dim3 block);
+}  // namespace wxx_emu
+
+#define threadIdx (wxx_emu::tl_thread)
+#define blockIdx (wxx_emu::tl_block)
+#define blockDim (wxx_emu::g_block_dim)
+#define gridDim (wxx_emu::g_grid_dim)
+
+inline void __syncthreads() { wxx_emu::g_launch->block.wait(); }
+
+template <typename T>
+inline T __shfl_xor(T v, int off, int width = 64) {
+  static_assert(sizeof(T) <= 8, "shuffle of a value wider than 8 bytes");
+  auto* L = wxx_emu::g_launch;
+  const int t = wxx_emu::flat_tid(), w = t >> 6, ln = t & 63;
+  uint64_t bits = 0;
+  std::memcpy(&bits, &v, sizeof(T));
+  L->slot[t][0] = bits;
+  L->wave[w].wait();
+  const int src = (w << 6) | ((ln ^ off) & (width - 1)) | (ln & ~(width - 1));
+  uint64_t got = L->slot[src][0];
+  L->wave[w].wait();
+  T r;
+  std::memcpy(&r, &got, sizeof(T));
+  return r;
+}
+
+inline float __int_as_float(int v) { float f; std::memcpy(&f, &v, 4); return f; }
+inline float __uint_as_float(uint32_t v) { float f; std::memcpy(&f, &v, 4); return f; }
+inline int __float_as_int(float f) { int v; std::memcpy(&v, &f, 4); return v; }
+inline uint32_t __float_as_uint(float f) { uint32_t v; std::memcpy(&v, &f, 4); return v; }
+inline float rsqrtf(float x) { return 1.0f / std::sqrt(x); }
+inline float __expf(float x) { return std::exp(x); }
+
+typedef float wxx_floatx16 __attribute__((ext_vector_type(16)));
+
+// v_mfma_f32_32x32x2f32: A[i][k] from lane i + 32k, B[k][j] from lane j + 32k,
+// D[i][j] in lane j + 32*((i/4)%2), register (i%4) + 4*(i/8).
+// Device atomics: blocks run one at a time but their threads run
+// concurrently, so these use real host atomics.
+template <class T>
+inline T atomicAdd(T* p, T v) {
+  return __atomic_fetch_add(p, v, __ATOMIC_SEQ_CST);
+}
+inline float atomicAdd(float* p, float v) {
+  float old, want;
+  __atomic_load(p, &old, __ATOMIC_SEQ_CST);
+  do {
+    want = old + v;
+  } while (!__atomic_compare_exchange(p, &old, &want, false, __ATOMIC_SEQ_CST, __ATOMIC_SEQ_CST));
+  return old;
+}
+
+inline wxx_floatx16 __builtin_amdgcn_mfma_f32_32x32x2f32(float a, float b, wxx_floatx16 c, int, int, int) {
+  auto* L = wxx_emu::g_launch;
+  const int t = wxx_emu::flat_tid(), w = t >> 6, ln = t & 63;
+  uint64_t ab = 0;
+  std::memcpy(&ab, &a, 4);
+  std::memcpy(reinterpret_cast<char*>(&ab) + 4, &b, 4);
+  L->slot[t][1] = ab;
+  L->wave[w].wait();
+  wxx_floatx16 d = c;
+  const int j = ln & 31;
+  for (int r = 0; r < 16; ++r) {
+    const int i = 8 * (r / 4) + 4 * (ln / 32) + (r % 4);
+    float acc = 0.f;
+    for (int k = 0; k < 2; ++k) {
+      float av, bv;
+      uint64_t sa = L->slot[(w << 6) + i + 32 * k][1], sb = L->slot[(w << 6) + j + 32 * k][1];
+      std::memcpy(&av, &sa, 4);
+      std::memcpy(&bv, reinterpret_cast<char*>(&sb) + 4, 4);
+      acc += av * bv;
+    }
+    d[r] += acc;
+  }
+  L->wave[w].wait();
+  return d;
+}
+
+// ---------------------------------------------------------------- runtime API
+typedef int hipError_t;
+enum { hipSuccess = 0, hipErrorMemoryAllocation = 2 };
+typedef void* hipStream_t;
+typedef void* hipEvent_t;
+enum hipMemcpyKind { hipMemcpyHostToDevice, hipMemcpyDeviceToHost, hipMemcpyDeviceToDevice,
+                     hipMemcpyHostToHost, hipMemcpyDefault };
+#define hipStreamNonBlocking 1
+#define hipEventDisableTiming 2
+#define hipHostMallocDefault 0
+struct hipDeviceProp_t { char name[256]; char gcnArchName[256]; int multiProcessorCount; size_t totalGlobalMem; };
+
+hipError_t hipGetDeviceCount(int* n);
+hipError_t hipSetDevice(int d);
+hipError_t hipGetDeviceProperties(hipDeviceProp_t* p, int d);
+hipError_t hipStreamCreateWithFlags(hipStream_t* s, unsigned f);
+hipError_t hipStreamSynchronize(hipStream_t s);
+hipError_t hipMalloc(void** p, size_t n);
+hipError_t hipFree(void* p);
+hipError_t hipHostMalloc(void** p, size_t n, unsigned f);
+hipError_t hipMemcpy(void* d, const void* s, size_t n, hipMemcpyKind k);
+hipError_t hipMemcpyAsync(void* d, const void* s, size_t n, hipMemcpyKind k, hipStream_t st);
+hipError_t hipEventCreate(hipEvent_t* e);
+hipError_t hipEventCreateWithFlags(hipEvent_t* e, unsigned f);
+hipError_t hipEventRecord(hipEvent_t e, hipStream_t s);
+hipError_t hipEventSynchronize(hipEvent_t e);
+hipError_t hipEventElapsedTime(float* ms, hipEvent_t a, hipEvent_t b);
+hipError_t hipGetLastError();
+const char* hipGetErrorString(hipError_t e);
+
+#define hipLaunchKernelGGL(KERNEL, GRID, BLOCK, SHMEM, STREAM, ...) \
+  wxx_emu::run([&]() { KERNEL(__VA_ARGS__); }, dim3(GRID), dim3(BLOCK))

@@ -138,3 +138,16 @@ def test_assign_and_scatter_and_unfold(device):
         for w in range(size):
             ref[:, l * step + w, :] += dy[:, l, :, w]
     assert_close(dx, ref, atol=1e-6)
+
+
+@pytest.mark.parametrize("name", ["relu", "gelu", "sigmoid", "selu", "sin", "cos"])
+def test_unary_backward_is_derivative_times_grad(device, name):
+    from wxx_amd.functional import activations as fa
+
+    x = (rng(18).standard_normal(4099) * 4).astype(np.float32)
+    g = rng(19).standard_normal(4099).astype(np.float32)
+    src = oa.sigmoid(x) if name == "sigmoid" else x
+    got = fa.unary_backward(up(src), up(g), name).numpy()
+    deriv = {"relu": "relubackwards", "gelu": "gelubackwards", "sigmoid": "sigmoidbackwards",
+             "selu": "selubackwards", "sin": "sinback", "cos": "cosback"}[name]
+    assert_close(got, oa.UNARY[deriv](src) * g, rtol=4e-6, atol=2e-6)

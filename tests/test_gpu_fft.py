@@ -1,0 +1,181 @@
+"""GPU parity: rfft / irfft and the complex ops vs the oracle.
+
+Tolerance.  The reference computes the transform in float32 (radix-2, f32
+twiddles), so per-bin errors scale with the row's largest bin, not with the
+bin itself: a near-zero bin of a 16384-point transform carries an absolute
+error of ~1e-5 in any float32 FFT.  The bar is therefore the north-star
+rtol 1e-4 / atol 1e-5 applied against the row's scale:
+``|got - want| <= 1e-5 + 1e-4 * max|want_row|`` per element, where ``want``
+is the float64 closed form.  The same test also checks that the error is no
+worse than 4x the reference's own float32 arithmetic (oracle.fft.*_radix2_f32)
+where that restatement is cheap enough to run.
+"""
+
+import numpy as np
+import pytest
+
+from conftest import rng
+from oracle import fft as of
+
+pytestmark = pytest.mark.gpu
+
+
+def F():
+    from wxx_amd import functional
+
+    return functional
+
+
+def up(a):
+    return F().from_numpy(np.asarray(a, np.float32))
+
+
+def upc(a):
+    return F().from_numpy_complex(np.asarray(a))
+
+
+def assert_fft_close(got, want, msg=""):
+    got = np.asarray(got)
+    want = np.asarray(want)
+    assert got.shape == want.shape, f"{msg} shape {got.shape} != {want.shape}"
+    scale = np.abs(want).reshape(-1, want.shape[-1]).max(axis=-1) if want.size else np.zeros(0)
+    scale = scale.reshape(want.shape[:-1] + (1,))
+    err = np.abs(got.astype(np.complex128) - want)
+    bound = 1e-5 + 1e-4 * scale
+    if not (err <= bound).all():
+        worst = (err / bound).max()
+        raise AssertionError(f"{msg} error {worst:.3g}x the bound (max abs err {err.max():.3g})")
+    return err
+
+
+# (rows shape, in_len, n): n = 1 .. 32768, padding (in_len < n), truncation
+# (in_len > n), odd in_len (scalar loads), ragged row counts.
+RFFT_CASES = [
+    ((3,), 1, 1), ((2,), 5, 1), ((4,), 2, 2), ((5,), 3, 4), ((7,), 8, 8), ((3,), 16, 16),
+    ((2, 3), 32, 32), ((9,), 64, 64), ((5,), 100, 128), ((3,), 300, 256), ((6,), 512, 512),
+    ((4,), 1024, 1024), ((3,), 1500, 2048), ((2,), 4096, 4096), ((3,), 8191, 8192),
+    ((2, 2), 8192, 16384), ((3,), 16384, 16384), ((2,), 20000, 32768), ((2,), 33000, 32768),
+]
+
+
+@pytest.mark.parametrize("rows,in_len,n", RFFT_CASES)
+def test_rfft_matches_closed_form(device, rows, in_len, n):
+    x = rng(n + in_len).standard_normal(rows + (in_len,)).astype(np.float32)
+    X, n_out = F().rfft(up(x), n)
+    assert n_out == n and X.type == "c64"
+    got = X.numpy()
+    want = of.rfft(x, n)
+    err = assert_fft_close(got, want, f"rfft n={n}")
+    if 2 <= n <= 4096:
+        ref_err = np.abs(of.rfft_radix2_f32(x, n) - want)
+        scale = np.abs(want).max()
+        assert err.max() <= 4 * ref_err.max() + 1e-6 * scale
+
+
+IRFFT_CASES = [
+    ((3,), 2, 2), ((4,), 3, 4), ((2,), 2, 8), ((5,), 5, 8), ((3,), 9, 8), ((2, 3), 17, 32),
+    ((7,), 65, 128), ((3,), 100, 256), ((4,), 513, 1024), ((3,), 1025, 2048),
+    ((2,), 2049, 4096), ((3,), 4097, 8192), ((2, 2), 8193, 16384), ((2,), 6000, 16384),
+    ((2,), 16385, 32768),
+]
+
+
+@pytest.mark.parametrize("rows,in_len,n", IRFFT_CASES)
+def test_irfft_matches_closed_form(device, rows, in_len, n):
+    g = rng(3 * n + in_len)
+    X = (g.standard_normal(rows + (in_len,)) + 1j * g.standard_normal(rows + (in_len,)))
+    X = X.astype(np.complex64)
+    got = F().irfft(upc(X), n).numpy()
+    want = of.irfft(X, n)
+    assert got.shape == rows + (n,)
+    err = assert_fft_close(got, want, f"irfft n={n}")
+    if n <= 1024:
+        ref_err = np.abs(of.irfft_radix2_f32(X, n) - want)
+        assert err.max() <= 4 * ref_err.max() + 1e-6 * np.abs(want).max()
+
+
+def test_irfft_default_length_and_empty(device):
+    X = (rng(1).standard_normal((3, 9)) + 1j * rng(2).standard_normal((3, 9))).astype(np.complex64)
+    got = F().irfft(upc(X)).numpy()
+    assert got.shape == (3, 16)
+    assert_fft_close(got, of.irfft(X, 16))
+    empty = F().rfft(up(np.zeros((0, 8))), 8)[0]
+    assert tuple(empty.shape) == (0, 5)
+    assert F().irfft(upc(np.zeros((0, 5), np.complex64)), 8).numpy().shape == (0, 8)
+
+
+def test_rfft_rejects_bad_lengths(device):
+    with pytest.raises(ValueError):
+        F().rfft(up(np.zeros((2, 6))), 6)
+    with pytest.raises(ValueError):
+        F().irfft(upc(np.zeros((2, 5), np.complex64)), 1)
+
+
+def test_rfft_strided_input(device):
+    x = rng(4).standard_normal((64, 6)).astype(np.float32)
+    t = F().permute(up(x), 1, 0)
+    assert not t.is_contiguous()
+    assert_fft_close(F().rfft(t, 64)[0].numpy(), of.rfft(x.T, 64))
+
+
+def test_fft_full_size_properties(device):
+    # Standalone config: [2048 x 16384] f32.  Whole-size checks that do not
+    # need the float64 oracle on every row: round trip, Parseval, linearity,
+    # plus the closed form on a sample of rows.
+    x = rng(5).standard_normal((2048, 16384)).astype(np.float32)
+    tx = up(x)
+    X, _ = F().rfft(tx, 16384)
+    back = F().irfft(X, 16384).numpy()
+    assert np.abs(back - x).max() < 2e-5 * np.abs(x).max() * 10
+    Xh = X.numpy()
+    energy = (np.abs(Xh[:, 0]) ** 2 + np.abs(Xh[:, -1]) ** 2
+              + 2 * (np.abs(Xh[:, 1:-1]) ** 2).sum(axis=1)) / 16384
+    np.testing.assert_allclose(energy, (x.astype(np.float64) ** 2).sum(axis=1), rtol=1e-5)
+    sample = [0, 1, 777, 2047]
+    assert_fft_close(Xh[sample], of.rfft(x[sample], 16384))
+    two = F().rfft(F().scalarpointwise(tx, 2.0, 2), 16384)[0].numpy()
+    assert_fft_close(two, 2 * Xh.astype(np.complex128))
+
+
+def test_hyena_shapes(device):
+    # Hyena fft_conv1d: x (8, 256, 8192) -> rfft(16384) -> (8, 256, 8193);
+    # here a 2-batch slice of it, checked on sampled rows.
+    x = rng(6).standard_normal((2, 256, 8192)).astype(np.float32)
+    X, n = F().rfft(up(x), 16384)
+    assert tuple(X.shape) == (2, 256, 8193) and n == 16384
+    Xh = X.numpy()
+    assert_fft_close(Xh[:, ::97], of.rfft(x[:, ::97], 16384))
+    y = F().irfft(X, 16384).numpy()
+    assert np.abs(y[..., :8192] - x).max() < 1e-4 and np.abs(y[..., 8192:]).max() < 1e-4
+
+
+@pytest.mark.parametrize("sa,sb", [((4, 9), (4, 9)), ((2, 3, 17), (3, 17)), ((5, 1), (1, 6)),
+                                   ((8, 256, 33), (256, 33))])
+@pytest.mark.parametrize("ca,cb", [(False, False), (True, False), (False, True)])
+def test_complex_mul_broadcast(device, sa, sb, ca, cb):
+    g = rng(7)
+    a = (g.standard_normal(sa) + 1j * g.standard_normal(sa)).astype(np.complex64)
+    b = (g.standard_normal(sb) + 1j * g.standard_normal(sb)).astype(np.complex64)
+    got = F().complex_mul(upc(a), upc(b), conj_a=ca, conj_b=cb).numpy()
+    want = of.complex_mul(a, b, ca, cb)
+    np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-6)
+
+
+def test_complex_support_ops(device):
+    g = rng(8)
+    a = (g.standard_normal((3, 10)) + 1j * g.standard_normal((3, 10))).astype(np.complex64)
+    b = (g.standard_normal((10,)) + 1j * g.standard_normal((10,))).astype(np.complex64)
+    ta = upc(a)
+    assert np.array_equal(F().complex_conj(ta).numpy(), np.conj(a))
+    assert np.array_equal(F().complex_pad(ta, 14).numpy(), of.complex_pad(a, 14))
+    assert np.array_equal(F().complex_pad(ta, 4).numpy(), of.complex_pad(a, 4))
+    np.testing.assert_allclose(F().complex_add(ta, upc(b)).numpy(), a + b, rtol=1e-6)
+    F().complex_add_inplace(ta, upc(b))
+    np.testing.assert_allclose(ta.numpy(), a + b, rtol=1e-6)
+    w = F().complex_weights([1.0, 0.5, 2.0]).numpy()
+    assert np.array_equal(w, np.array([1.0, 0.5, 2.0], np.complex64))
+    # strided complex view -> contiguous (bit exact)
+    t = upc(a)[:, ::3]
+    assert not t.is_contiguous()
+    assert np.array_equal(F().complex_contiguous(t).numpy(), a[:, ::3])
+    assert np.array_equal(F().complex_conj(t).numpy(), np.conj(a[:, ::3]))

@@ -60,19 +60,19 @@ def test_norm_zero_rows_and_row_cap(device):
     x[3] = 0.0
     g = rng(2).standard_normal(8).astype(np.float32)
     b = rng(3).standard_normal(8).astype(np.float32)
-    y, mu, inv = F().meanvarnorm(up(x), up(g), up(b))
+    y, mu, inv = F().meanvarnorm(up(x), up(g), up(b), axis=-1)
     assert inv.numpy()[3] == 0.0
     assert_close(y.numpy()[3], b)
     assert np.any(y.numpy()[65535:] != 0)  # default: every row computed
-    yr, rr = F().rmsnorm(up(x), up(g))
+    yr, rr = F().rmsnorm(up(x), up(g), axis=-1)
     assert rr.numpy()[3] == 0.0
     compat.REFERENCE_ROW_CAP = True
     try:
-        yc, muc, invc = F().meanvarnorm(up(x), up(g), up(b))
+        yc, muc, invc = F().meanvarnorm(up(x), up(g), up(b), axis=-1)
         ey, emu, einv = on.meanvarnorm(x, g, b, row_cap=65535)
         assert np.all(yc.numpy()[65535:] == 0) and np.all(invc.numpy()[65535:] == 0)
         assert_close(yc.numpy(), ey, atol=1e-4)
-        yrc, rrc = F().rmsnorm(up(x), up(g))
+        yrc, rrc = F().rmsnorm(up(x), up(g), axis=-1)
         assert np.all(yrc.numpy()[65535:] == 0) and np.all(rrc.numpy()[65535:] == 0)
     finally:
         compat.REFERENCE_ROW_CAP = False
@@ -125,3 +125,19 @@ def test_batchnorm(device, shape, training):
     assert_close(db.numpy(), edb, rtol=1e-4, atol=1e-5 * np.sqrt(n) * 10)
     dx = F().batchnormdx(up(dy), up(x), up(g), dg, db, mu, inv)
     assert_close(dx.numpy(), on.batchnormdx(dy, x, g, edg, edb, emu, einv), rtol=1e-3, atol=1e-4)
+
+
+def test_norm_parameter_size_is_validated(device):
+    # gamma/beta are indexed by the reduce coordinate: a mismatch must be
+    # rejected on the host, never read out of bounds on the device
+    x = up(rng(4).standard_normal((16, 8)))
+    g8 = up(np.ones(8))
+    with pytest.raises(ValueError):
+        F().meanvarnorm(x, g8, g8)          # axis=None normalises all 128 elements
+    with pytest.raises(ValueError):
+        F().rmsnorm(x, g8)
+    with pytest.raises(ValueError):
+        F().meanvarnorm(x, up(np.ones(7)), g8, axis=-1)
+    with pytest.raises(ValueError):
+        F().batchnorm(up(np.ones((2, 3, 2, 2))), up(np.ones(2)), up(np.ones(3)), up(np.ones(3)),
+                      up(np.ones(3)), training=True)

@@ -111,3 +111,22 @@ def test_softmax_masked_rows(device):
     got = F().softmax(up(x), -1).numpy()
     assert_close(got, oa.softmax(x, -1))
     assert np.all(got[:, 10:] == 0)
+
+
+@pytest.mark.parametrize("shape,dim", [((5, 7), -1), ((64, 1024), -1), ((8, 12, 33, 129), -1),
+                                       ((4, 50257), -1), ((6, 5, 9), 1), ((3, 70000), -1)])
+def test_softmax_backward(device, shape, dim):
+    r = rng(21)
+    y = oa.softmax(r.standard_normal(shape).astype(np.float32) * 2, dim)
+    g = r.standard_normal(shape).astype(np.float32)
+    got = F().softmax_backward(up(y), up(g), dim).numpy()
+    assert_close(got, oa.softmax_backward(y, g, dim), rtol=1e-4, atol=1e-6)
+
+
+@pytest.mark.parametrize("src,shape,scale", [((1, 1), (4, 5), 1.0), ((4, 1), (4, 5), 0.25),
+                                             ((1, 5), (4, 5), 2.0), ((3, 1, 6), (3, 4, 6), 1.0),
+                                             ((1,), (1000,), 0.001)])
+def test_broadcast_to(device, src, shape, scale):
+    g = rng(22).standard_normal(src).astype(np.float32)
+    got = F().broadcast_to(up(g), shape, scale).numpy()
+    assert np.array_equal(got, (np.broadcast_to(g, shape) * np.float32(scale)).astype(np.float32))

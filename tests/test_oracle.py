@@ -381,3 +381,89 @@ def test_clamp_equal_fill():
     assert np.array_equal(oe.masked_fill(x, -9.0), np.array([-2, -0.5, -9, 0.5, 2], np.float32))
     assert np.array_equal(oe.equal(x, 0.5), (x == 0.5).astype(np.float32))
     assert math.isclose(float(oe.mul_backward(x, x, 2 * x)[0][0]), 8.0)
+
+
+# ---------------------------------------------------------------------- FFT
+from oracle import fft as of  # noqa: E402
+
+
+def _dft_brute(x, n):
+    """Definition of the DFT with explicit loops, after the reference's
+    zero-pad / truncate of each row (fft_bitrev_real.wgsl:39-51)."""
+    x = np.asarray(x, np.float64)
+    rows = x.reshape(-1, x.shape[-1])
+    out = np.zeros((rows.shape[0], n // 2 + 1), np.complex128)
+    for r in range(rows.shape[0]):
+        xr = [rows[r, j] if j < rows.shape[1] else 0.0 for j in range(n)]
+        for k in range(n // 2 + 1):
+            out[r, k] = sum(xr[j] * complex(math.cos(2 * math.pi * j * k / n),
+                                            -math.sin(2 * math.pi * j * k / n))
+                            for j in range(n))
+    return out.reshape(x.shape[:-1] + (n // 2 + 1,))
+
+
+def _idft_brute(X, n):
+    """The reference's inverse taken literally: Hermitian expansion with the
+    mirror rule of fft_bitrev_complex.wgsl:41-53, full complex inverse DFT,
+    real part times 1/n (ifft_write_real.wgsl:25-28)."""
+    X = np.asarray(X, np.complex128)
+    rows = X.reshape(-1, X.shape[-1])
+    in_len = rows.shape[1]
+    out = np.zeros((rows.shape[0], n))
+    for r in range(rows.shape[0]):
+        full = []
+        for i in range(n):
+            if i <= n // 2:
+                full.append(rows[r, i] if i < in_len else 0j)
+            else:
+                m = n - i
+                full.append(np.conj(rows[r, m]) if m < in_len else 0j)
+        for j in range(n):
+            acc = sum(full[k] * complex(math.cos(2 * math.pi * j * k / n),
+                                        math.sin(2 * math.pi * j * k / n)) for k in range(n))
+            out[r, j] = acc.real / n
+    return out.reshape(X.shape[:-1] + (n,))
+
+
+@pytest.mark.parametrize("n,in_len", [(1, 1), (1, 3), (2, 2), (4, 3), (8, 8), (8, 11), (16, 5)])
+def test_rfft_oracle_matches_brute_force_dft(n, in_len):
+    x = rng(n * 31 + in_len).standard_normal((3, in_len))
+    np.testing.assert_allclose(of.rfft(x, n), _dft_brute(x, n), atol=1e-9)
+
+
+@pytest.mark.parametrize("n,in_len", [(2, 2), (4, 3), (8, 5), (8, 2), (8, 9), (16, 9)])
+def test_irfft_oracle_matches_literal_hermitian_inverse(n, in_len):
+    g = rng(n * 7 + in_len)
+    X = g.standard_normal((2, in_len)) + 1j * g.standard_normal((2, in_len))
+    # non-zero imaginary DC / Nyquist parts are part of the check
+    np.testing.assert_allclose(of.irfft(X, n), _idft_brute(X, n), atol=1e-9)
+
+
+def test_fft_identities():
+    g = rng(5)
+    x = g.standard_normal((4, 64))
+    X = of.rfft(x)
+    # round trip, Parseval (one-sided form), delta -> flat, linearity
+    np.testing.assert_allclose(of.irfft(X, 64), x, atol=1e-12)
+    energy = (np.abs(X[:, 0]) ** 2 + np.abs(X[:, -1]) ** 2
+              + 2 * (np.abs(X[:, 1:-1]) ** 2).sum(axis=1)) / 64
+    np.testing.assert_allclose(energy, (x ** 2).sum(axis=1), rtol=1e-12)
+    delta = np.zeros((1, 32))
+    delta[0, 0] = 1
+    np.testing.assert_allclose(of.rfft(delta), np.ones((1, 17)), atol=1e-12)
+    y = g.standard_normal((4, 64))
+    np.testing.assert_allclose(of.rfft(2 * x - y), 2 * X - of.rfft(y), atol=1e-10)
+
+
+@pytest.mark.parametrize("n", [2, 8, 256, 2048])
+def test_reference_float32_arithmetic_error_is_small(n):
+    # The reference's own f32 radix-2 result sits within ~1e-6 of the closed
+    # form (relative to the row's largest bin), which sizes the tolerance the
+    # HIP kernels are held to.
+    x = rng(n).standard_normal((3, n)).astype(np.float32)
+    want = of.rfft(x)
+    got = of.rfft_radix2_f32(x)
+    scale = np.abs(want).max(axis=-1, keepdims=True)
+    assert (np.abs(got - want) / scale).max() < 2e-6
+    back = of.irfft_radix2_f32(want.astype(np.complex64), n)
+    np.testing.assert_allclose(back, x, atol=2e-6 * np.abs(x).max())

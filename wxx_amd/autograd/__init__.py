@@ -1,0 +1,53 @@
+"""Differentiable ops recorded into a reverse-mode graph (the surface of
+reference src/wxx/autograd/__init__.py:1-128)."""
+
+from .function import Function
+from .layers import CrossEntropyLoss, Dropout, Embedding
+from .normalization import batchnorm, meanvarnorm, rmsnorm
+from .pointwise import (
+    abs,
+    add,
+    addscaler,
+    clamp,
+    cos,
+    decay_window,
+    div,
+    exp,
+    gelu,
+    log,
+    mul,
+    mulscaler,
+    negate,
+    powscaler,
+    rdivscaler,
+    relu,
+    rpowscaler,
+    rsqrt,
+    selu,
+    sigmoid,
+    sign,
+    sin,
+    sqrt,
+    square,
+    sub,
+    subscaler,
+)
+from .reductions import argmax, argmin, max, mean, min, softmax, std, sum, var
+from .utils import (
+    complex_conj,
+    complex_mul,
+    concat,
+    diagonal,
+    flatten,
+    getitem,
+    irfft,
+    matmul,
+    matmuladd,
+    narrow,
+    permute,
+    reshape,
+    rfft,
+    squeeze,
+    unfold,
+    unsqueeze,
+)

@@ -115,15 +115,19 @@ class DeviceBufferPool:
         return buf
 
     def create_buffer_with_data(self, data, usage=None, label=None):
-        mv = memoryview(data).cast("B")
-        if mv.nbytes % 4:
+        if isinstance(data, np.ndarray):
+            arr = np.ascontiguousarray(data).reshape(-1).view(np.uint8)
+        else:
+            arr = np.frombuffer(memoryview(data).tobytes() if not isinstance(data, bytes) else data,
+                                dtype=np.uint8)
+        nbytes = int(arr.nbytes)
+        if nbytes % 4:
             raise ValueError("device buffer data size must be a multiple of 4 bytes")
         caller = sys._getframe(1).f_code.co_name
         label = caller if label is None else f"{caller}: {label}"
-        buf = self.create_buffer(mv.nbytes, usage, label=label)
-        if mv.nbytes:
-            arr = np.frombuffer(mv, dtype=np.uint8)
-            _lib.call("wxx_h2d", C.c_void_p(buf.ptr), arr.ctypes.data_as(C.c_void_p), mv.nbytes)
+        buf = self.create_buffer(nbytes, usage, label=label)
+        if nbytes:
+            _lib.call("wxx_h2d", C.c_void_p(buf.ptr), arr.ctypes.data_as(C.c_void_p), nbytes)
         return buf
 
     def release(self, buffer):

@@ -50,6 +50,7 @@ SIGNATURES = {
     "wxx_reduce_minmax": (I32, [P, P, P, I64, I64, I64, I32]),
     "wxx_maxmin_backward": (I32, [P, P, P, I64, I64, I64]),
     "wxx_softmax": (I32, [P, P, I64, I64, I64]),
+    "wxx_softmax_backward": (I32, [P, P, P, I64, I64, I64]),
     # normalisation
     "wxx_meanvarnorm": (I32, [P, P, P, P, P, P, I64, I64, I64, F32, I64]),
     "wxx_meanvarnormdx": (I32, [P, P, P, P, P, P, I64, I64, I64, I64]),
@@ -64,6 +65,8 @@ SIGNATURES = {
     "wxx_pointwise": (I32, [P, P, P, I32, P, P, P, P, I32]),
     "wxx_scalarpointwise": (I32, [P, P, I64, I32, F32, I32]),
     "wxx_unary": (I32, [P, P, I64, I32]),
+    "wxx_unary_backward": (I32, [P, P, P, I64, I32]),
+    "wxx_broadcast_scale": (I32, [P, P, I32, P, P, F32]),
     "wxx_clamp": (I32, [P, P, I64, F32, F32, I32]),
     "wxx_equal": (I32, [P, P, P, I64, I32, U32]),
     "wxx_mul_backward": (I32, [P, P, P, P, P, I64]),
@@ -71,6 +74,25 @@ SIGNATURES = {
     "wxx_fill_strided": (I32, [P, I32, P, P, U32]),
     "wxx_scatter_zeros": (I32, [P, P, I32, P, P, I32, I64, I64]),
     "wxx_unfolddx": (I32, [P, P, I64, I64, I64, I64, I64, I64]),
+    # FFT / complex
+    "wxx_rfft": (I32, [P, P, I64, I64, I64]),
+    "wxx_irfft": (I32, [P, P, I64, I64, I64]),
+    "wxx_complex_binary": (I32, [P, P, P, I32, P, P, P, P, I32, I32, I32]),
+    "wxx_complex_conj": (I32, [P, P, I32, P, P, P]),
+    "wxx_complex_pad": (I32, [P, P, I64, I64, I64]),
+    # loss
+    "wxx_cceloss": (I32, [P, P, P, P, I64, I64, P]),
+    # optimizer / grad norm
+    "wxx_adamw": (I32, [P, P, P, P, I64, F32, F32, F32, F32, F32, F32, F32]),
+    "wxx_adamw_multi": (I32, [P, P, P, P, P, I32, F32, F32, F32, F32, F32, F32, F32]),
+    "wxx_sumsq_multi": (I32, [P, P, I32, P]),
+    "wxx_scale_multi": (I32, [P, P, I32, F32]),
+    # embedding / dropout / decay window
+    "wxx_embed": (I32, [P, P, P, I64, I64, I64]),
+    "wxx_embeddx": (I32, [P, P, P, I64, I64, I64]),
+    "wxx_dropout": (I32, [P, P, I64, U32, F32, F32]),
+    "wxx_decay_window": (I32, [P, P, I64, I64, I64, I64]),
+    "wxx_decay_window_backward": (I32, [P, P, P, I64, I64, I64, I64]),
 }
 
 _lib = None

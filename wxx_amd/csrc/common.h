@@ -17,6 +17,9 @@
 #define WXX_API extern "C" __attribute__((visibility("default")))
 
 WXX_API int wxx_fill_u32(void* dst, int64_t n, uint32_t bits);
+WXX_API int wxx_h2d(void* dst, const void* src, size_t bytes);
+WXX_API void* wxx_alloc(size_t bytes);
+WXX_API int wxx_free(void* ptr);
 
 enum {
   WXX_OK = 0,

@@ -19,83 +19,17 @@
 // accesses.  Index arithmetic is 32-bit whenever the tensor has fewer than
 // 2^31 elements.
 #include "common.h"
+#include "nd.h"
 
 #include <cmath>
 
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kMaxOps = 3;
-
-struct ND {
-  int rank;
-  int64_t shape[wxx::kMaxRank];
-  int64_t stride[kMaxOps][wxx::kMaxRank];
-};
-
-// Merge dimensions that are contiguous in every operand, drop size-1 dims.
-ND collapse(int rank, const int64_t* shape, const int64_t* const* strides, int nops) {
-  ND r;
-  r.rank = 0;
-  for (int d = 0; d < rank; ++d) {
-    if (shape[d] == 1) continue;
-    if (r.rank > 0) {
-      const int p = r.rank - 1;
-      bool merge = true;
-      for (int o = 0; o < nops; ++o)
-        if (r.stride[o][p] != strides[o][d] * shape[d]) merge = false;
-      if (merge) {
-        r.shape[p] *= shape[d];
-        for (int o = 0; o < nops; ++o) r.stride[o][p] = strides[o][d];
-        continue;
-      }
-    }
-    r.shape[r.rank] = shape[d];
-    for (int o = 0; o < nops; ++o) r.stride[o][r.rank] = strides[o][d];
-    ++r.rank;
-  }
-  if (r.rank == 0) {
-    r.rank = 1;
-    r.shape[0] = 1;
-    for (int o = 0; o < nops; ++o) r.stride[o][0] = 0;
-  }
-  return r;
-}
-
-template <int NOPS>
-__device__ __forceinline__ void offsets(const ND& nd, int64_t idx, int64_t* off) {
-#pragma unroll
-  for (int o = 0; o < NOPS; ++o) off[o] = 0;
-  if (nd.rank == 1) {
-#pragma unroll
-    for (int o = 0; o < NOPS; ++o) off[o] = idx * nd.stride[o][0];
-    return;
-  }
-  // 32-bit decomposition when possible (AMD has no hardware 64-bit divide).
-  uint32_t rem = (uint32_t)idx;
-  for (int d = nd.rank - 1; d >= 0; --d) {
-    const uint32_t n = (uint32_t)nd.shape[d];
-    const uint32_t q = rem / n;
-    const uint32_t c = rem - q * n;
-    rem = q;
-#pragma unroll
-    for (int o = 0; o < NOPS; ++o) off[o] += (int64_t)c * nd.stride[o][d];
-  }
-}
-
-template <int NOPS>
-__device__ __forceinline__ void offsets64(const ND& nd, int64_t idx, int64_t* off) {
-#pragma unroll
-  for (int o = 0; o < NOPS; ++o) off[o] = 0;
-  for (int d = nd.rank - 1; d >= 0; --d) {
-    const int64_t n = nd.shape[d];
-    const int64_t q = idx / n;
-    const int64_t c = idx - q * n;
-    idx = q;
-#pragma unroll
-    for (int o = 0; o < NOPS; ++o) off[o] += c * nd.stride[o][d];
-  }
-}
+using wxx::ND;
+using wxx::collapse;
+using wxx::offsets;
+using wxx::offsets64;
 
 // ---- binary ----------------------------------------------------------------
 __device__ __forceinline__ float binop(int op, float a, float b) {
@@ -229,6 +163,40 @@ __global__ __launch_bounds__(kBlock) void unary_kernel(const float* __restrict__
                         unary_op(OP, v.w));
   }
   for (int64_t i = (n4 << 2) + t; i < n; i += step) y[i] = unary_op(OP, x[i]);
+}
+
+// out = f'(x) * g with f' given by a derivative op code (bit-identical to
+// computing the derivative tensor and multiplying it by g).
+template <int OP>
+__global__ __launch_bounds__(kBlock) void unary_bwd_kernel(const float* __restrict__ x,
+                                                           const float* __restrict__ g,
+                                                           float* __restrict__ y, int64_t n,
+                                                           int vec) {
+  const int64_t n4 = vec ? n >> 2 : 0;
+  const int64_t step = (int64_t)gridDim.x * kBlock;
+  const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  const float4* g4 = reinterpret_cast<const float4*>(g);
+  float4* y4 = reinterpret_cast<float4*>(y);
+  for (int64_t i = t; i < n4; i += step) {
+    const float4 v = x4[i], w = g4[i];
+    y4[i] = make_float4(unary_op(OP, v.x) * w.x, unary_op(OP, v.y) * w.y,
+                        unary_op(OP, v.z) * w.z, unary_op(OP, v.w) * w.w);
+  }
+  for (int64_t i = (n4 << 2) + t; i < n; i += step) y[i] = unary_op(OP, x[i]) * g[i];
+}
+
+// dst[i] = src[offset(i)] * scale for a dense dst over `shape` (broadcast read).
+__global__ __launch_bounds__(kBlock) void broadcast_scale_kernel(float* __restrict__ dst,
+                                                                 const float* __restrict__ src,
+                                                                 ND nd, int64_t n, float scale) {
+  int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t step = (int64_t)gridDim.x * kBlock;
+  for (; i < n; i += step) {
+    int64_t off[2];
+    offsets64<2>(nd, i, off);
+    dst[off[0]] = src[off[1]] * scale;
+  }
 }
 
 __global__ __launch_bounds__(kBlock) void scalar_kernel(const float* __restrict__ x,
@@ -497,6 +465,54 @@ WXX_API int wxx_unary(const float* x, float* y, int64_t n, int op) {
     default: break;
   }
 #undef WXX_UCASE
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// Fused local derivative times gradient: out = f'(x) * g, where op is the
+// derivative's Unary code (relu', gelu', sigmoid' (from y), selu', sin',
+// cos').  Replaces the derivative kernel + pointwise multiply pair that the
+// reference's activation backwards issue (reference
+// src/wxx/autograd/pointwise.py:291-388).
+WXX_API int wxx_unary_backward(const float* x, const float* g, float* y, int64_t n, int op) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(x && g && y, "null pointer");
+  WXX_REQUIRE(op >= 0 && op < U_COUNT, "bad unary op %d", op);
+  if (n <= 0) return WXX_OK;
+  const int vec = ((uintptr_t)x | (uintptr_t)g | (uintptr_t)y) % 16 == 0;
+  dim3 grid(grid_for((n + 3) / 4));
+  hipStream_t s = wxx::stream();
+#define WXX_UBCASE(OP) \
+  case OP: hipLaunchKernelGGL(unary_bwd_kernel<OP>, grid, dim3(kBlock), 0, s, x, g, y, n, vec); break;
+  switch (op) {
+    WXX_UBCASE(U_RELU_BWD) WXX_UBCASE(U_GELU_BWD) WXX_UBCASE(U_SIGMOID_BWD)
+    WXX_UBCASE(U_SELU_BWD) WXX_UBCASE(U_SIN_BWD) WXX_UBCASE(U_COS_BWD)
+    default: return wxx::set_error(WXX_E_ARG, "op %d is not a derivative op", op);
+  }
+#undef WXX_UBCASE
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// dst (dense over `shape`) = src read through s_src (0 = broadcast) * scale.
+// Replaces the ones_like * grad products of sum/mean backward (reference
+// src/wxx/autograd/reductions.py:38-95).
+WXX_API int wxx_broadcast_scale(float* dst, const float* src, int rank, const int64_t* shape,
+                                const int64_t* s_src, float scale) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(dst && src && shape && s_src, "null pointer");
+  WXX_REQUIRE(rank >= 0 && rank <= wxx::kMaxRank, "rank %d unsupported", rank);
+  int64_t n = 1;
+  int64_t dense[wxx::kMaxRank];
+  for (int d = rank - 1; d >= 0; --d) {
+    dense[d] = n;
+    n *= shape[d];
+  }
+  if (n == 0) return WXX_OK;
+  const int64_t* ss[2] = {dense, s_src};
+  ND nd = collapse(rank, shape, ss, 2);
+  hipLaunchKernelGGL(broadcast_scale_kernel, dim3(grid_for(n)), dim3(kBlock), 0, wxx::stream(),
+                     dst, src, nd, n, scale);
   WXX_LAUNCHED();
   return WXX_OK;
 }

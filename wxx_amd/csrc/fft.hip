@@ -1,0 +1,519 @@
+// Real FFT / inverse real FFT along the last dimension, and the complex
+// support kernels (multiply, add, conjugate, pad) of the spectral path.
+//
+// Reference: src/wxx/functional/fft.py:386-645 (rfft / irfft hosts) with
+// shaders/helpers/fft_wg_real.wgsl, fft_wg_inverse.wgsl (n <= 1024, one
+// workgroup per row) and fft_bitrev_real / fft_stage / fft_copy_out /
+// fft_bitrev_complex / ifft_write_real (n > 1024: 1 + log2(n) + 1 launches,
+// each a full HBM pass); complex helpers fft.py:168-383.
+//
+// MI355X design.  A length-n real transform is computed as one length
+// M = n/2 complex transform of z[m] = x[2m] + i x[2m+1] followed by the
+// standard even/odd untangling X[k] = E[k] + W_n^k O[k] (and the mirror image
+// of that for the inverse).  For n <= 32768 the M complex points of a row
+// (64 KiB at n = 16384) stay in LDS for the whole transform: one workgroup
+// per row reads the input from HBM once and writes the spectrum once.
+// Inside the workgroup the transform is a Stockham auto-sort FFT: every pass
+// loads 16 points per thread from LDS, applies the pass twiddles, does a
+// radix-16 (or radix-2/4/8 first pass) DFT in registers and writes the points
+// back in their next-pass order, so no bit reversal pass is needed.  The
+// first pass reads straight from HBM and, for the inverse, the last pass
+// writes straight to HBM (its output order is already natural).
+//
+// Twiddles come from a per-size table built once on the host in double
+// precision.  Pass p stores W_{Ns R}^{r k} at [(r-1) * Ns + k], so for a
+// fixed r consecutive lanes (consecutive k) load consecutive entries; the
+// untangling twiddles W_n^k, k <= M, follow.
+#include "common.h"
+#include "nd.h"
+
+#include <cmath>
+#include <map>
+#include <mutex>
+#include <vector>
+
+namespace {
+
+// ---- plan --------------------------------------------------------------
+// log2(M) bits are split into passes: the first pass takes log2(M) mod 4
+// bits (4 when that is 0), every later pass 4 bits (radix 16).
+struct Plan {
+  int logm;
+  __host__ __device__ constexpr int m() const { return 1 << logm; }
+  __host__ __device__ constexpr int ebits() const { return logm < 4 ? logm : 4; }
+  __host__ __device__ constexpr int first() const {
+    return logm % 4 == 0 ? ebits() : logm % 4;
+  }
+  __host__ __device__ constexpr int npass() const {
+    return logm == 0 ? 1 : (logm - first()) / 4 + 1;
+  }
+  __host__ __device__ constexpr int bits(int p) const { return p == 0 ? first() : 4; }
+  __host__ __device__ constexpr int ns_bits(int p) const {
+    return p == 0 ? 0 : first() + 4 * (p - 1);
+  }
+  // Twiddle entries stored for the passes before p (pass tables back to back).
+  __host__ __device__ constexpr int offset(int p) const {
+    int o = 0;
+    for (int q = 0; q < p; ++q) o += (1 << ns_bits(q)) * ((1 << bits(q)) - 1);
+    return o;
+  }
+  __host__ __device__ constexpr int table_size() const { return offset(npass()) + m() + 1; }
+};
+
+constexpr int kMaxLogM = 14;  // n <= 32768 stays resident in LDS
+
+template <int LOGM>
+struct Geo {
+  static constexpr Plan plan{LOGM};
+  static constexpr int M = 1 << LOGM;
+  static constexpr int E = 1 << plan.ebits();   // points per thread
+  static constexpr int T = M / E;               // threads per row
+  static constexpr int NT = T < 256 ? 256 : T;  // threads per block
+  static constexpr int RPB = NT / T;            // rows per block
+  static constexpr int PM = M + (M >> 4);       // padded LDS row (one pad slot per 16)
+};
+
+__device__ __forceinline__ int lds_pad(int i) { return i + (i >> 4); }
+
+__device__ __forceinline__ float2 cmul(float2 a, float2 b) {
+  return make_float2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
+}
+
+// cos(pi m / 8), m in [0, 16)
+__device__ constexpr float kCosPi8[16] = {
+    1.0f,  0.92387953251128674f,  0.70710678118654752f,  0.38268343236508977f,
+    0.0f,  -0.38268343236508977f, -0.70710678118654752f, -0.92387953251128674f,
+    -1.0f, -0.92387953251128674f, -0.70710678118654752f, -0.38268343236508977f,
+    0.0f,  0.38268343236508977f,  0.70710678118654752f,  0.92387953251128674f};
+
+// v * exp(-i pi m / 8) (forward) or v * exp(+i pi m / 8) (inverse); m is a
+// compile-time constant after unrolling, so the branches fold away.
+template <bool INV>
+__device__ __forceinline__ float2 rot(float2 v, int m) {
+  m &= 15;
+  if (m == 0) return v;
+  if (m == 8) return make_float2(-v.x, -v.y);
+  if (m == 4) return INV ? make_float2(-v.y, v.x) : make_float2(v.y, -v.x);
+  if (m == 12) return INV ? make_float2(v.y, -v.x) : make_float2(-v.y, v.x);
+  const float c = kCosPi8[m];
+  const float s = INV ? kCosPi8[(m + 12) & 15] : -kCosPi8[(m + 12) & 15];
+  return make_float2(v.x * c - v.y * s, v.x * s + v.y * c);
+}
+
+// In-register radix-2 decimation-in-frequency DFT of R <= 16 points; the
+// result is in bit-reversed order: X[k] = u[bitrev(k)].
+template <int R, bool INV>
+__device__ __forceinline__ void dft(float2* u) {
+  static_assert(R <= 16, "radix above 16 needs finer rotation constants");
+#pragma unroll
+  for (int s = R / 2; s >= 1; s >>= 1) {
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      if (j & s) continue;
+      const float2 a = u[j], b = u[j + s];
+      u[j] = make_float2(a.x + b.x, a.y + b.y);
+      u[j + s] = rot<INV>(make_float2(a.x - b.x, a.y - b.y), (j & (s - 1)) * (8 / s));
+    }
+  }
+}
+
+__host__ __device__ constexpr int bitrev(int x, int bits) {
+  int r = 0;
+  for (int i = 0; i < bits; ++i) {
+    r = (r << 1) | (x & 1);
+    x >>= 1;
+  }
+  return r;
+}
+
+// Twiddle + DFT of pass P on the E register points (E/R groups of R).
+template <int LOGM, int P, bool INV>
+__device__ __forceinline__ void pass_math(float2* v, int t, const float2* __restrict__ tw) {
+  using G = Geo<LOGM>;
+  constexpr Plan pl{LOGM};
+  constexpr int R = 1 << pl.bits(P), NS = 1 << pl.ns_bits(P);
+  constexpr int OFF = pl.offset(P);
+#pragma unroll
+  for (int q = 0; q < G::E / R; ++q) {
+    float2* u = v + q * R;
+    if constexpr (NS > 1) {
+      const int k = (t + q * G::T) & (NS - 1);
+#pragma unroll
+      for (int r = 1; r < R; ++r) {
+        float2 w = tw[OFF + (r - 1) * NS + k];
+        if (INV) w.y = -w.y;
+        u[r] = cmul(u[r], w);
+      }
+    }
+    dft<R, INV>(u);
+  }
+}
+
+// Passes P.. of the transform.  On entry v holds pass P's input points
+// (P == 0: loaded by the caller).  On exit the transform is in buf in natural
+// order (TO_GLOBAL false) or written to gout * scale (TO_GLOBAL true).
+template <int LOGM, int P, bool INV, bool TO_GLOBAL>
+__device__ __forceinline__ void run_passes(float2* v, float2* buf, int t,
+                                           const float2* __restrict__ tw, float2* gout,
+                                           float scale, bool live) {
+  using G = Geo<LOGM>;
+  constexpr Plan pl{LOGM};
+  constexpr int BITS = pl.bits(P), R = 1 << BITS, NSB = pl.ns_bits(P), NS = 1 << NSB;
+  constexpr int GR = G::M / R;  // groups per pass
+  if constexpr (P > 0) {
+#pragma unroll
+    for (int q = 0; q < G::E / R; ++q)
+#pragma unroll
+      for (int r = 0; r < R; ++r) v[q * R + r] = buf[lds_pad(t + q * G::T + r * GR)];
+  }
+  pass_math<LOGM, P, INV>(v, t, tw);
+  constexpr bool LAST = P + 1 == pl.npass();
+  if constexpr (LAST && TO_GLOBAL) {
+    // Last pass: NS == GR, so the output position of (group g, k) is g + k*GR.
+    if (live) {
+#pragma unroll
+      for (int q = 0; q < G::E / R; ++q)
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+          const float2 z = v[q * R + bitrev(k, BITS)];
+          gout[t + q * G::T + k * GR] = make_float2(z.x * scale, z.y * scale);
+        }
+    }
+  } else {
+    if constexpr (P > 0) __syncthreads();  // every thread has read its pass input
+#pragma unroll
+    for (int q = 0; q < G::E / R; ++q) {
+      const int g = t + q * G::T;
+      const int base = ((g >> NSB) << (NSB + BITS)) + (g & (NS - 1));
+#pragma unroll
+      for (int k = 0; k < R; ++k) buf[lds_pad(base + k * NS)] = v[q * R + bitrev(k, BITS)];
+    }
+    __syncthreads();
+    if constexpr (!LAST) run_passes<LOGM, P + 1, INV, TO_GLOBAL>(v, buf, t, tw, gout, scale, live);
+  }
+}
+
+// x: rows x in_len f32 (zero-padded / truncated to n = 2M); X: rows x (M+1) c64.
+template <int LOGM, bool VEC>
+__global__ __launch_bounds__(Geo<LOGM>::NT) void rfft_kernel(const float* __restrict__ x,
+                                                             float2* __restrict__ X,
+                                                             const float2* __restrict__ tw,
+                                                             int64_t rows, int64_t in_len) {
+  using G = Geo<LOGM>;
+  constexpr Plan pl{LOGM};
+  __shared__ float2 lds[G::RPB * G::PM];
+  const int t = threadIdx.x % G::T;
+  const int rb = threadIdx.x / G::T;
+  const int64_t row = (int64_t)blockIdx.x * G::RPB + rb;
+  const bool live = row < rows;
+  float2* buf = lds + rb * G::PM;
+  const float* xr = x + (live ? row : 0) * in_len;
+
+  float2 v[G::E];
+  constexpr int R0 = 1 << pl.bits(0);
+#pragma unroll
+  for (int q = 0; q < G::E / R0; ++q)
+#pragma unroll
+    for (int r = 0; r < R0; ++r) {
+      const int64_t j2 = 2 * (int64_t)(t + q * G::T + r * (G::M / R0));
+      float2 z = make_float2(0.f, 0.f);
+      if (live) {
+        if (VEC) {
+          if (j2 < in_len) z = *reinterpret_cast<const float2*>(xr + j2);
+        } else {
+          if (j2 < in_len) z.x = xr[j2];
+          if (j2 + 1 < in_len) z.y = xr[j2 + 1];
+        }
+      }
+      v[q * R0 + r] = z;
+    }
+  run_passes<LOGM, 0, false, false>(v, buf, t, tw, nullptr, 1.f, live);
+
+  if (!live) return;
+  const float2* wu = tw + pl.offset(pl.npass());
+  float2* Xr = X + row * (G::M + 1);
+  for (int k = t; k <= G::M; k += G::T) {
+    const float2 a = buf[lds_pad(k & (G::M - 1))];
+    const float2 b = buf[lds_pad((G::M - k) & (G::M - 1))];
+    const float2 e = make_float2(0.5f * (a.x + b.x), 0.5f * (a.y - b.y));
+    const float2 o = make_float2(0.5f * (a.y + b.y), 0.5f * (b.x - a.x));
+    const float2 w = wu[k];
+    Xr[k] = make_float2(e.x + (w.x * o.x - w.y * o.y), e.y + (w.x * o.y + w.y * o.x));
+  }
+}
+
+// X: rows x in_len c64 one-sided spectrum; x: rows x n f32 (n = 2M).
+template <int LOGM>
+__global__ __launch_bounds__(Geo<LOGM>::NT) void irfft_kernel(const float2* __restrict__ X,
+                                                              float* __restrict__ x,
+                                                              const float2* __restrict__ tw,
+                                                              int64_t rows, int64_t in_len) {
+  using G = Geo<LOGM>;
+  constexpr Plan pl{LOGM};
+  __shared__ float2 lds[G::RPB * G::PM];
+  const int t = threadIdx.x % G::T;
+  const int rb = threadIdx.x / G::T;
+  const int64_t row = (int64_t)blockIdx.x * G::RPB + rb;
+  const bool live = row < rows;
+  float2* buf = lds + rb * G::PM;
+  const float2* Xr = X + (live ? row : 0) * in_len;
+  const float2* wu = tw + pl.offset(pl.npass());
+
+  // Pack the Hermitian spectrum into Z = E + i O (E, O: spectra of the even
+  // and odd samples).  Bins at or above in_len are zero; the imaginary parts
+  // of the DC and Nyquist bins do not contribute to a real signal.
+  float2 v[G::E];
+  constexpr int R0 = 1 << pl.bits(0);
+#pragma unroll
+  for (int q = 0; q < G::E / R0; ++q)
+#pragma unroll
+    for (int r = 0; r < R0; ++r) {
+      const int j = t + q * G::T + r * (G::M / R0);
+      const int jj = G::M - j;
+      float2 a = make_float2(0.f, 0.f), b = make_float2(0.f, 0.f);
+      if (live) {
+        if (j < in_len) a = Xr[j];
+        if (jj < in_len) b = Xr[jj];
+      }
+      if (j == 0) a.y = 0.f;
+      if (jj == G::M) b.y = 0.f;
+      const float2 e = make_float2(0.5f * (a.x + b.x), 0.5f * (a.y - b.y));
+      const float2 d = make_float2(0.5f * (a.x - b.x), 0.5f * (a.y + b.y));
+      const float2 w = wu[j];  // o = d * conj(w)
+      const float2 o = make_float2(d.x * w.x + d.y * w.y, d.y * w.x - d.x * w.y);
+      v[q * R0 + r] = make_float2(e.x - o.y, e.y + o.x);
+    }
+  float2* out = reinterpret_cast<float2*>(x + (live ? row : 0) * (2 * (int64_t)G::M));
+  run_passes<LOGM, 0, true, true>(v, buf, t, tw, out, 1.0f / G::M, live);
+}
+
+// n == 1: X[row] = x[row, 0] (or 0 for an empty row).
+__global__ __launch_bounds__(256) void rfft1_kernel(const float* __restrict__ x,
+                                                    float2* __restrict__ X, int64_t rows,
+                                                    int64_t in_len) {
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r < rows) X[r] = make_float2(in_len > 0 ? x[r * in_len] : 0.f, 0.f);
+}
+
+// ---- twiddle tables (built once per size, kept for the process) -----------
+std::mutex g_tw_mu;
+std::map<int, float2*> g_tw;
+
+const float2* twiddles(int logm) {
+  std::lock_guard<std::mutex> lock(g_tw_mu);
+  auto it = g_tw.find(logm);
+  if (it != g_tw.end()) return it->second;
+  const Plan pl{logm};
+  const int64_t M = pl.m();
+  std::vector<float2> h(pl.table_size());
+  const double two_pi = 6.283185307179586476925286766559;
+  for (int p = 0; p < pl.npass(); ++p) {
+    const int64_t R = 1 << pl.bits(p), NS = 1 << pl.ns_bits(p);
+    for (int64_t r = 1; r < R; ++r)
+      for (int64_t k = 0; k < NS; ++k) {
+        const double a = -two_pi * (double)(r * k) / (double)(NS * R);
+        h[pl.offset(p) + (r - 1) * NS + k] = make_float2((float)std::cos(a), (float)std::sin(a));
+      }
+  }
+  for (int64_t k = 0; k <= M; ++k) {
+    const double a = -two_pi * (double)k / (double)(2 * M);
+    h[pl.offset(pl.npass()) + k] = make_float2((float)std::cos(a), (float)std::sin(a));
+  }
+  void* d = wxx_alloc(h.size() * sizeof(float2));
+  if (!d) return nullptr;
+  if (wxx_h2d(d, h.data(), h.size() * sizeof(float2)) != WXX_OK) {
+    wxx_free(d);
+    return nullptr;
+  }
+  g_tw[logm] = static_cast<float2*>(d);
+  return static_cast<float2*>(d);
+}
+
+int log2_exact(int64_t n) {
+  int l = 0;
+  while ((int64_t(1) << l) < n) ++l;
+  return (int64_t(1) << l) == n ? l : -1;
+}
+
+template <int LOGM>
+void launch_rfft(const float* x, float2* X, const float2* tw, int64_t rows, int64_t in_len,
+                 bool vec) {
+  using G = Geo<LOGM>;
+  const dim3 grid((unsigned)((rows + G::RPB - 1) / G::RPB));
+  if (vec)
+    hipLaunchKernelGGL((rfft_kernel<LOGM, true>), grid, dim3(G::NT), 0, wxx::stream(), x, X, tw,
+                       rows, in_len);
+  else
+    hipLaunchKernelGGL((rfft_kernel<LOGM, false>), grid, dim3(G::NT), 0, wxx::stream(), x, X, tw,
+                       rows, in_len);
+}
+
+template <int LOGM>
+void launch_irfft(const float2* X, float* x, const float2* tw, int64_t rows, int64_t in_len) {
+  using G = Geo<LOGM>;
+  const dim3 grid((unsigned)((rows + G::RPB - 1) / G::RPB));
+  hipLaunchKernelGGL((irfft_kernel<LOGM>), grid, dim3(G::NT), 0, wxx::stream(), X, x, tw, rows,
+                     in_len);
+}
+
+template <int L = 0>
+void dispatch_rfft(int logm, const float* x, float2* X, const float2* tw, int64_t rows,
+                   int64_t in_len, bool vec) {
+  if constexpr (L <= kMaxLogM) {
+    if (logm == L) return launch_rfft<L>(x, X, tw, rows, in_len, vec);
+    dispatch_rfft<L + 1>(logm, x, X, tw, rows, in_len, vec);
+  }
+}
+
+template <int L = 0>
+void dispatch_irfft(int logm, const float2* X, float* x, const float2* tw, int64_t rows,
+                    int64_t in_len) {
+  if constexpr (L <= kMaxLogM) {
+    if (logm == L) return launch_irfft<L>(X, x, tw, rows, in_len);
+    dispatch_irfft<L + 1>(logm, X, x, tw, rows, in_len);
+  }
+}
+
+// ---- complex elementwise --------------------------------------------------
+// op 0: out = a * b, op 1: out = a + b; conj flags conjugate an operand.
+__global__ __launch_bounds__(256) void complex_binary_kernel(float2* __restrict__ out,
+                                                             const float2* __restrict__ a,
+                                                             const float2* __restrict__ b,
+                                                             wxx::ND nd, int64_t n, int op,
+                                                             int conj_a, int conj_b) {
+  const int64_t step = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += step) {
+    int64_t off[3];
+    wxx::offsets64<3>(nd, i, off);
+    float2 u = a[off[1]], w = b[off[2]];
+    if (conj_a) u.y = -u.y;
+    if (conj_b) w.y = -w.y;
+    out[off[0]] = op == 0 ? cmul(u, w) : make_float2(u.x + w.x, u.y + w.y);
+  }
+}
+
+__global__ __launch_bounds__(256) void complex_conj_kernel(float2* __restrict__ dst,
+                                                           const float2* __restrict__ src,
+                                                           wxx::ND nd, int64_t n) {
+  const int64_t step = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += step) {
+    int64_t off[2];
+    wxx::offsets64<2>(nd, i, off);
+    const float2 u = src[off[1]];
+    dst[off[0]] = make_float2(u.x, -u.y);
+  }
+}
+
+__global__ __launch_bounds__(256) void complex_pad_kernel(const float2* __restrict__ src,
+                                                          float2* __restrict__ dst,
+                                                          int64_t batch, int64_t in_len,
+                                                          int64_t out_len) {
+  const int64_t n = batch * out_len;
+  const int64_t step = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += step) {
+    const int64_t r = i / out_len, c = i - r * out_len;
+    dst[i] = c < in_len ? src[r * in_len + c] : make_float2(0.f, 0.f);
+  }
+}
+
+}  // namespace
+
+// Replaces functional.rfft (fft.py:484-563): rows x in_len f32 -> rows x
+// (n/2+1) c64, zero-padding or truncating each row to the power of two n.
+WXX_API int wxx_rfft(const float* x, void* X, int64_t rows, int64_t in_len, int64_t n) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(x && X, "null pointer");
+  WXX_REQUIRE(rows >= 0 && in_len >= 0, "bad rfft dims");
+  const int logn = log2_exact(n);
+  WXX_REQUIRE(logn >= 0, "FFT length must be a positive power of two, got %lld", (long long)n);
+  if (rows == 0) return WXX_OK;
+  if (logn - 1 > kMaxLogM)
+    return wxx::set_error(WXX_E_UNSUPPORTED, "rfft length %lld above %d", (long long)n,
+                          2 << kMaxLogM);
+  float2* Xc = static_cast<float2*>(X);
+  if (n == 1) {
+    hipLaunchKernelGGL(rfft1_kernel, dim3(wxx::grid_1d(rows, 256)), dim3(256), 0, wxx::stream(),
+                       x, Xc, rows, in_len);
+  } else {
+    const float2* tw = twiddles(logn - 1);
+    if (!tw) return wxx::set_error(WXX_E_OOM, "rfft twiddle table allocation failed");
+    const bool vec = in_len % 2 == 0 && (uintptr_t)x % 8 == 0;
+    dispatch_rfft(logn - 1, x, Xc, tw, rows, in_len, vec);
+  }
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// Replaces functional.irfft (fft.py:566-645): rows x in_len c64 one-sided
+// spectrum -> rows x n f32, n a power of two >= 2.
+WXX_API int wxx_irfft(const void* X, float* x, int64_t rows, int64_t in_len, int64_t n) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(x && X, "null pointer");
+  WXX_REQUIRE(rows >= 0 && in_len >= 0, "bad irfft dims");
+  const int logn = log2_exact(n);
+  WXX_REQUIRE(logn >= 1, "irfft length must be a power of two >= 2, got %lld", (long long)n);
+  if (rows == 0) return WXX_OK;
+  if (logn - 1 > kMaxLogM)
+    return wxx::set_error(WXX_E_UNSUPPORTED, "irfft length %lld above %d", (long long)n,
+                          2 << kMaxLogM);
+  const float2* tw = twiddles(logn - 1);
+  if (!tw) return wxx::set_error(WXX_E_OOM, "irfft twiddle table allocation failed");
+  dispatch_irfft(logn - 1, static_cast<const float2*>(X), x, tw, rows, in_len);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// Replaces functional.complex_mul (fft.py:168-213, op 0, conj flags) and
+// complex_add_inplace (fft.py:216-245, op 1; here out-of-place or with
+// out == a).  Strides count complex elements; 0 = broadcast.
+WXX_API int wxx_complex_binary(void* out, const void* a, const void* b, int rank,
+                               const int64_t* shape, const int64_t* s_out, const int64_t* s_a,
+                               const int64_t* s_b, int op, int conj_a, int conj_b) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(out && a && b && shape && s_out && s_a && s_b, "null pointer");
+  WXX_REQUIRE(rank >= 0 && rank <= wxx::kMaxRank, "rank %d unsupported", rank);
+  WXX_REQUIRE(op == 0 || op == 1, "bad complex op %d", op);
+  int64_t n = 1;
+  for (int d = 0; d < rank; ++d) n *= shape[d];
+  if (n == 0) return WXX_OK;
+  const int64_t* ss[3] = {s_out, s_a, s_b};
+  const wxx::ND nd = wxx::collapse(rank, shape, ss, 3);
+  hipLaunchKernelGGL(complex_binary_kernel, dim3(wxx::grid_1d(n, 256, 16384)), dim3(256), 0,
+                     wxx::stream(), static_cast<float2*>(out), static_cast<const float2*>(a),
+                     static_cast<const float2*>(b), nd, n, op, conj_a ? 1 : 0, conj_b ? 1 : 0);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// Replaces functional.complex_conj (fft.py:248-292).
+WXX_API int wxx_complex_conj(void* dst, const void* src, int rank, const int64_t* shape,
+                             const int64_t* s_dst, const int64_t* s_src) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(dst && src && shape && s_dst && s_src, "null pointer");
+  WXX_REQUIRE(rank >= 0 && rank <= wxx::kMaxRank, "rank %d unsupported", rank);
+  int64_t n = 1;
+  for (int d = 0; d < rank; ++d) n *= shape[d];
+  if (n == 0) return WXX_OK;
+  const int64_t* ss[2] = {s_dst, s_src};
+  const wxx::ND nd = wxx::collapse(rank, shape, ss, 2);
+  hipLaunchKernelGGL(complex_conj_kernel, dim3(wxx::grid_1d(n, 256, 16384)), dim3(256), 0,
+                     wxx::stream(), static_cast<float2*>(dst), static_cast<const float2*>(src),
+                     nd, n);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// Replaces functional.complex_pad (fft.py:345-383): batch x in_len ->
+// batch x out_len, zero-padded or truncated.
+WXX_API int wxx_complex_pad(const void* src, void* dst, int64_t batch, int64_t in_len,
+                            int64_t out_len) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(src && dst, "null pointer");
+  WXX_REQUIRE(batch >= 0 && in_len >= 0 && out_len >= 0, "bad complex_pad dims");
+  if (batch == 0 || out_len == 0) return WXX_OK;
+  hipLaunchKernelGGL(complex_pad_kernel, dim3(wxx::grid_1d(batch * out_len, 256, 16384)),
+                     dim3(256), 0, wxx::stream(), static_cast<const float2*>(src),
+                     static_cast<float2*>(dst), batch, in_len, out_len);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}

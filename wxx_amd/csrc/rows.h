@@ -12,7 +12,7 @@ namespace wxx {
 
 template <int TPR>
 struct RowReduce {
-  // `red` is LDS scratch of at least 4 floats per row group (TPR == 256 only).
+  // `red` is LDS scratch of at least TPR / 64 floats (TPR >= 256 only).
   __device__ static float sum(float v, float* red) {
     if (TPR == 64) return warp_sum(v);
     return block_sum(v, red);
@@ -124,8 +124,27 @@ int row_dispatch(int64_t C, bool vec, F&& f) {
 #undef WXX_RD_CASE
 }
 
+// Wide-row plan for kernels that can use 1024-lane workgroups (up to 65536
+// columns in registers): TPR * 100 + NCH, or 0 for the looped kernel.
+inline int wide_row_plan(int64_t C) {
+  const int p = row_plan(C);
+  if (p) return p;
+  if (C <= 1024 * 4 * 8) return 1024 * 100 + 8;
+  if (C <= 1024 * 4 * 16) return 1024 * 100 + 16;
+  return 0;
+}
+
+template <typename F>
+int wide_row_dispatch(int64_t C, bool vec, F&& f) {
+  const int plan = wide_row_plan(C);
+  if (plan / 100 != 1024) return row_dispatch(C, vec, f);
+  if (plan % 100 == 8)
+    return vec ? f(ic<1024>{}, ic<8>{}, std::true_type{}) : f(ic<1024>{}, ic<8>{}, std::false_type{});
+  return vec ? f(ic<1024>{}, ic<16>{}, std::true_type{}) : f(ic<1024>{}, ic<16>{}, std::false_type{});
+}
+
 inline dim3 row_grid(int tpr, int64_t rows) {
-  const int64_t rpb = 256 / tpr;
+  const int64_t rpb = tpr >= 256 ? 1 : 256 / tpr;
   return dim3((unsigned)((rows + rpb - 1) / rpb));
 }
 

@@ -102,7 +102,73 @@ __global__ __launch_bounds__(256) void softmax_cols_kernel(const float* __restri
   for (int64_t c = 0; c < C; ++c) q[c * inner] = expf(p[c * inner] - m) * inv;
 }
 
+// dx = y * (g - sum(g * y)) per row: one read of y and g, one write.
+template <int TPR, int NCH, bool VEC>
+__global__ __launch_bounds__(256) void softmax_bwd_rows_kernel(const float* __restrict__ y,
+                                                                const float* __restrict__ g,
+                                                                float* __restrict__ dx,
+                                                                int64_t rows, int C) {
+  __shared__ float red[4];
+  constexpr int RPB = 256 / TPR;
+  const int t = threadIdx.x % TPR;
+  const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;
+  if (TPR == 64 && row >= rows) return;
+  wxx::RowRegs<TPR, NCH, VEC> vy, vg;
+  vy.load(y + row * C, C, t, 0.f);
+  vg.load(g + row * C, C, t, 0.f);
+  float dot = 0.f;
+#pragma unroll
+  for (int e = 0; e < NCH * 4; ++e) dot += vg.v[e] * vy.v[e];
+  dot = wxx::RowReduce<TPR>::sum(dot, red);
+#pragma unroll
+  for (int e = 0; e < NCH * 4; ++e) vy.v[e] = vy.v[e] * (vg.v[e] - dot);
+  vy.store(dx + row * C, C, t);
+}
+
+__global__ __launch_bounds__(256) void softmax_bwd_cols_kernel(const float* __restrict__ y,
+                                                                const float* __restrict__ g,
+                                                                float* __restrict__ dx,
+                                                                int64_t outer, int64_t C,
+                                                                int64_t inner) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= outer * inner) return;
+  const int64_t o = t / inner, i = t - o * inner;
+  const int64_t base = o * C * inner + i;
+  float dot = 0.f;
+  for (int64_t c = 0; c < C; ++c) dot += g[base + c * inner] * y[base + c * inner];
+  for (int64_t c = 0; c < C; ++c)
+    dx[base + c * inner] = y[base + c * inner] * (g[base + c * inner] - dot);
+}
+
 }  // namespace
+
+// Softmax backward dx = y * (g - sum_c g y) along C.  Replaces the composite
+// multiply / sum / unsqueeze / subtract / multiply chain of reference
+// src/wxx/autograd/reductions.py:25-35.
+WXX_API int wxx_softmax_backward(const float* y, const float* g, float* dx, int64_t outer,
+                                 int64_t C, int64_t inner) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(y && g && dx, "null pointer");
+  WXX_REQUIRE(outer >= 0 && C >= 1 && inner >= 1, "bad softmax dims");
+  if (outer == 0) return WXX_OK;
+  hipStream_t s = wxx::stream();
+  if (inner == 1 && wxx::row_plan(C) != 0) {
+    const bool vec = (C % 4 == 0) && ((((uintptr_t)y) | ((uintptr_t)g) | ((uintptr_t)dx)) % 16 == 0);
+    int rc = wxx::row_dispatch(C, vec, [&](auto tpr, auto nch, auto v) {
+      hipLaunchKernelGGL((softmax_bwd_rows_kernel<decltype(tpr)::value, decltype(nch)::value,
+                                                  decltype(v)::value>),
+                         wxx::row_grid(decltype(tpr)::value, outer), dim3(256), 0, s, y, g, dx,
+                         outer, (int)C);
+      return 0;
+    });
+    if (rc) return rc;
+  } else {
+    hipLaunchKernelGGL(softmax_bwd_cols_kernel, dim3(wxx::grid_1d(outer * inner, 256)), dim3(256),
+                       0, s, y, g, dx, outer, C, inner);
+  }
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
 
 // Replaces functional.softmax (reference src/wxx/functional/activations.py:126-173).
 WXX_API int wxx_softmax(const float* x, float* y, int64_t outer, int64_t C, int64_t inner) {

@@ -44,6 +44,36 @@ def unary(tensor1, name):
     return out
 
 
+# Derivative op used by unary_backward for each differentiable activation.
+_DERIVATIVE = {
+    "relu": "relubackwards",
+    "gelu": "gelubackwards",
+    "sigmoid": "sigmoidbackwards",
+    "selu": "selubackwards",
+    "sin": "sinback",
+    "cos": "cosback",
+}
+
+
+def unary_backward(src, grad, name):
+    """``f'(src) * grad`` for activation ``name`` in one kernel (for sigmoid
+    ``src`` is the forward output, as the reference's sigmoidbackwards takes)."""
+    if name not in _DERIVATIVE:
+        raise ValueError(f"no fused backward for {name!r}")
+    if not src.is_contiguous():
+        src = src.contiguous()
+    if not grad.is_contiguous():
+        grad = grad.contiguous()
+    if tuple(src.shape) != tuple(grad.shape):
+        raise ValueError(
+            f"unary_backward shapes differ: {tuple(src.shape)} vs {tuple(grad.shape)}"
+        )
+    out = empty(src.shape)
+    call("wxx_unary_backward", ptr(src), ptr(grad), ptr(out), validation.numel(src.shape),
+         UNARY[_DERIVATIVE[name]])
+    return out
+
+
 def relu(tensor1):
     return unary(tensor1, "relu")
 
@@ -105,4 +135,24 @@ def softmax(tensor1, dim):
     out = empty(tensor1.shape, requires_grad=tensor1.requires_grad)
     if validation.numel(tensor1.shape):
         call("wxx_softmax", ptr(tensor1), ptr(out), outer, c, inner)
+    return out
+
+
+def softmax_backward(y, grad, dim):
+    """``y * (grad - sum(grad * y, dim))`` from the softmax output ``y`` in one
+    kernel (the chain of reference src/wxx/autograd/reductions.py:25-35)."""
+    if not y.is_contiguous():
+        y = y.contiguous()
+    if not grad.is_contiguous():
+        grad = grad.contiguous()
+    if tuple(y.shape) != tuple(grad.shape):
+        raise ValueError(
+            f"softmax_backward shapes differ: {tuple(y.shape)} vs {tuple(grad.shape)}"
+        )
+    rank = validation.check_rank(y.shape, name="softmax_backward input")
+    dim = validation.normalize_dim(dim, rank, name="dim")
+    outer, c, inner, _ = _get_reduce_dims(y.shape, dim)
+    out = empty(y.shape)
+    if validation.numel(y.shape):
+        call("wxx_softmax_backward", ptr(y), ptr(grad), ptr(out), outer, c, inner)
     return out

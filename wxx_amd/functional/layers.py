@@ -1,0 +1,133 @@
+"""AdamW, dropout and embedding ops (reference src/wxx/functional/layers.py:21-254)."""
+
+import ctypes as C
+import math
+import random
+
+from .. import validation
+from ._common import call, empty, ptr
+
+
+def adamw(tensor1, grad, exp_avg, exp_avg_sq, step, lr, beta1, beta2, eps, weight_decay, bc1,
+          bc2):
+    """In-place AdamW update of ``tensor1`` and its two moment buffers."""
+    if not tensor1.is_contiguous():
+        raise ValueError("adamw updates its parameter in place: it must be contiguous")
+    n = validation.numel(tensor1.shape)
+    for t, name in ((grad, "grad"), (exp_avg, "exp_avg"), (exp_avg_sq, "exp_avg_sq")):
+        if validation.numel(t.shape) != n or not t.is_contiguous():
+            raise ValueError(f"adamw {name} must be contiguous with {n} elements")
+    call("wxx_adamw", ptr(tensor1), ptr(grad), ptr(exp_avg), ptr(exp_avg_sq), n, float(lr),
+         float(beta1), float(beta2), float(eps), float(weight_decay), float(bc1), float(bc2))
+
+
+def adamw_multi(params, grads, exp_avgs, exp_avg_sqs, lr, beta1, beta2, eps, weight_decay, bc1,
+                bc2):
+    """AdamW over a whole parameter list in one launch (same per-element math)."""
+    count = len(params)
+    if not count:
+        return
+    arrs = [(C.c_void_p * count)() for _ in range(4)]
+    sizes = (C.c_int64 * count)()
+    for i, group in enumerate(zip(params, grads, exp_avgs, exp_avg_sqs)):
+        n = validation.numel(group[0].shape)
+        for a, t in zip(arrs, group):
+            if validation.numel(t.shape) != n or not t.is_contiguous():
+                raise ValueError("adamw_multi expects contiguous tensors of matching size")
+            a[i] = t.data_ptr()
+        sizes[i] = n
+    call("wxx_adamw_multi", *arrs, sizes, count, float(lr), float(beta1), float(beta2),
+         float(eps), float(weight_decay), float(bc1), float(bc2))
+
+
+def sumsq_multi(tensors):
+    """Device scalar (shape (1,)) holding the sum of squares of every tensor."""
+    count = len(tensors)
+    out = empty((1,))
+    ptrs = (C.c_void_p * max(1, count))()
+    sizes = (C.c_int64 * max(1, count))()
+    for i, t in enumerate(tensors):
+        if not t.is_contiguous() or t.type != "f32":
+            raise ValueError("sumsq_multi expects contiguous f32 tensors")
+        ptrs[i] = t.data_ptr()
+        sizes[i] = validation.numel(t.shape)
+    call("wxx_sumsq_multi", ptrs, sizes, count, ptr(out))
+    return out
+
+
+def scale_multi(tensors, coef):
+    """Multiply every tensor in place by ``coef`` (each storage once)."""
+    seen = set()
+    uniq = []
+    for t in tensors:
+        key = (t.data_ptr(), validation.numel(t.shape))
+        if key not in seen:
+            seen.add(key)
+            uniq.append(t)
+    count = len(uniq)
+    if not count:
+        return
+    ptrs = (C.c_void_p * count)()
+    sizes = (C.c_int64 * count)()
+    for i, t in enumerate(uniq):
+        if not t.is_contiguous() or t.type != "f32":
+            raise ValueError("scale_multi expects contiguous f32 tensors")
+        ptrs[i] = t.data_ptr()
+        sizes[i] = validation.numel(t.shape)
+    call("wxx_scale_multi", ptrs, sizes, count, float(coef))
+
+
+def dropout(tensor1, p):
+    """Inverted dropout; returns ``(y, seed)`` with a fresh 32-bit seed per call."""
+    if not tensor1.is_contiguous():
+        tensor1 = tensor1.contiguous()
+    n = math.prod(tensor1.shape)
+    scale = 1 / (1 - p)
+    r = random.randint(0, 2**32 - 1)
+    out = empty(tensor1.shape)
+    call("wxx_dropout", ptr(tensor1), ptr(out), n, r, float(p), float(scale))
+    return out, r
+
+
+def dropoutdx(tensor1, p, seed):
+    """Gradient of :func:`dropout` with the forward call's ``seed``."""
+    if not tensor1.is_contiguous():
+        tensor1 = tensor1.contiguous()
+    n = math.prod(tensor1.shape)
+    out = empty(tensor1.shape)
+    call("wxx_dropout", ptr(tensor1), ptr(out), n, int(seed) & 0xFFFFFFFF, float(p),
+         float(1 / (1 - p)))
+    return out
+
+
+def embed(tensor1, tensor2, n_token, embed_dim):
+    """Gather rows of ``tensor2`` (V, D) by the u32 ids in ``tensor1`` (B, L)."""
+    if not tensor1.is_contiguous():
+        tensor1 = tensor1.contiguous()
+    if not tensor2.is_contiguous():
+        tensor2 = tensor2.contiguous()
+    if tensor1.type != "u32":
+        raise TypeError(f"embed expects u32 ids, got {tensor1.type!r}")
+    if validation.numel(tensor1.shape) < n_token:
+        raise ValueError(f"embed: {n_token} tokens requested, ids hold {validation.numel(tensor1.shape)}")
+    V = tensor2.shape[0]
+    if validation.numel(tensor2.shape) != V * embed_dim:
+        raise ValueError(f"embed weight {tuple(tensor2.shape)} does not have width {embed_dim}")
+    out = empty((tensor1.shape[0], tensor1.shape[1], embed_dim))
+    call("wxx_embed", ptr(tensor1), ptr(tensor2), ptr(out), n_token, embed_dim, V)
+    return out
+
+
+def embeddx(tensor1, tensor2, n_token, embed_dim, vocab_size):
+    """Weight gradient of :func:`embed` (``tensor1`` = grad, ``tensor2`` = ids)."""
+    if not tensor1.is_contiguous():
+        tensor1 = tensor1.contiguous()
+    if not tensor2.is_contiguous():
+        tensor2 = tensor2.contiguous()
+    if validation.numel(tensor1.shape) < n_token * embed_dim:
+        raise ValueError("embeddx grad is smaller than n_token * embed_dim")
+    if validation.numel(tensor2.shape) < n_token:
+        raise ValueError("embeddx ids are fewer than n_token")
+    grad = empty((vocab_size, embed_dim))
+    call("wxx_embeddx", ptr(tensor1), ptr(tensor2), ptr(grad), n_token, embed_dim, vocab_size)
+    return grad

@@ -1,0 +1,58 @@
+"""Cross-entropy loss (reference src/wxx/functional/loss.py:20-101)."""
+
+import ctypes as C
+
+import numpy as np
+
+from .. import validation
+from ..backend import lib as _lib
+from ._common import call, empty, ptr
+
+_bad_flag = {"buf": None}
+
+
+def _flag():
+    """A persistent 4-byte device word for the out-of-range-target flag."""
+    if _bad_flag["buf"] is None:
+        from ..backend.device import get_buffer_pool
+
+        _bad_flag["buf"] = get_buffer_pool().create_buffer(4, label="cceloss flag")
+    return _bad_flag["buf"]
+
+
+def cceloss(tensor1, tensor2):
+    """Softmax cross-entropy of ``(B, K)`` logits against ``(B,)`` u32 targets.
+
+    Returns ``(loss (B, 1), dlogits (B, K))``.  A target ``>= K`` raises
+    ``ValueError`` like the reference; the check runs on the device and costs
+    one 4-byte readback instead of reading back every target.
+    """
+    validation.check_rank(tensor1.shape, min_rank=2, max_rank=2, name="logits")
+    validation.check_rank(tensor2.shape, min_rank=1, max_rank=1, name="targets")
+    if tensor1.type != "f32":
+        raise TypeError(f"cceloss expects f32 logits, got {tensor1.type!r}")
+    if tensor2.type != "u32":
+        raise TypeError(f"cceloss expects u32 targets, got {tensor2.type!r}")
+    if not tensor1.is_contiguous():
+        tensor1 = tensor1.contiguous()
+    if not tensor2.is_contiguous():
+        tensor2 = tensor2.contiguous()
+    B, K = tensor1.shape
+    if tensor2.shape[0] != B:
+        raise ValueError(
+            f"cceloss expects one target per row, got {tensor2.shape[0]} targets for {B} rows"
+        )
+    if B < 1 or K < 1:
+        raise ValueError(f"cceloss expects non-empty logits, got {(B, K)}")
+    flag = _flag()
+    call("wxx_fill_u32", C.c_void_p(flag.ptr), 1, 0)
+    loss = empty((B, 1), requires_grad=tensor1.requires_grad)
+    grad = empty(tensor1.shape)
+    call("wxx_cceloss", ptr(tensor1), ptr(tensor2), ptr(loss), ptr(grad), B, K,
+         C.c_void_p(flag.ptr))
+    bad = np.zeros(1, np.int32)
+    _lib.call("wxx_d2h", bad.ctypes.data_as(C.c_void_p), C.c_void_p(flag.ptr), 4)
+    if bad[0]:
+        tmax = int(tensor2.numpy().max())
+        raise ValueError(f"cceloss targets must be in [0, {K}), got max target {tmax}")
+    return loss, grad

@@ -5,6 +5,7 @@ Eps values follow the reference: LayerNorm 1e-5 (normalization.py:94),
 RMSNorm 1e-6 (:36), BatchNorm 1e-5 with momentum 0.1 (:157).
 """
 
+from .. import validation
 from ..backend import compat
 from ..backend.dispatch import _get_reduce_dims
 from ._common import call, contiguous_f32, empty, ptr
@@ -15,11 +16,29 @@ BN_EPS = 1e-5
 BN_MOMENTUM = 0.1
 
 
+def _check_param(t, n, name):
+    """The kernels index per-feature parameters by the reduce coordinate:
+    a parameter with fewer than ``n`` elements would be read out of bounds,
+    so a size mismatch is rejected before launch."""
+    if t.type != "f32":
+        raise TypeError(f"{name} must be an f32 tensor, got {t.type!r}")
+    if validation.numel(t.shape) != n:
+        raise ValueError(
+            f"{name} has {validation.numel(t.shape)} elements but the normalised extent is {n}"
+        )
+
+
+def _check_stats(t, n, name):
+    if validation.numel(t.shape) != n:
+        raise ValueError(f"{name} has {validation.numel(t.shape)} elements, expected {n}")
+
+
 def rmsnorm(tensor1, gamma, axis=None):
     """``y = x * r * gamma`` with ``r = rsqrt(mean(x^2) + 1e-6)`` (0 for an all-zero slice)."""
     tensor1 = contiguous_f32(tensor1)
     gamma = contiguous_f32(gamma, "gamma")
     outer, red, inner, out_shape = _get_reduce_dims(tensor1.shape, axis)
+    _check_param(gamma, red, "gamma")
     y = empty(tensor1.shape)
     irms = empty(out_shape)
     call("wxx_rmsnorm", ptr(tensor1), ptr(gamma), ptr(y), ptr(irms), outer, red, inner,
@@ -33,6 +52,8 @@ def meanvarnorm(tensor1, gamma, beta, axis=None):
     gamma = contiguous_f32(gamma, "gamma")
     beta = contiguous_f32(beta, "beta")
     outer, red, inner, out_shape = _get_reduce_dims(tensor1.shape, axis)
+    _check_param(gamma, red, "gamma")
+    _check_param(beta, red, "beta")
     y = empty(tensor1.shape)
     mean = empty(out_shape)
     istd = empty(out_shape)
@@ -47,6 +68,10 @@ def meanvarnormdx(grad, tensor1, gamma, mean, var, axis=None):
     gamma = contiguous_f32(gamma, "gamma")
     grad = contiguous_f32(grad, "grad")
     outer, red, inner, _ = _get_reduce_dims(tensor1.shape, axis)
+    _check_param(gamma, red, "gamma")
+    validation.check_same_shape(grad.shape, tensor1.shape, name="grad and input")
+    _check_stats(mean, outer * inner, "mean")
+    _check_stats(var, outer * inner, "inv_std")
     dx = empty(tensor1.shape)
     call("wxx_meanvarnormdx", ptr(grad), ptr(tensor1), ptr(gamma), ptr(mean), ptr(var), ptr(dx),
          outer, red, inner, compat.row_cap())
@@ -58,6 +83,9 @@ def meanvarnormdg(grad, tensor1, mean, var, axis=None):
     tensor1 = contiguous_f32(tensor1)
     grad = contiguous_f32(grad, "grad")
     outer, red, inner, _ = _get_reduce_dims(tensor1.shape, axis)
+    validation.check_same_shape(grad.shape, tensor1.shape, name="grad and input")
+    _check_stats(mean, outer * inner, "mean")
+    _check_stats(var, outer * inner, "inv_std")
     dg = empty((red,))
     db = empty((red,))
     call("wxx_meanvarnormdg", ptr(grad), ptr(tensor1), ptr(mean), ptr(var), ptr(dg), ptr(db),
@@ -70,6 +98,9 @@ def rmsnormdx(grad, tensor1, gamma, irms, axis=None):
     gamma = contiguous_f32(gamma, "gamma")
     grad = contiguous_f32(grad, "grad")
     outer, red, inner, _ = _get_reduce_dims(tensor1.shape, axis)
+    _check_param(gamma, red, "gamma")
+    validation.check_same_shape(grad.shape, tensor1.shape, name="grad and input")
+    _check_stats(irms, outer * inner, "inv_rms")
     dx = empty(tensor1.shape)
     call("wxx_rmsnormdx", ptr(grad), ptr(tensor1), ptr(gamma), ptr(irms), ptr(dx),
          outer, red, inner)
@@ -80,6 +111,9 @@ def rmsnormdg(grad, tensor1, gamma, irms, axis=None):
     tensor1 = contiguous_f32(tensor1)
     grad = contiguous_f32(grad, "grad")
     outer, red, inner, _ = _get_reduce_dims(tensor1.shape, axis)
+    _check_param(gamma, red, "gamma")
+    validation.check_same_shape(grad.shape, tensor1.shape, name="grad and input")
+    _check_stats(irms, outer * inner, "inv_rms")
     dg = empty(gamma.shape)
     call("wxx_rmsnormdg", ptr(grad), ptr(tensor1), ptr(irms), ptr(dg), outer, red, inner)
     return dg
@@ -92,7 +126,11 @@ def batchnorm(tensor1, gamma, beta, running_mean, running_std, training=False):
     """
     tensor1 = contiguous_f32(tensor1)
     gamma = contiguous_f32(gamma, "gamma")
+    validation.check_rank(tensor1.shape, min_rank=4, max_rank=4, name="batchnorm input")
     B, Cc, H, W = tensor1.shape
+    for t, name in ((gamma, "gamma"), (beta, "beta"), (running_mean, "running_mean"),
+                    (running_std, "running_std")):
+        _check_param(t, Cc, name)
     y = empty(tensor1.shape)
     mean = empty((Cc,))
     istd = empty((Cc,))
@@ -106,7 +144,12 @@ def batchnormdx(grad, tensor1, gamma, dgamma, dbeta, saved_mean, saved_std):
     tensor1 = contiguous_f32(tensor1)
     gamma = contiguous_f32(gamma, "gamma")
     grad = contiguous_f32(grad, "grad")
+    validation.check_rank(tensor1.shape, min_rank=4, max_rank=4, name="batchnorm input")
     B, Cc, H, W = tensor1.shape
+    validation.check_same_shape(grad.shape, tensor1.shape, name="grad and input")
+    for t, name in ((gamma, "gamma"), (dgamma, "dgamma"), (dbeta, "dbeta"),
+                    (saved_mean, "saved_mean"), (saved_std, "saved_std")):
+        _check_param(t, Cc, name)
     dx = empty(tensor1.shape)
     call("wxx_batchnormdx", ptr(grad), ptr(tensor1), ptr(gamma), ptr(dgamma), ptr(dbeta),
          ptr(saved_mean), ptr(saved_std), ptr(dx), B, Cc, H * W)
@@ -116,7 +159,11 @@ def batchnormdx(grad, tensor1, gamma, dgamma, dbeta, saved_mean, saved_std):
 def batchnormdg(grad, tensor1, saved_mean, saved_std):
     tensor1 = contiguous_f32(tensor1)
     grad = contiguous_f32(grad, "grad")
+    validation.check_rank(tensor1.shape, min_rank=4, max_rank=4, name="batchnorm input")
     B, Cc, H, W = tensor1.shape
+    validation.check_same_shape(grad.shape, tensor1.shape, name="grad and input")
+    _check_param(saved_mean, Cc, "saved_mean")
+    _check_param(saved_std, Cc, "saved_std")
     dg = empty((Cc,))
     db = empty((Cc,))
     call("wxx_batchnormdg", ptr(grad), ptr(tensor1), ptr(saved_mean), ptr(saved_std), ptr(dg),

@@ -154,6 +154,10 @@ def log(tensor1):
 
 def mul_backward(grad, tensor_a, tensor_b):
     """``(grad * b, grad * a)`` in one pass (all three same-shape and contiguous)."""
+    validation.check_same_shape(grad.shape, tensor_a.shape, tensor_b.shape,
+                                name="mul_backward operands")
+    if not (grad.is_contiguous() and tensor_a.is_contiguous() and tensor_b.is_contiguous()):
+        raise ValueError("mul_backward expects contiguous operands")
     n = validation.numel(grad.shape)
     da = empty(grad.shape)
     db = empty(grad.shape)

@@ -71,6 +71,13 @@ def maxmin_backward(grad_output, indices, input_shape, axis=None):
     if not indices.is_contiguous():
         indices = indices.contiguous()
     outer, red, inner, _ = _get_reduce_dims(input_shape, axis)
+    for t, name in ((grad_output, "grad_output"), (indices, "indices")):
+        if validation.numel(t.shape) != outer * inner:
+            raise ValueError(
+                f"{name} has {validation.numel(t.shape)} elements, expected {outer * inner}"
+            )
+    if indices.type != "u32":
+        raise TypeError(f"indices must be u32, got {indices.type!r}")
     out = empty(tuple(input_shape))
     call("wxx_maxmin_backward", ptr(grad_output), ptr(indices), ptr(out), outer, red, inner)
     return out
@@ -100,4 +107,3 @@ def std(tensor1, axis=None, keepdims=False, *, keepdim=None):
 
 
 __all__ = ["sum", "mean", "sumsq", "max", "min", "maxmin_backward", "var", "std"]
-_ = validation

@@ -167,6 +167,11 @@ def unfolddx(grad, input_shape, dimension, size, step=1):
     suffix = math.prod(input_shape[dim + 1:]) if dim + 1 < len(input_shape) else 1
     length = input_shape[dim]
     windows = (length - size) // step + 1
+    expect = prefix * windows * suffix * size
+    if validation.numel(grad.shape) != expect:
+        raise ValueError(
+            f"unfold grad has {validation.numel(grad.shape)} elements, expected {expect}"
+        )
     out = empty(tuple(input_shape))
     call("wxx_unfolddx", ptr(grad), ptr(out), prefix, length, suffix, windows, size, step)
     return out
@@ -368,14 +373,34 @@ def uniform(a, b, shape):
     return Tensor(shape, data=values.tobytes())
 
 
+def empty_like_shape(shape, dtype="f32"):
+    """A new uninitialised tensor of ``shape`` and ``dtype``."""
+    return empty(list(shape), dtype=dtype)
+
+
+def broadcast_to(tensor1, shape, scale=1.0):
+    """Dense ``tensor1 * scale`` broadcast to ``shape`` in one strided kernel
+    (the backward of sum / mean)."""
+    shape = list(validation.normalize_shape(shape, name="shape"))
+    rank = validation.check_rank(shape, name="broadcast_to shape")
+    from ..backend.dispatch import view_broadcast_strides
+
+    strides = view_broadcast_strides(tensor1, shape)
+    out = empty(shape)
+    if validation.numel(shape):
+        call("wxx_broadcast_scale", ptr(out), ptr(tensor1), rank, i64_array(shape),
+             i64_array(strides), float(scale))
+    return out
+
+
 def from_numpy(array, dtype=np.float32):
     """Upload a NumPy array (float32, or uint32 when ``dtype`` is ``np.uint32``)."""
     if dtype == np.uint32:
         array = np.ascontiguousarray(array, dtype=np.uint32)
-        buf = buffer_pool.create_buffer_with_data(memoryview(array).cast("B"), label="from_numpy")
+        buf = buffer_pool.create_buffer_with_data(array, label="from_numpy")
         return Tensor(list(array.shape), buf, dtype="u32")
     array = np.ascontiguousarray(array, dtype=np.float32)
-    buf = buffer_pool.create_buffer_with_data(memoryview(array).cast("B"), label="from_numpy")
+    buf = buffer_pool.create_buffer_with_data(array, label="from_numpy")
     return Tensor(list(array.shape), buf)
 
 
