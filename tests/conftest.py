@@ -31,7 +31,9 @@ if _EMU:
 # they run unchanged on the GPU.
 _EMU_HEAVY = ("test_matmul_config2_sizes", "test_softmax[shape2", "test_softmax[shape1-",
               "test_layernorm_fwd_bwd[shape1-", "test_rmsnorm_fwd_bwd[shape1-",
-              "test_fft_full_size_properties", "test_hyena_shapes")
+              "test_fft_full_size_properties", "test_hyena_shapes",
+              "test_embed_bit_exact_and_embeddx[50304", "test_dropout_bit_exact[6291459",
+              "test_cceloss[64-50304")
 
 
 def pytest_configure(config):
