@@ -70,6 +70,47 @@ int wxx_matmul_add(const float* A, const float* B, const float* bias, float* C, 
                    int64_t N, int64_t K, int64_t batch, int64_t sA, int64_t sB, int64_t sBias,
                    int bias_mode, int transpose_A, int transpose_B, int tile);
 
+/* ---- B: convolution and pooling (functional/convolution.py), NCHW f32.
+ *      Output size Ho = (H + 2ph - dh(KH-1) - 1)/sh + 1 (conv), (H + 2ph - KH)/sh + 1 (pool). */
+/* functional.conv2d (functional/convolution.py:658-729); bias may be null */
+int wxx_conv2d(const float* X, const float* W, const float* bias, float* Y, int64_t B,
+               int64_t Cin, int64_t H, int64_t Wd, int64_t Cout, int64_t KH, int64_t KW,
+               int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw);
+/* functional.conv2ddx (functional/convolution.py:732-793): dX from dY and W */
+int wxx_conv2ddx(const float* dY, const float* W, float* dX, int64_t B, int64_t Cin, int64_t H,
+                 int64_t Wd, int64_t Cout, int64_t KH, int64_t KW, int64_t sh, int64_t sw,
+                 int64_t ph, int64_t pw, int64_t dh, int64_t dw);
+/* functional.conv2ddw + conv2ddw_reduce (functional/convolution.py:796-908): dW from dY and X */
+int wxx_conv2ddw(const float* dY, const float* X, float* dW, int64_t B, int64_t Cin, int64_t H,
+                 int64_t Wd, int64_t Cout, int64_t KH, int64_t KW, int64_t sh, int64_t sw,
+                 int64_t ph, int64_t pw, int64_t dh, int64_t dw);
+/* functional.maxpool2d (avg 0) / avgpool2d (avg 1) (functional/convolution.py:60-192) and
+ * maxpool1d / avgpool1d (:195-321, as H = 1); idx (u32 flat input index) may be null */
+int wxx_pool2d(const float* x, float* y, uint32_t* idx, int64_t B, int64_t C, int64_t H,
+               int64_t W, int64_t KH, int64_t KW, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+               int avg);
+/* functional.maxpool2ddx (avg 0, idx required) / avgpool2ddx (avg 1)
+ * (functional/convolution.py:425-476, 601-653) and the 1-D backwards (:324-422) */
+int wxx_pool2d_backward(const float* dy, const uint32_t* idx, float* dx, int64_t B, int64_t C,
+                        int64_t H, int64_t W, int64_t KH, int64_t KW, int64_t sh, int64_t sw,
+                        int64_t ph, int64_t pw, int avg);
+/* functional.adaptive_avgpool2d (functional/convolution.py:490-543) */
+int wxx_adaptive_avgpool2d(const float* x, float* y, int64_t B, int64_t C, int64_t H, int64_t W,
+                           int64_t Ho, int64_t Wo);
+/* functional.adaptive_avgpool2ddx (functional/convolution.py:546-598) */
+int wxx_adaptive_avgpool2ddx(const float* dy, float* dx, int64_t B, int64_t C, int64_t H,
+                             int64_t W, int64_t Ho, int64_t Wo);
+/* functional.causal_conv1d (functional/convolution.py:1188-1257); x is a strided
+ * (B, D, L) view: base pointer, element offset and strides */
+int wxx_causal_conv1d(const float* x, int64_t x_off, int64_t sb, int64_t sc, int64_t sl,
+                      const float* w, const float* bias, float* y, int64_t B, int64_t D,
+                      int64_t L, int64_t KS);
+/* functional.causal_conv1d_backward (functional/convolution.py:1260-1351);
+ * dw and db are both null when the weight gradient is not needed */
+int wxx_causal_conv1d_backward(const float* dy, const float* x, int64_t x_off, int64_t sb,
+                               int64_t sc, int64_t sl, const float* w, float* dx, float* dw,
+                               float* db, int64_t B, int64_t D, int64_t L, int64_t KS);
+
 /* ---- D: reductions over (outer, reduce, inner) ------------------------- */
 /* functional.sum / mean / sumsq (functional/reductions.py:27-197); mode 0/1/2 */
 int wxx_reduce(const float* x, float* out, int64_t outer, int64_t reduce, int64_t inner,

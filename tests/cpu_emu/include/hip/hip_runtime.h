@@ -108,6 +108,9 @@ inline T __shfl_xor(T v, int off, int width = 64) {
   return r;
 }
 
+// Wave-uniform value: every lane of the emulated wave already holds it.
+inline int __builtin_amdgcn_readfirstlane(int v) { return v; }
+
 inline float __int_as_float(int v) { float f; std::memcpy(&f, &v, 4); return f; }
 inline float __uint_as_float(uint32_t v) { float f; std::memcpy(&f, &v, 4); return f; }
 inline int __float_as_int(float f) { int v; std::memcpy(&v, &f, 4); return v; }

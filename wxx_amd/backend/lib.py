@@ -45,6 +45,17 @@ SIGNATURES = {
         I32,
         [P, P, P, P, I64, I64, I64, I64, I64, I64, I64, I32, I32, I32, I32],
     ),
+    # convolution / pooling
+    "wxx_conv2d": (I32, [P, P, P, P] + [I64] * 13),
+    "wxx_conv2ddx": (I32, [P, P, P] + [I64] * 13),
+    "wxx_conv2ddw": (I32, [P, P, P] + [I64] * 13),
+    "wxx_pool2d": (I32, [P, P, P] + [I64] * 10 + [I32]),
+    "wxx_pool2d_backward": (I32, [P, P, P] + [I64] * 10 + [I32]),
+    "wxx_adaptive_avgpool2d": (I32, [P, P] + [I64] * 6),
+    "wxx_adaptive_avgpool2ddx": (I32, [P, P] + [I64] * 6),
+    "wxx_causal_conv1d": (I32, [P, I64, I64, I64, I64, P, P, P, I64, I64, I64, I64]),
+    "wxx_causal_conv1d_backward": (I32, [P, P, I64, I64, I64, I64, P, P, P, P, I64, I64, I64,
+                                         I64]),
     # reductions
     "wxx_reduce": (I32, [P, P, I64, I64, I64, I32]),
     "wxx_reduce_minmax": (I32, [P, P, P, I64, I64, I64, I32]),

@@ -1,0 +1,388 @@
+// Pooling (max / average / adaptive average over NCHW, 1-D as H = 1) and the
+// depthwise causal 1-D convolution of Hyena, forward and backward.
+//
+// Reference semantics:
+//  * maxpool2d (src/wxx/shaders/layers/maxpool2d.wgsl:28-70, host
+//    src/wxx/functional/convolution.py:60-125): window max starting from
+//    -1e38 with index 0xFFFFFFFF, strict '>' in (kh, kw) order, padded cells
+//    skipped; the index is the flat input index b*C*H*W + c*H*W + ih*W + iw.
+//  * maxpool2ddx (maxpool2ddx.wgsl): each input cell sums dY over the output
+//    windows that can contain it (ho, wo ascending) whose index equals it.
+//  * avgpool2d (avgpool2d.wgsl): mean over in-range cells
+//    (count_include_pad = False), 0 for an empty window; optional max index.
+//  * avgpool2ddx (avgpool2ddx.wgsl): sum of dY / valid_count over the windows
+//    that can contain the cell.
+//  * adaptive_avgpool2d / dx (adaptive_avgpool2d.wgsl, adaptive_avgpool2ddx.wgsl):
+//    window [floor(o in / out), ceil((o+1) in / out)), and the backward over
+//    o in [floor(i out / in), floor(((i+1) out - 1) / in)].
+//  * maxpool1d / avgpool1d (+dx) are the 2-D kernels with H = 1.
+//  * causal_conv1d (helpers/causal_conv1d.wgsl): y[b,d,n] = bias[d] +
+//    sum_k w[d,k] x[b,d,n-k] over n >= k, x a strided view;
+//    backward (causal_conv1d_backward.wgsl): dx[b,d,n] = sum_k w[d,k]
+//    dy[b,d,n+k] (n+k < L); dw[d,k] = sum_{b, n>=k} dy[b,d,n] x[b,d,n-k];
+//    db[d] = sum_{b,n} dy[b,d,n].
+//
+// MI355X design: the pools are one thread per output (or per input cell for
+// the backward, a gather with no atomics, so results are deterministic),
+// 32-bit index math.  The causal conv's weight / bias gradients are reduced
+// per channel by whole workgroups (the reference gives each (d, k) one
+// thread that walks B*L elements serially).
+#include "common.h"
+
+namespace {
+
+constexpr int kBlock = 256;
+
+struct PoolArgs {
+  int B, C, H, W, Ho, Wo, KH, KW, sh, sw, ph, pw;
+};
+
+template <bool AVG>
+__global__ __launch_bounds__(kBlock) void pool2d_kernel(const float* __restrict__ x,
+                                                         float* __restrict__ y,
+                                                         uint32_t* __restrict__ idx, PoolArgs a,
+                                                         int64_t total) {
+  for (int64_t o = (int64_t)blockIdx.x * kBlock + threadIdx.x; o < total;
+       o += (int64_t)gridDim.x * kBlock) {
+    int64_t rem = o;
+    const int wo = (int)(rem % a.Wo);
+    rem /= a.Wo;
+    const int ho = (int)(rem % a.Ho);
+    rem /= a.Ho;
+    const int64_t bc = rem;  // b * C + c
+    const int64_t base = bc * a.H * a.W;
+    const int h0 = ho * a.sh - a.ph, w0 = wo * a.sw - a.pw;
+    float best = -1e38f, sum = 0.f, cnt = 0.f;
+    uint32_t bi = 0xFFFFFFFFu;
+    for (int kh = 0; kh < a.KH; ++kh) {
+      const int ih = h0 + kh;
+      if (ih < 0 || ih >= a.H) continue;
+      for (int kw = 0; kw < a.KW; ++kw) {
+        const int iw = w0 + kw;
+        if (iw < 0 || iw >= a.W) continue;
+        const int64_t in = base + (int64_t)ih * a.W + iw;
+        const float v = x[in];
+        if (AVG) {
+          sum += v;
+          cnt += 1.f;
+        }
+        if (v > best) {
+          best = v;
+          bi = (uint32_t)in;
+        }
+      }
+    }
+    y[o] = AVG ? (cnt > 0.f ? sum / cnt : 0.f) : best;
+    if (idx) idx[o] = bi;
+  }
+}
+
+// Output rows [lo, hi] whose windows may contain input coordinate i
+// (the reference's signed-division bounds, truncating like WGSL i32 '/').
+__device__ __forceinline__ void out_range(int i, int p, int k, int s, int n_out, int& lo, int& hi) {
+  const int ip = i + p;
+  lo = max(0, (ip - k + s) / s);
+  hi = min(n_out - 1, ip / s);
+}
+
+template <bool AVG>
+__global__ __launch_bounds__(kBlock) void pool2d_dx_kernel(const float* __restrict__ dy,
+                                                            const uint32_t* __restrict__ idx,
+                                                            float* __restrict__ dx, PoolArgs a,
+                                                            int64_t total) {
+  for (int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * kBlock) {
+    int64_t rem = e;
+    const int iw = (int)(rem % a.W);
+    rem /= a.W;
+    const int ih = (int)(rem % a.H);
+    rem /= a.H;
+    const int64_t bc = rem;
+    int hlo, hhi, wlo, whi;
+    out_range(ih, a.ph, a.KH, a.sh, a.Ho, hlo, hhi);
+    out_range(iw, a.pw, a.KW, a.sw, a.Wo, wlo, whi);
+    float acc = 0.f;
+    if (hlo <= hhi && wlo <= whi) {
+      const int64_t obase = bc * a.Ho * a.Wo;
+      for (int ho = hlo; ho <= hhi; ++ho) {
+        const int hs = ho * a.sh - a.ph;
+        for (int wo = wlo; wo <= whi; ++wo) {
+          const int64_t o = obase + (int64_t)ho * a.Wo + wo;
+          if (AVG) {
+            const int ws = wo * a.sw - a.pw;
+            const int vh = min(a.H, hs + a.KH) - max(0, hs);
+            const int vw = min(a.W, ws + a.KW) - max(0, ws);
+            const float cnt = (float)(vh * vw);
+            if (cnt > 0.f) acc += dy[o] / cnt;
+          } else if (idx[o] == (uint32_t)e) {
+            acc += dy[o];
+          }
+        }
+      }
+    }
+    dx[e] = acc;
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void adaptive_avg_kernel(const float* __restrict__ x,
+                                                               float* __restrict__ y, int H, int W,
+                                                               int Ho, int Wo, int64_t total) {
+  for (int64_t o = (int64_t)blockIdx.x * kBlock + threadIdx.x; o < total;
+       o += (int64_t)gridDim.x * kBlock) {
+    const int ow = (int)(o % Wo);
+    const int64_t t0 = o / Wo;
+    const int oh = (int)(t0 % Ho);
+    const int64_t bc = t0 / Ho;
+    const int hs = (oh * H) / Ho, he = ((oh + 1) * H + Ho - 1) / Ho;
+    const int ws = (ow * W) / Wo, we = ((ow + 1) * W + Wo - 1) / Wo;
+    const float* xb = x + bc * H * W;
+    float acc = 0.f;
+    for (int h = hs; h < he; ++h)
+      for (int w = ws; w < we; ++w) acc += xb[h * W + w];
+    y[o] = acc / (float)((he - hs) * (we - ws));
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void adaptive_avg_dx_kernel(const float* __restrict__ dy,
+                                                                  float* __restrict__ dx, int H,
+                                                                  int W, int Ho, int Wo,
+                                                                  int64_t total) {
+  for (int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * kBlock) {
+    const int iw = (int)(e % W);
+    const int64_t t0 = e / W;
+    const int ih = (int)(t0 % H);
+    const int64_t bc = t0 / H;
+    const int ohs = (ih * Ho) / H, ohe = ((ih + 1) * Ho - 1) / H;
+    const int ows = (iw * Wo) / W, owe = ((iw + 1) * Wo - 1) / W;
+    const float* gb = dy + bc * Ho * Wo;
+    float acc = 0.f;
+    for (int oh = ohs; oh <= ohe; ++oh) {
+      const int hs = (oh * H) / Ho, he = ((oh + 1) * H + Ho - 1) / Ho;
+      for (int ow = ows; ow <= owe; ++ow) {
+        const int ws = (ow * W) / Wo, we = ((ow + 1) * W + Wo - 1) / Wo;
+        const float cnt = (float)((he - hs) * (we - ws));
+        acc += gb[oh * Wo + ow] / cnt;
+      }
+    }
+    dx[e] = acc;
+  }
+}
+
+// ---- depthwise causal conv1d ------------------------------------------------
+
+struct View3 {
+  int64_t off, sb, sc, sl;
+};
+
+__global__ __launch_bounds__(kBlock) void causal_conv1d_kernel(const float* __restrict__ x,
+                                                                View3 v,
+                                                                const float* __restrict__ w,
+                                                                const float* __restrict__ bias,
+                                                                float* __restrict__ y, int D,
+                                                                int L, int KS, int64_t total) {
+  for (int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * kBlock) {
+    const int n = (int)(e % L);
+    const int64_t r = e / L;
+    const int d = (int)(r % D);
+    const int64_t b = r / D;
+    float acc = bias[d];
+    const float* xr = x + v.off + b * v.sb + d * v.sc;
+    for (int k = 0; k < KS; ++k)
+      if (n >= k) acc = fmaf(w[d * KS + k], xr[(int64_t)(n - k) * v.sl], acc);
+    y[e] = acc;
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void causal_conv1d_dx_kernel(const float* __restrict__ dy,
+                                                                   const float* __restrict__ w,
+                                                                   float* __restrict__ dx, int D,
+                                                                   int L, int KS, int64_t total) {
+  for (int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * kBlock) {
+    const int n = (int)(e % L);
+    const int d = (int)((e / L) % D);
+    float acc = 0.f;
+    for (int k = 0; k < KS; ++k)
+      if (n + k < L) acc = fmaf(w[d * KS + k], dy[e + k], acc);
+    dx[e] = acc;
+  }
+}
+
+// One workgroup per (d, k) weight (k == KS is the bias): a block-wide sum
+// over (b, n), b-major then n, combined by a fixed tree (deterministic).
+__global__ __launch_bounds__(kBlock) void causal_conv1d_dw_kernel(const float* __restrict__ dy,
+                                                                   const float* __restrict__ x,
+                                                                   View3 v, float* __restrict__ dw,
+                                                                   float* __restrict__ db, int B,
+                                                                   int D, int L, int KS) {
+  __shared__ float red[kBlock / 64];
+  const int d = blockIdx.x / (KS + 1);
+  const int k = blockIdx.x % (KS + 1);
+  float acc = 0.f;
+  for (int b = 0; b < B; ++b) {
+    const float* g = dy + ((int64_t)b * D + d) * L;
+    if (k == KS) {
+      for (int n = threadIdx.x; n < L; n += kBlock) acc += g[n];
+    } else {
+      const float* xr = x + v.off + b * v.sb + d * v.sc;
+      for (int n = k + threadIdx.x; n < L; n += kBlock)
+        acc = fmaf(g[n], xr[(int64_t)(n - k) * v.sl], acc);
+    }
+  }
+  acc = wxx::block_sum(acc, red);
+  if (threadIdx.x == 0) {
+    if (k == KS)
+      db[d] = acc;
+    else
+      dw[d * KS + k] = acc;
+  }
+}
+
+int pool_setup(PoolArgs& a, int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH, int64_t KW,
+               int64_t sh, int64_t sw, int64_t ph, int64_t pw) {
+  WXX_REQUIRE(B >= 0 && C >= 0 && H >= 1 && W >= 1 && KH >= 1 && KW >= 1 && sh >= 1 && sw >= 1 &&
+                  ph >= 0 && pw >= 0,
+              "pool: bad shape / kernel / stride / padding");
+  const int64_t Ho = (H + 2 * ph - KH) / sh + 1, Wo = (W + 2 * pw - KW) / sw + 1;
+  WXX_REQUIRE(H + 2 * ph - KH >= 0 && W + 2 * pw - KW >= 0 && Ho >= 1 && Wo >= 1,
+              "pooling produces an empty output");
+  WXX_REQUIRE(B * C * H * W < (int64_t(1) << 32) - 1, "pool input too large for u32 indices");
+  a = PoolArgs{(int)B, (int)C, (int)H, (int)W, (int)Ho, (int)Wo, (int)KH, (int)KW,
+               (int)sh,  (int)sw, (int)ph, (int)pw};
+  return WXX_OK;
+}
+
+}  // namespace
+
+// Replaces functional.maxpool2d (avg = 0) and avgpool2d (avg = 1)
+// (reference src/wxx/functional/convolution.py:60-192); maxpool1d / avgpool1d
+// (:195-321) call it with H = 1.  idx may be null (no indices requested).
+WXX_API int wxx_pool2d(const float* x, float* y, uint32_t* idx, int64_t B, int64_t C, int64_t H,
+                       int64_t W, int64_t KH, int64_t KW, int64_t sh, int64_t sw, int64_t ph,
+                       int64_t pw, int avg) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(x && y, "null pointer");
+  PoolArgs a;
+  int rc = pool_setup(a, B, C, H, W, KH, KW, sh, sw, ph, pw);
+  if (rc) return rc;
+  const int64_t total = B * C * (int64_t)a.Ho * a.Wo;
+  if (total == 0) return WXX_OK;
+  const dim3 g(wxx::grid_1d(total, kBlock, 65536));
+  if (avg)
+    hipLaunchKernelGGL(pool2d_kernel<true>, g, dim3(kBlock), 0, wxx::stream(), x, y, idx, a, total);
+  else
+    hipLaunchKernelGGL(pool2d_kernel<false>, g, dim3(kBlock), 0, wxx::stream(), x, y, idx, a,
+                       total);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// Replaces functional.maxpool2ddx (avg = 0, idx required) and avgpool2ddx
+// (avg = 1) (reference src/wxx/functional/convolution.py:425-476, 601-653);
+// maxpool1ddx / avgpool1ddx (:324-422) call it with H = 1.
+WXX_API int wxx_pool2d_backward(const float* dy, const uint32_t* idx, float* dx, int64_t B,
+                                int64_t C, int64_t H, int64_t W, int64_t KH, int64_t KW,
+                                int64_t sh, int64_t sw, int64_t ph, int64_t pw, int avg) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(dy && dx && (avg || idx), "null pointer");
+  PoolArgs a;
+  int rc = pool_setup(a, B, C, H, W, KH, KW, sh, sw, ph, pw);
+  if (rc) return rc;
+  const int64_t total = B * C * H * W;
+  if (total == 0) return WXX_OK;
+  const dim3 g(wxx::grid_1d(total, kBlock, 65536));
+  if (avg)
+    hipLaunchKernelGGL(pool2d_dx_kernel<true>, g, dim3(kBlock), 0, wxx::stream(), dy, idx, dx, a,
+                       total);
+  else
+    hipLaunchKernelGGL(pool2d_dx_kernel<false>, g, dim3(kBlock), 0, wxx::stream(), dy, idx, dx,
+                       a, total);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// Replaces functional.adaptive_avgpool2d (reference
+// src/wxx/functional/convolution.py:490-543).
+WXX_API int wxx_adaptive_avgpool2d(const float* x, float* y, int64_t B, int64_t C, int64_t H,
+                                   int64_t W, int64_t Ho, int64_t Wo) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(x && y, "null pointer");
+  WXX_REQUIRE(B >= 0 && C >= 0 && H >= 1 && W >= 1 && Ho >= 1 && Wo >= 1,
+              "adaptive_avgpool2d: bad shape");
+  WXX_REQUIRE((Ho + 1) * H < (int64_t(1) << 31) && (Wo + 1) * W < (int64_t(1) << 31),
+              "adaptive_avgpool2d: sizes too large");
+  const int64_t total = B * C * Ho * Wo;
+  if (total == 0) return WXX_OK;
+  hipLaunchKernelGGL(adaptive_avg_kernel, dim3(wxx::grid_1d(total, kBlock, 65536)), dim3(kBlock),
+                     0, wxx::stream(), x, y, (int)H, (int)W, (int)Ho, (int)Wo, total);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// Replaces functional.adaptive_avgpool2ddx (reference
+// src/wxx/functional/convolution.py:546-598).
+WXX_API int wxx_adaptive_avgpool2ddx(const float* dy, float* dx, int64_t B, int64_t C, int64_t H,
+                                     int64_t W, int64_t Ho, int64_t Wo) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(dy && dx, "null pointer");
+  WXX_REQUIRE(B >= 0 && C >= 0 && H >= 1 && W >= 1 && Ho >= 1 && Wo >= 1,
+              "adaptive_avgpool2ddx: bad shape");
+  WXX_REQUIRE((Ho + 1) * H < (int64_t(1) << 31) && (Wo + 1) * W < (int64_t(1) << 31),
+              "adaptive_avgpool2ddx: sizes too large");
+  const int64_t total = B * C * H * W;
+  if (total == 0) return WXX_OK;
+  hipLaunchKernelGGL(adaptive_avg_dx_kernel, dim3(wxx::grid_1d(total, kBlock, 65536)),
+                     dim3(kBlock), 0, wxx::stream(), dy, dx, (int)H, (int)W, (int)Ho, (int)Wo,
+                     total);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// Replaces functional.causal_conv1d (reference
+// src/wxx/functional/convolution.py:1188-1257); x is a strided (B, D, L) view
+// given by its element offset and strides.
+WXX_API int wxx_causal_conv1d(const float* x, int64_t x_off, int64_t sb, int64_t sc, int64_t sl,
+                              const float* w, const float* bias, float* y, int64_t B, int64_t D,
+                              int64_t L, int64_t KS) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(x && w && bias && y, "null pointer");
+  WXX_REQUIRE(B >= 0 && D >= 1 && L >= 1 && KS >= 1 && D * KS < (int64_t(1) << 31) &&
+                  L < (int64_t(1) << 31),
+              "causal_conv1d: bad shape");
+  const int64_t total = B * D * L;
+  if (total == 0) return WXX_OK;
+  View3 v{x_off, sb, sc, sl};
+  hipLaunchKernelGGL(causal_conv1d_kernel, dim3(wxx::grid_1d(total, kBlock, 65536)), dim3(kBlock),
+                     0, wxx::stream(), x, v, w, bias, y, (int)D, (int)L, (int)KS, total);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// Replaces functional.causal_conv1d_backward (reference
+// src/wxx/functional/convolution.py:1260-1351).  dy is contiguous (B, D, L);
+// dw / db may be null when the weight gradient is not needed.
+WXX_API int wxx_causal_conv1d_backward(const float* dy, const float* x, int64_t x_off, int64_t sb,
+                                       int64_t sc, int64_t sl, const float* w, float* dx,
+                                       float* dw, float* db, int64_t B, int64_t D, int64_t L,
+                                       int64_t KS) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(dy && x && w && dx, "null pointer");
+  WXX_REQUIRE((dw == nullptr) == (db == nullptr), "dw and db must both be given or both null");
+  WXX_REQUIRE(B >= 0 && D >= 1 && L >= 1 && KS >= 1 && D * (KS + 1) < (int64_t(1) << 31) &&
+                  L < (int64_t(1) << 31) && B < (int64_t(1) << 31),
+              "causal_conv1d_backward: bad shape");
+  const int64_t total = B * D * L;
+  hipStream_t s = wxx::stream();
+  if (total > 0)
+    hipLaunchKernelGGL(causal_conv1d_dx_kernel, dim3(wxx::grid_1d(total, kBlock, 65536)),
+                       dim3(kBlock), 0, s, dy, w, dx, (int)D, (int)L, (int)KS, total);
+  if (dw) {
+    View3 v{x_off, sb, sc, sl};
+    hipLaunchKernelGGL(causal_conv1d_dw_kernel, dim3((unsigned)(D * (KS + 1))), dim3(kBlock), 0,
+                       s, dy, x, v, dw, db, (int)B, (int)D, (int)L, (int)KS);
+  }
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
