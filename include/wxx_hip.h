@@ -84,6 +84,23 @@ int wxx_conv2ddx(const float* dY, const float* W, float* dX, int64_t B, int64_t 
 int wxx_conv2ddw(const float* dY, const float* X, float* dW, int64_t B, int64_t Cin, int64_t H,
                  int64_t Wd, int64_t Cout, int64_t KH, int64_t KW, int64_t sh, int64_t sw,
                  int64_t ph, int64_t pw, int64_t dh, int64_t dw);
+/* functional.conv2dtranspose (functional/convolution.py:911-1000): X (B,Cin,H,Wd),
+ * W (Cin,Cout,KH,KW), Y (B,Cout,Hout,Wout) with
+ * Hout = (H-1)sh - 2ph + dh(KH-1) + output_padding_h + 1; bias may be null */
+int wxx_conv2dtranspose(const float* X, const float* W, const float* bias, float* Y, int64_t B,
+                        int64_t Cin, int64_t H, int64_t Wd, int64_t Cout, int64_t KH, int64_t KW,
+                        int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw,
+                        int64_t Hout, int64_t Wout);
+/* functional.conv2dtranspose_dx (functional/convolution.py:1003-1064) */
+int wxx_conv2dtranspose_dx(const float* dY, const float* W, float* dX, int64_t B, int64_t Cin,
+                           int64_t H, int64_t Wd, int64_t Cout, int64_t KH, int64_t KW,
+                           int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw,
+                           int64_t Hout, int64_t Wout);
+/* functional.conv2dtranspose_dw (functional/convolution.py:1067-1185) */
+int wxx_conv2dtranspose_dw(const float* dY, const float* X, float* dW, int64_t B, int64_t Cin,
+                           int64_t H, int64_t Wd, int64_t Cout, int64_t KH, int64_t KW,
+                           int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw,
+                           int64_t Hout, int64_t Wout);
 /* functional.maxpool2d (avg 0) / avgpool2d (avg 1) (functional/convolution.py:60-192) and
  * maxpool1d / avgpool1d (:195-321, as H = 1); idx (u32 flat input index) may be null */
 int wxx_pool2d(const float* x, float* y, uint32_t* idx, int64_t B, int64_t C, int64_t H,

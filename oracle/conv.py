@@ -216,3 +216,82 @@ def causal_conv1d_backward(dy, x, w):
         dx[:, :, :L - k] += w[None, :, k, None] * dy[:, :, k:]
         dw[:, k] = (dy[:, :, k:] * x[:, :, :L - k]).sum(axis=(0, 2))
     return dx, dw, dy.sum(axis=(0, 2))
+
+
+def conv2dtranspose(X, Wt, stride, padding, dilation, out_hw, bias=None):
+    """Transposed conv (shaders/layers/conv2dtranspose.wgsl): the scatter of every
+    input cell (b, ci, h, w) times W[ci, co, kh, kw] to output
+    (h sh - ph + kh dh, w sw - pw + kw dw), written as a direct loop."""
+    X = np.asarray(X, np.float64)
+    Wt = np.asarray(Wt, np.float64)
+    B, Cin, H, W = X.shape
+    _, Cout, KH, KW = Wt.shape
+    sh, sw = stride
+    ph, pw = padding
+    dh, dw = dilation
+    Ho, Wo = out_hw
+    y = np.zeros((B, Cout, Ho, Wo))
+    for kh in range(KH):
+        for kw in range(KW):
+            for h in range(H):
+                oh = h * sh - ph + kh * dh
+                if oh < 0 or oh >= Ho:
+                    continue
+                for w in range(W):
+                    ow = w * sw - pw + kw * dw
+                    if ow < 0 or ow >= Wo:
+                        continue
+                    y[:, :, oh, ow] += X[:, :, h, w] @ Wt[:, :, kh, kw]
+    if bias is not None:
+        y += np.asarray(bias, np.float64)[None, :, None, None]
+    return y
+
+
+def conv2dtranspose_dx(dY, Wt, stride, padding, dilation, Xshape):
+    """dX[b,ci,h,w] = sum_{co,kh,kw} dY[b,co,h sh - ph + kh dh, ...] W[ci,co,kh,kw]."""
+    dY = np.asarray(dY, np.float64)
+    Wt = np.asarray(Wt, np.float64)
+    B, Cin, H, W = Xshape
+    _, Cout, KH, KW = Wt.shape
+    sh, sw = stride
+    ph, pw = padding
+    dh, dw = dilation
+    Ho, Wo = dY.shape[2], dY.shape[3]
+    dX = np.zeros((B, Cin, H, W))
+    for kh in range(KH):
+        for kw in range(KW):
+            for h in range(H):
+                oh = h * sh - ph + kh * dh
+                if oh < 0 or oh >= Ho:
+                    continue
+                for w in range(W):
+                    ow = w * sw - pw + kw * dw
+                    if ow < 0 or ow >= Wo:
+                        continue
+                    dX[:, :, h, w] += dY[:, :, oh, ow] @ Wt[:, :, kh, kw].T
+    return dX
+
+
+def conv2dtranspose_dw(dY, X, stride, padding, dilation, wshape):
+    """dW[ci,co,kh,kw] = sum_{b,h,w} X[b,ci,h,w] dY[b,co,h sh - ph + kh dh, ...]."""
+    dY = np.asarray(dY, np.float64)
+    X = np.asarray(X, np.float64)
+    Cin, Cout, KH, KW = wshape
+    B, _, H, W = X.shape
+    sh, sw = stride
+    ph, pw = padding
+    dh, dw = dilation
+    Ho, Wo = dY.shape[2], dY.shape[3]
+    dW = np.zeros(wshape)
+    for kh in range(KH):
+        for kw in range(KW):
+            for h in range(H):
+                oh = h * sh - ph + kh * dh
+                if oh < 0 or oh >= Ho:
+                    continue
+                for w in range(W):
+                    ow = w * sw - pw + kw * dw
+                    if ow < 0 or ow >= Wo:
+                        continue
+                    dW[:, :, kh, kw] += X[:, :, h, w].T @ dY[:, :, oh, ow]
+    return dW

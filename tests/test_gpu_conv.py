@@ -191,3 +191,75 @@ def test_causal_conv1d(device, B, D, L, K, view):
     dx2, dw2, db2 = F().causal_conv1d_backward(up(g), xt, up(w), up(b), need_weight_grad=False)
     assert dw2 is None and db2 is None
     assert np.array_equal(dx2.numpy(), dx.numpy())
+
+
+# --------------------------------------------------- transposed convolution
+
+TCONV = [
+    (2, 3, 5, 4, 4, 3, 3, (2, 2), (1, 1), (1, 1), (1, 0)),
+    (1, 2, 3, 3, 5, 2, 2, (2, 2), (0, 0), (1, 1), (0, 0)),
+    (2, 4, 4, 5, 3, 3, 2, (1, 2), (1, 0), (2, 1), (1, 1)),
+    (8, 64, 8, 8, 32, 4, 4, (2, 2), (1, 1), (1, 1), (0, 0)),
+]
+
+
+@pytest.mark.parametrize("case", TCONV)
+def test_conv2dtranspose(device, case):
+    B, Cin, H, W, Cout, KH, KW, s, p, d, op = case
+    r = rng(Cin * 31 + Cout)
+    X = r.standard_normal((B, Cin, H, W)).astype(np.float32)
+    Wt = r.standard_normal((Cin, Cout, KH, KW)).astype(np.float32)
+    b = r.standard_normal(Cout).astype(np.float32)
+    y = F().conv2dtranspose(up(X), up(Wt), s, p, d, op, up(b))
+    Ho = (H - 1) * s[0] - 2 * p[0] + d[0] * (KH - 1) + op[0] + 1
+    Wo = (W - 1) * s[1] - 2 * p[1] + d[1] * (KW - 1) + op[1] + 1
+    assert y.shape == [B, Cout, Ho, Wo]
+    assert_close(y.numpy(), oc.conv2dtranspose(X, Wt, s, p, d, (Ho, Wo), b), **tol(Cin * KH * KW))
+    g = r.standard_normal((B, Cout, Ho, Wo)).astype(np.float32)
+    dx = F().conv2dtranspose_dx(up(g), up(Wt), s, p, d, X.shape, Wt.shape, y.shape)
+    assert_close(dx.numpy(), oc.conv2dtranspose_dx(g, Wt, s, p, d, X.shape),
+                 **tol(Cout * KH * KW))
+    dw = F().conv2dtranspose_dw(up(g), up(X), s, p, d, y.shape, Wt.shape)
+    assert_close(dw.numpy(), oc.conv2dtranspose_dw(g, X, s, p, d, Wt.shape), **tol(B * H * W))
+    with pytest.raises(ValueError):
+        F().conv2dtranspose(up(X), up(Wt), s, p, d, (max(s[0], d[0]), 0))
+
+
+# ---------------------------------------------------------------- autograd
+
+
+def test_conv_pool_autograd_graph(device):
+    """conv -> maxpool -> conv (no bias) -> adaptive avgpool -> sum, backward."""
+    from wxx_amd import autograd
+
+    r = rng(77)
+    X = r.standard_normal((4, 3, 12, 12)).astype(np.float32)
+    W1 = r.standard_normal((8, 3, 3, 3)).astype(np.float32)
+    b1 = r.standard_normal(8).astype(np.float32)
+    W2 = r.standard_normal((5, 8, 3, 3)).astype(np.float32)
+    tx, tw1, tb1, tw2 = up(X), up(W1), up(b1), up(W2)
+    for t in (tx, tw1, tb1, tw2):
+        t.requires_grad = True
+    y1 = autograd.Conv2D(tx, tw1, tb1).forward(tx, tw1, tb1, (1, 1), (1, 1), (1, 1))
+    y2 = autograd.maxpooling2d(y1).forward(y1, (3, 3), (2, 2), (1, 1))
+    y3 = autograd.Conv2D(y2, tw2).forward(y2, tw2, None, (2, 2), (1, 1), (1, 1))
+    y4 = autograd.adaptive_avgpooling2d(y3).forward(y3, (1, 1))
+    loss = y4.sum()
+    loss.backward()
+    # oracle chain, float64, with the same maxpool routing
+    e1 = oc.conv2d(X, W1, (1, 1), (1, 1), (1, 1), b1)
+    e2, i2 = oc.pool2d(e1.astype(np.float32), (3, 3), (2, 2), (1, 1), avg=False)
+    e3 = oc.conv2d(e2, W2, (2, 2), (1, 1), (1, 1))
+    g4 = np.ones((4, 5, 1, 1))
+    g3 = oc.adaptive_avgpool2ddx(g4, e3.shape)
+    gw2 = oc.conv2ddw(g3, e2, (2, 2), (1, 1), (1, 1), W2.shape)
+    g2 = oc.conv2ddx(g3, W2, (2, 2), (1, 1), (1, 1), e2.shape)
+    g1 = oc.pool2d_backward(g2, i2, e1.shape, (3, 3), (2, 2), (1, 1), avg=False)
+    gw1 = oc.conv2ddw(g1, X, (1, 1), (1, 1), (1, 1), W1.shape)
+    gx = oc.conv2ddx(g1, W1, (1, 1), (1, 1), (1, 1), X.shape)
+    assert_close(loss.numpy(), np.array(e3.mean(axis=(2, 3)).sum(), np.float32).reshape(1),
+                 rtol=1e-4, atol=1e-3)
+    assert_close(tw2.grad.numpy(), gw2, **tol(4 * 36))
+    assert_close(tw1.grad.numpy(), gw1, **tol(4 * 144))
+    assert_close(tb1.grad.numpy(), g1.sum(axis=(0, 2, 3)), **tol(4 * 144))
+    assert_close(tx.grad.numpy(), gx, **tol(8 * 9))

@@ -138,3 +138,32 @@ def test_causal_conv1d_matches_torch(B, D, L, K):
     assert_close(dx, tx.grad.numpy(), rtol=1e-12, atol=1e-12)
     assert_close(dw, tw.grad.numpy(), rtol=1e-12, atol=1e-12)
     assert_close(db, tb.grad.numpy(), rtol=1e-12, atol=1e-12)
+
+
+TCONV_CASES = [
+    # (B, Cin, H, W, Cout, KH, KW, stride, padding, dilation, output_padding)
+    (2, 3, 5, 4, 4, 3, 3, (2, 2), (1, 1), (1, 1), (1, 0)),
+    (1, 2, 3, 3, 5, 2, 2, (2, 2), (0, 0), (1, 1), (0, 0)),
+    (2, 4, 4, 5, 3, 3, 2, (1, 2), (1, 0), (2, 1), (1, 1)),
+]
+
+
+@pytest.mark.parametrize("case", TCONV_CASES)
+def test_conv2dtranspose_and_gradients_match_torch(case):
+    B, Cin, H, W, Cout, KH, KW, s, p, d, op = case
+    X = rng(20).standard_normal((B, Cin, H, W))
+    Wt = rng(21).standard_normal((Cin, Cout, KH, KW))
+    b = rng(22).standard_normal(Cout)
+    tx, tw, tb = _t(X, True), _t(Wt, True), _t(b, True)
+    ty = TF.conv_transpose2d(tx, tw, tb, stride=s, padding=p, output_padding=op, dilation=d)
+    Ho = (H - 1) * s[0] - 2 * p[0] + d[0] * (KH - 1) + op[0] + 1
+    Wo = (W - 1) * s[1] - 2 * p[1] + d[1] * (KW - 1) + op[1] + 1
+    assert tuple(ty.shape[2:]) == (Ho, Wo)
+    y = oc.conv2dtranspose(X, Wt, s, p, d, (Ho, Wo), b)
+    assert_close(y, ty.detach().numpy(), rtol=1e-12, atol=1e-12)
+    g = rng(23).standard_normal(y.shape)
+    ty.backward(_t(g))
+    assert_close(oc.conv2dtranspose_dx(g, Wt, s, p, d, X.shape), tx.grad.numpy(),
+                 rtol=1e-12, atol=1e-12)
+    assert_close(oc.conv2dtranspose_dw(g, X, s, p, d, Wt.shape), tw.grad.numpy(),
+                 rtol=1e-12, atol=1e-12)

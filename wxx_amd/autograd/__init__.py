@@ -2,6 +2,16 @@
 reference src/wxx/autograd/__init__.py:1-128)."""
 
 from .function import Function
+from .convolution import (
+    Conv2D,
+    Conv2DTranspose,
+    adaptive_avgpooling2d,
+    avgpooling1d,
+    avgpooling2d,
+    causal_conv1d,
+    maxpooling1d,
+    maxpooling2d,
+)
 from .layers import CrossEntropyLoss, Dropout, Embedding
 from .normalization import batchnorm, meanvarnorm, rmsnorm
 from .pointwise import (

@@ -49,6 +49,9 @@ SIGNATURES = {
     "wxx_conv2d": (I32, [P, P, P, P] + [I64] * 13),
     "wxx_conv2ddx": (I32, [P, P, P] + [I64] * 13),
     "wxx_conv2ddw": (I32, [P, P, P] + [I64] * 13),
+    "wxx_conv2dtranspose": (I32, [P, P, P, P] + [I64] * 15),
+    "wxx_conv2dtranspose_dx": (I32, [P, P, P] + [I64] * 15),
+    "wxx_conv2dtranspose_dw": (I32, [P, P, P] + [I64] * 15),
     "wxx_pool2d": (I32, [P, P, P] + [I64] * 10 + [I32]),
     "wxx_pool2d_backward": (I32, [P, P, P] + [I64] * 10 + [I32]),
     "wxx_adaptive_avgpool2d": (I32, [P, P] + [I64] * 6),

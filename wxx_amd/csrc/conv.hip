@@ -49,12 +49,6 @@ struct ConvArgs {
 constexpr int BK = 16;
 constexpr int kPad = 4;
 
-// Coordinates of output column j for the forward / dX gathers.
-struct ColPos {
-  int b, y, x;  // batch and spatial position (oh, ow) or (ih, iw)
-  bool ok;
-};
-
 template <int MODE, int BI, int BJ>
 __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
   constexpr int WI = BI / 2, WJ = BJ / 2;  // 2 x 2 waves
@@ -230,7 +224,7 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
         const int i = i0 + wi * WI + 32 * x + 8 * (r >> 2) + 4 * half + (r & 3);
         if (i < a.I) {
           float v = acc[x][y][r];
-          if (MODE == kFwd && a.splits == 1 && a.bias) v += a.bias[i];
+          if (MODE != kDw && a.splits == 1 && a.bias) v += a.bias[i];
           a.out[base + (int64_t)i * istride] = v;
         }
       }
@@ -256,7 +250,7 @@ __global__ __launch_bounds__(256) void conv_splitk_reduce_kernel(ConvArgs a,
       const int S = MODE == kFwd ? HoWo : HW;
       const int C = MODE == kFwd ? a.Cout : a.Cin;
       const int b = j / S, pos = j - b * S;
-      if (MODE == kFwd && a.bias) v += a.bias[i];
+      if (a.bias) v += a.bias[i];
       out[((int64_t)b * C + i) * S + pos] = v;
     }
   }
@@ -313,16 +307,24 @@ int dispatch(ConvArgs& a, float* final_out) {
   return launch<MODE, 64, 64>(a, final_out);
 }
 
+// Shapes of a convolution with input (B, Cin, H, W), weight (Cout, Cin, KH, KW)
+// and output (B, Cout, Ho, Wo).  Ho / Wo < 0 means the conv2d formula; a
+// transposed convolution passes its own input size there (with its output
+// padding that size need not follow from the formula).
 int setup(ConvArgs& a, int64_t B, int64_t Cin, int64_t H, int64_t W, int64_t Cout, int64_t KH,
-          int64_t KW, int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw) {
+          int64_t KW, int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw,
+          int64_t Ho = -1, int64_t Wo = -1) {
   WXX_REQUIRE(B >= 0 && Cin >= 1 && H >= 1 && W >= 1 && Cout >= 1 && KH >= 1 && KW >= 1,
               "conv2d: bad shape");
   WXX_REQUIRE(sh >= 1 && sw >= 1 && dh >= 1 && dw >= 1 && ph >= 0 && pw >= 0,
               "conv2d: stride/dilation must be >= 1 and padding >= 0");
-  const int64_t Ho = (H + 2 * ph - dh * (KH - 1) - 1) / sh + 1;
-  const int64_t Wo = (W + 2 * pw - dw * (KW - 1) - 1) / sw + 1;
-  WXX_REQUIRE(H + 2 * ph - dh * (KH - 1) - 1 >= 0 && W + 2 * pw - dw * (KW - 1) - 1 >= 0,
-              "conv2d: kernel larger than the padded input");
+  if (Ho < 0) {
+    WXX_REQUIRE(H + 2 * ph - dh * (KH - 1) - 1 >= 0 && W + 2 * pw - dw * (KW - 1) - 1 >= 0,
+                "conv2d: kernel larger than the padded input");
+    Ho = (H + 2 * ph - dh * (KH - 1) - 1) / sh + 1;
+    Wo = (W + 2 * pw - dw * (KW - 1) - 1) / sw + 1;
+  }
+  WXX_REQUIRE(Ho >= 1 && Wo >= 1, "conv2d: empty output");
   const int64_t lim = (int64_t(1) << 31) - 1;
   WXX_REQUIRE(B * Cin * H * W < lim && B * Cout * Ho * Wo < lim && Cout * Cin * KH * KW < lim,
               "conv2d: tensor too large for 32-bit indexing");
@@ -397,6 +399,74 @@ WXX_API int wxx_conv2ddw(const float* dY, const float* X, float* dW, int64_t B, 
   if (B == 0) return wxx_fill_u32(dW, Cout * Cin * KH * KW, 0u);
   a.P = dY;
   a.Q = X;
+  a.I = a.Cout;
+  a.J = a.Cin * a.KH * a.KW;
+  a.K = a.B * a.Ho * a.Wo;
+  return dispatch<kDw>(a, dW);
+}
+
+// Transposed convolution: X (B, Cin, H, W), W (Cin, Cout, KH, KW), output
+// (B, Cout, Hout, Wout).  It is the input gradient of the convolution that maps
+// (B, Cout, Hout, Wout) to (B, Cin, H, W) with the same weight, so it runs on
+// the dX gather with that convolution's shapes (and a bias epilogue).
+
+// Replaces functional.conv2dtranspose (reference
+// src/wxx/functional/convolution.py:911-1000); bias may be null.
+WXX_API int wxx_conv2dtranspose(const float* X, const float* Wt, const float* bias, float* Y,
+                                int64_t B, int64_t Cin, int64_t H, int64_t W, int64_t Cout,
+                                int64_t KH, int64_t KW, int64_t sh, int64_t sw, int64_t ph,
+                                int64_t pw, int64_t dh, int64_t dw, int64_t Hout, int64_t Wout) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(X && Wt && Y, "null pointer");
+  ConvArgs a;
+  int rc = setup(a, B, Cout, Hout, Wout, Cin, KH, KW, sh, sw, ph, pw, dh, dw, H, W);
+  if (rc) return rc;
+  if (B == 0) return WXX_OK;
+  a.P = Wt;
+  a.Q = X;
+  a.bias = bias;
+  a.I = a.Cin;
+  a.J = a.B * a.H * a.W;
+  a.K = a.Cout * a.KH * a.KW;
+  return dispatch<kDx>(a, Y);
+}
+
+// Replaces functional.conv2dtranspose_dx (reference
+// src/wxx/functional/convolution.py:1003-1064): dX (B, Cin, H, W) from
+// dY (B, Cout, Hout, Wout), a plain convolution of dY with the weight.
+WXX_API int wxx_conv2dtranspose_dx(const float* dY, const float* Wt, float* dX, int64_t B,
+                                   int64_t Cin, int64_t H, int64_t W, int64_t Cout, int64_t KH,
+                                   int64_t KW, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+                                   int64_t dh, int64_t dw, int64_t Hout, int64_t Wout) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(dY && Wt && dX, "null pointer");
+  ConvArgs a;
+  int rc = setup(a, B, Cout, Hout, Wout, Cin, KH, KW, sh, sw, ph, pw, dh, dw, H, W);
+  if (rc) return rc;
+  if (B == 0) return WXX_OK;
+  a.P = Wt;
+  a.Q = dY;
+  a.I = a.Cout;
+  a.J = a.B * a.Ho * a.Wo;
+  a.K = a.Cin * a.KH * a.KW;
+  return dispatch<kFwd>(a, dX);
+}
+
+// Replaces functional.conv2dtranspose_dw (reference
+// src/wxx/functional/convolution.py:1067-1185): dW (Cin, Cout, KH, KW) from
+// dY (B, Cout, Hout, Wout) and X (B, Cin, H, W).
+WXX_API int wxx_conv2dtranspose_dw(const float* dY, const float* X, float* dW, int64_t B,
+                                   int64_t Cin, int64_t H, int64_t W, int64_t Cout, int64_t KH,
+                                   int64_t KW, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+                                   int64_t dh, int64_t dw, int64_t Hout, int64_t Wout) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(dY && X && dW, "null pointer");
+  ConvArgs a;
+  int rc = setup(a, B, Cout, Hout, Wout, Cin, KH, KW, sh, sw, ph, pw, dh, dw, H, W);
+  if (rc) return rc;
+  if (B == 0) return wxx_fill_u32(dW, Cout * Cin * KH * KW, 0u);
+  a.P = X;
+  a.Q = dY;
   a.I = a.Cout;
   a.J = a.Cin * a.KH * a.KW;
   a.K = a.B * a.Ho * a.Wo;

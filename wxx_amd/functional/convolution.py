@@ -268,6 +268,75 @@ def conv2ddw(tensor1, X, stride, padding, dilation, Xshape, wshape):
     return out
 
 
+def _tconv_dims(Xshape, wshape, stride, padding, dilation, out_shape):
+    B, Cin, H, W = Xshape
+    _, Cout, KH, KW = wshape
+    sh, sw = stride
+    ph, pw = padding
+    dh, dw = dilation
+    return (B, Cin, H, W, Cout, KH, KW, sh, sw, ph, pw, dh, dw, out_shape[2], out_shape[3])
+
+
+def conv2dtranspose(tensor1, W, stride, padding, dilation, output_padding, bias=None):
+    """Transposed 2-D convolution; ``W`` is (C_in, C_out, KH, KW) and the output
+    size is (H_in - 1) * stride - 2 * padding + dilation * (K - 1) + output_padding + 1
+    (reference convolution.py:911-1000)."""
+    if not tensor1.is_contiguous():
+        tensor1 = tensor1.contiguous()
+    if not W.is_contiguous():
+        W = W.contiguous()
+    if bias is not None and not bias.is_contiguous():
+        bias = bias.contiguous()
+    B, C_in, H_in, W_in = tensor1.shape
+    weight_in_c, C_out, KH, KW = W.shape
+    if weight_in_c != C_in:
+        raise ValueError(f"conv2dtranspose weight expects {C_in} input channels, got {weight_in_c}")
+    sh, sw = stride
+    ph, pw = padding
+    dh, dw = dilation
+    oph, opw = output_padding
+    if not (0 <= oph < max(sh, dh)) or not (0 <= opw < max(sw, dw)):
+        raise ValueError(
+            f"output_padding {(oph, opw)} must be >= 0 and smaller than "
+            f"max(stride, dilation) {(max(sh, dh), max(sw, dw))}"
+        )
+    H_out = (H_in - 1) * sh - 2 * ph + dh * (KH - 1) + oph + 1
+    W_out = (W_in - 1) * sw - 2 * pw + dw * (KW - 1) + opw + 1
+    if H_out < 1 or W_out < 1:
+        raise ValueError(f"conv2dtranspose produces an empty output ({H_out}, {W_out})")
+    out = empty((B, C_out, H_out, W_out), requires_grad=tensor1.requires_grad)
+    d = _tconv_dims(tensor1.shape, W.shape, stride, padding, dilation, out.shape)
+    call("wxx_conv2dtranspose", ptr(tensor1), ptr(W), ptr(bias) if bias is not None else None,
+         ptr(out), *d)
+    return out
+
+
+def conv2dtranspose_dx(tensor1, W, stride, padding, dilation, Xshape, wshape, out_shape):
+    """Input gradient of :func:`conv2dtranspose`; ``tensor1`` is dY
+    (reference convolution.py:1003-1064)."""
+    if not tensor1.is_contiguous():
+        tensor1 = tensor1.contiguous()
+    if not W.is_contiguous():
+        W = W.contiguous()
+    d = _tconv_dims(Xshape, wshape, stride, padding, dilation, out_shape)
+    out = empty(tuple(Xshape), requires_grad=tensor1.requires_grad)
+    call("wxx_conv2dtranspose_dx", ptr(tensor1), ptr(W), ptr(out), *d)
+    return out
+
+
+def conv2dtranspose_dw(tensor1, X, stride, padding, dilation, out_shape, wshape):
+    """Weight gradient of :func:`conv2dtranspose`; ``tensor1`` is dY
+    (reference convolution.py:1067-1185)."""
+    if not tensor1.is_contiguous():
+        tensor1 = tensor1.contiguous()
+    if not X.is_contiguous():
+        X = X.contiguous()
+    d = _tconv_dims(X.shape, wshape, stride, padding, dilation, out_shape)
+    out = empty((X.shape[1], wshape[1], wshape[2], wshape[3]), requires_grad=tensor1.requires_grad)
+    call("wxx_conv2dtranspose_dw", ptr(tensor1), ptr(X), ptr(out), *d)
+    return out
+
+
 def causal_conv1d(tensor1, weight, bias):
     """Depthwise causal conv over ``(B, D, L)``: out[b,d,n] = bias[d] +
     sum_k weight[d,k] x[b,d,n-k]; ``tensor1`` may be a strided view
