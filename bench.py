@@ -7,15 +7,22 @@ resident in HBM:
   * row softmax and LayerNorm on [8192 x 4096] fp32.
 
 ``value`` is the aggregate fp32 GEMM throughput of the step (total GEMM FLOP
-/ total GEMM time).  Every kernel launch is bracketed by HIP events recorded
-on the library's own stream; ``roofline`` reports the dominant kernel (the
-4096^3 GEMM) against the 157.3 TFLOP/s fp32 matrix peak, and ``components``
-reports each GEMM's TFLOP/s and the softmax / LayerNorm GB/s against 8 TB/s.
+/ total GEMM time).  Each kernel is timed over ``--reps`` back-to-back
+launches between one pair of HIP events recorded on the library's own stream
+(the stream every kernel runs on), with outputs preallocated and the C ABI
+called directly, so the average is the kernel's own duration and agrees with
+``rocprofv3 --kernel-trace``.  ``roofline`` reports the dominant kernel (the
+4096^3 GEMM) against the 157.3 TFLOP/s fp32 matrix peak; ``components``
+reports every kernel of the step, and ``extra`` the HBM-bound kernels of the
+other configs measured on the same box (config 4's standalone batched real
+FFT / inverse FFT on [2048 x 16384], a row sum over [8192 x 4096]) and a
+256 MiB device-to-device copy as the achievable-bandwidth reference.
 ``cpu_baseline`` times the oracle's exact-order fp32 GEMM restatement
-(oracle/csrc/gemm_ref.c, OpenMP on all host cores) on a bounded row sample of
+(oracle/csrc/gemm_ref.c, OpenMP on the host cores) on a bounded row sample of
 the 4096^3 GEMM, on rank 0 at N=1 only.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--reps R] [--no-cpu]
+                       [--only NAME]
 """
 
 import argparse
@@ -41,39 +48,25 @@ GEMMS = [
     ("linear_8192x3072x768", 8192, 768, 3072),
 ]
 ROWS, COLS = 8192, 4096
+FFT_ROWS, FFT_N = 2048, 16384
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gemm_4096.json")
 
 
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--steps", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=2)
+    p.add_argument("--reps", type=int, default=0,
+                   help="launches per timed kernel per step (0: about 2 ms of work each)")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--only", default=None, help="run only this component (profiling)")
     return p.parse_args()
 
 
-class Timer:
-    """HIP events on the library stream; one slot pair per kernel call."""
-
-    def __init__(self, lib):
-        self.lib = lib
-        self.samples = {}
-
-    def run(self, name, fn):
-        self.lib.call("wxx_timer_record", 0)
-        fn()
-        self.lib.call("wxx_timer_record", 1)
-        ms = C.c_float(0.0)
-        self.lib.call("wxx_timer_elapsed", 0, 1, C.byref(ms))
-        self.samples.setdefault(name, []).append(ms.value)
-
-    def avg(self, name):
-        return float(np.mean(self.samples[name]))
-
-
 def cpu_gemm_baseline(budget_s):
-    """GFLOP/s of the oracle fp32 fma-chain GEMM on a row sample of 4096^3."""
+    """TFLOP/s of the oracle fp32 fma-chain GEMM on a row sample of 4096^3."""
     from oracle import gemm as og
 
     r = np.random.default_rng(0)
@@ -103,63 +96,153 @@ def cpu_gemm_baseline(budget_s):
     }
 
 
+class Kernels:
+    """Preallocated operands and one zero-argument launcher per component."""
+
+    def __init__(self, lib):
+        from wxx_amd import functional as F
+
+        self.F = F
+        self.keep = []
+        self.launch = {}
+        self.work = {}  # name -> (amount, unit kind "flop" | "byte")
+        rng = np.random.default_rng(10)
+        for name, M, N, K in GEMMS:
+            a = self._up(rng.standard_normal((M, K), dtype=np.float32))
+            b = self._up(rng.standard_normal((K, N), dtype=np.float32))
+            c = self._empty((M, N))
+            self.launch[name] = self._gemm(lib, a, b, c, M, N, K)
+            self.work[name] = (2.0 * M * N * K, "flop")
+        x = self._up(np.random.default_rng(20).standard_normal((ROWS, COLS), dtype=np.float32))
+        y = self._empty((ROWS, COLS))
+        g = self._up(np.ones(COLS, np.float32))
+        bt = self._up(np.zeros(COLS, np.float32))
+        mu, istd = self._empty((ROWS,)), self._empty((ROWS,))
+        P = C.c_void_p
+        self.launch["softmax"] = lambda: lib.call("wxx_softmax", P(x.data_ptr()),
+                                                  P(y.data_ptr()), 1 * ROWS, COLS, 1)
+        self.work["softmax"] = (2.0 * ROWS * COLS * 4, "byte")
+        self.launch["layernorm"] = lambda: lib.call(
+            "wxx_meanvarnorm", P(x.data_ptr()), P(g.data_ptr()), P(bt.data_ptr()),
+            P(y.data_ptr()), P(mu.data_ptr()), P(istd.data_ptr()), ROWS, COLS, 1,
+            C.c_float(1e-5), 0)
+        self.work["layernorm"] = (2.0 * ROWS * COLS * 4 + 2 * COLS * 4 + 2 * ROWS * 4, "byte")
+        s = self._empty((ROWS,))
+        self.launch["row_sum"] = lambda: lib.call("wxx_reduce", P(x.data_ptr()),
+                                                  P(s.data_ptr()), ROWS, COLS, 1, 0)
+        self.work["row_sum"] = (ROWS * COLS * 4.0 + ROWS * 4, "byte")
+        fx = self._up(np.random.default_rng(41).standard_normal((FFT_ROWS, FFT_N),
+                                                               dtype=np.float32))
+        nb = FFT_N // 2 + 1
+        fX = self._empty((FFT_ROWS, nb), dtype="c64")
+        fy = self._empty((FFT_ROWS, FFT_N))
+        self.launch["rfft_2048x16384"] = lambda: lib.call(
+            "wxx_rfft", P(fx.data_ptr()), P(fX.data_ptr()), FFT_ROWS, FFT_N, FFT_N)
+        self.work["rfft_2048x16384"] = (FFT_ROWS * (FFT_N * 4.0 + nb * 8), "byte")
+        self.launch["irfft_2048x16384"] = lambda: lib.call(
+            "wxx_irfft", P(fX.data_ptr()), P(fy.data_ptr()), FFT_ROWS, nb, FFT_N)
+        self.work["irfft_2048x16384"] = (FFT_ROWS * (FFT_N * 4.0 + nb * 8), "byte")
+        # device-to-device copy of 256 MiB: the achievable-bandwidth reference and
+        # the calibration kernel for the HBM byte counters
+        cb = 256 << 20
+        csrc, cdst = self._empty((cb // 4,)), self._empty((cb // 4,))
+        self.launch["copy_256MiB"] = lambda: lib.call("wxx_d2d", P(cdst.data_ptr()),
+                                                      P(csrc.data_ptr()), cb)
+        self.work["copy_256MiB"] = (2.0 * cb, "byte")
+
+    def _up(self, a):
+        t = self.F.from_numpy(a)
+        self.keep.append(t)
+        return t
+
+    def _empty(self, shape, dtype="f32"):
+        from wxx_amd.functional._common import empty
+
+        t = empty(shape, dtype=dtype)
+        self.keep.append(t)
+        return t
+
+    @staticmethod
+    def _gemm(lib, a, b, c, M, N, K):
+        P = C.c_void_p
+        pa, pb, pc = P(a.data_ptr()), P(b.data_ptr()), P(c.data_ptr())
+        return lambda: lib.call("wxx_matmul_add", pa, pb, None, pc, M, N, K, 1, 0, 0, 0, 0, 0, 0,
+                                0)
+
+
+STEP = [n for n, *_ in GEMMS] + ["softmax", "layernorm"]
+EXTRA = ["row_sum", "rfft_2048x16384", "irfft_2048x16384", "copy_256MiB"]
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
-              "(this build runs on a single MI355X)", file=sys.stderr)
+              "(every box in this build has a single MI355X)", file=sys.stderr)
         sys.exit(2)
 
-    from wxx_amd import functional as F
     from wxx_amd.backend import device, lib
 
     device.ensure_device()
-    timer = Timer(lib)
-    rng = np.random.default_rng(10)
-    gemm_in = {}
-    for name, M, N, K in GEMMS:
-        gemm_in[name] = (F.from_numpy(rng.standard_normal((M, K), dtype=np.float32)),
-                         F.from_numpy(rng.standard_normal((K, N), dtype=np.float32)))
-    x = F.from_numpy(np.random.default_rng(20).standard_normal((ROWS, COLS), dtype=np.float32))
-    gamma = F.from_numpy(np.ones(COLS, np.float32))
-    beta = F.from_numpy(np.zeros(COLS, np.float32))
-    keep = []
+    ks = Kernels(lib)
+    names = STEP + EXTRA
+    if args.only:
+        names = [args.only]
 
-    def step():
-        for name, *_ in GEMMS:
-            a, b = gemm_in[name]
-            timer.run(name, lambda: keep.append(F.matmul_add(a, b, None)))
-        timer.run("softmax", lambda: keep.append(F.softmax(x, -1)))
-        timer.run("layernorm", lambda: keep.append(F.meanvarnorm(x, gamma, beta, -1)))
-        keep.clear()
+    def reps_for(name):
+        if args.reps:
+            return args.reps
+        amount, kind = ks.work[name]
+        est_ms = amount / (80e9 if kind == "flop" else 4e6)  # rough 80 TF/s, 4 TB/s
+        return int(min(200, max(3, round(2.0 / max(est_ms, 1e-3)))))
+
+    reps = {n: reps_for(n) for n in names}
+    samples = {n: [] for n in names}
+    ms = C.c_float(0.0)
+
+    def run_step(record):
+        for n in names:
+            lib.call("wxx_timer_record", 0)
+            for _ in range(reps[n]):
+                ks.launch[n]()
+            lib.call("wxx_timer_record", 1)
+            lib.call("wxx_timer_elapsed", 0, 1, C.byref(ms))
+            if record:
+                samples[n].append(ms.value / reps[n])
 
     for _ in range(args.warmup):
-        step()
-    timer.samples.clear()
+        run_step(False)
     lib.call("wxx_sync")
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step()
+        run_step(True)
     lib.call("wxx_sync")
-    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    wall_s = time.perf_counter() - t0
 
     comps = {}
-    gemm_flop = gemm_ms = 0.0
-    for name, M, N, K in GEMMS:
-        ms = timer.avg(name)
-        flop = 2.0 * M * N * K
-        gemm_flop += flop
-        gemm_ms += ms
-        comps[name] = {"tflops": flop / ms / 1e9, "ms": ms,
-                       "frac_of_peak": flop / ms / 1e9 / PEAK_FP32_TFLOPS}
-    sm_bytes = 2.0 * ROWS * COLS * 4
-    ln_bytes = 2.0 * ROWS * COLS * 4 + 2 * COLS * 4 + 2 * ROWS * 4
-    for name, nbytes in (("softmax", sm_bytes), ("layernorm", ln_bytes)):
-        ms = timer.avg(name)
-        comps[name] = {"gbs": nbytes / ms / 1e6, "ms": ms,
-                       "frac_of_peak": nbytes / ms / 1e6 / PEAK_HBM_GBS}
+    for n in names:
+        t = float(np.median(samples[n]))
+        amount, kind = ks.work[n]
+        if kind == "flop":
+            rate = amount / t / 1e9
+            comps[n] = {"tflops": rate, "ms": t, "frac_of_peak": rate / PEAK_FP32_TFLOPS,
+                        "launches_timed": reps[n] * args.steps}
+        else:
+            rate = amount / t / 1e6
+            comps[n] = {"gbs": rate, "ms": t, "frac_of_peak": rate / PEAK_HBM_GBS,
+                        "launches_timed": reps[n] * args.steps}
+    if args.only:
+        print(json.dumps({"only": args.only, "component": comps[args.only]}))
+        return
+
+    gemm_flop = sum(ks.work[n][0] for n, *_ in GEMMS)
+    gemm_ms = sum(comps[n]["ms"] for n, *_ in GEMMS)
+    step_ms = sum(comps[n]["ms"] for n in STEP)
     dom = comps["gemm_4096"]
-    step_ms = sum(timer.avg(n) for n in timer.samples)
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
     out = {
         "metric": "GPT2 train-step tokens/s; fp32 GEMM TFLOP/s; FFT+reduction GB/s (1 GPU)",
         "value": gemm_flop / gemm_ms / 1e9,
@@ -168,28 +251,31 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": step_ms,
-        "wall_ms_per_step": wall_ms,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic N(0,1) inputs (numpy default_rng(10)/(20)), resident in HBM",
+        "data": "synthetic N(0,1) inputs (numpy default_rng(10)/(20)/(41)), resident in HBM",
         "config": {
             "workload": "BASELINE config 2: fp32 GEMM M=N=K 1024/2048/4096, "
                         "[8192x768]@[768x3072], [8192x3072]@[3072x768]; "
                         "row softmax and LayerNorm on [8192x4096]",
-            "value_is": "aggregate fp32 GEMM TFLOP/s over the five GEMMs",
+            "value_is": "aggregate fp32 GEMM TFLOP/s over the five GEMMs of the step",
+            "timing": "per kernel: median over steps of (HIP-event time of R back-to-back "
+                      "launches on the library stream) / R",
         },
         "roofline": {
-            "kernel": "gemm_f32_mfma_kernel (4096x4096x4096)",
+            "kernel": "gemm_f32_mfma_kernel<256,128,16,128,64> (4096x4096x4096)",
             "bound": "mfma",
             "achieved": dom["tflops"],
             "peak": PEAK_FP32_TFLOPS,
             "unit": "TFLOP/s",
             "frac": dom["tflops"] / PEAK_FP32_TFLOPS,
-            "traffic": None,
+            "traffic": traffic,
         },
-        "components": comps,
+        "components": {n: comps[n] for n in STEP},
+        "extra": {n: comps[n] for n in EXTRA},
+        "wall_s": wall_s,
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_gemm_baseline(args.cpu_seconds)
