@@ -35,7 +35,8 @@ _EMU_HEAVY = ("test_matmul_config2_sizes", "test_softmax[shape2", "test_softmax[
               "test_embed_bit_exact_and_embeddx[50304", "test_dropout_bit_exact[6291459",
               "test_cceloss[64-50304", "test_conv2d_resnet18_shapes", "test_causal_conv1d[8-256",
               "test_maxpool2d_bit_exact[shape0", "test_avgpool2d[shape0",
-              "test_adaptive_avgpool2d[shape0")
+              "test_adaptive_avgpool2d[shape0", "test_fft_many_rows_every_row[3000",
+              "test_fft_many_rows_every_row[1100", "test_fft_many_rows_every_row[600")
 
 
 def pytest_configure(config):

@@ -108,6 +108,9 @@ inline T __shfl_xor(T v, int off, int width = 64) {
   return r;
 }
 
+// Register-allocation hint of the device build; nothing to do on the CPU.
+#define WXX_OPAQUE(x) ((void)(x))
+
 // Wave-uniform value: every lane of the emulated wave already holds it.
 inline int __builtin_amdgcn_readfirstlane(int v) { return v; }
 
@@ -191,6 +194,12 @@ hipError_t hipEventRecord(hipEvent_t e, hipStream_t s);
 hipError_t hipEventSynchronize(hipEvent_t e);
 hipError_t hipEventElapsedTime(float* ms, hipEvent_t a, hipEvent_t b);
 hipError_t hipGetLastError();
+// Occupancy query: the emulation runs one workgroup at a time.
+template <class F>
+inline hipError_t hipOccupancyMaxActiveBlocksPerMultiprocessor(int* n, F, int, size_t) {
+  *n = 1;
+  return hipSuccess;
+}
 const char* hipGetErrorString(hipError_t e);
 
 #define hipLaunchKernelGGL(KERNEL, GRID, BLOCK, SHMEM, STREAM, ...) \

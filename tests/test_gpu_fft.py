@@ -137,6 +137,18 @@ def test_fft_full_size_properties(device):
     assert_fft_close(two, 2 * Xh.astype(np.complex128))
 
 
+@pytest.mark.parametrize("rows,n", [(300, 4096), (3000, 4096), (1100, 8192), (600, 32768)])
+def test_fft_many_rows_every_row(device, rows, n):
+    # More rows than one pass of the resident workgroups holds, so every
+    # workgroup walks several rows; every row is checked.
+    x = rng(rows + n).standard_normal((rows, n)).astype(np.float32)
+    X, _ = F().rfft(up(x), n)
+    assert_fft_close(X.numpy(), of.rfft(x, n), f"rfft rows={rows} n={n}")
+    Xc = (rng(n).standard_normal((rows, n // 2 + 1))
+          + 1j * rng(n + 1).standard_normal((rows, n // 2 + 1))).astype(np.complex64)
+    assert_fft_close(F().irfft(upc(Xc), n).numpy(), of.irfft(Xc, n), f"irfft rows={rows} n={n}")
+
+
 def test_hyena_shapes(device):
     # Hyena fft_conv1d: x (8, 256, 8192) -> rfft(16384) -> (8, 256, 8193);
     # here a 2-batch slice of it, checked on sampled rows.

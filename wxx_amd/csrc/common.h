@@ -16,6 +16,13 @@
 
 #define WXX_API extern "C" __attribute__((visibility("default")))
 
+// Make a per-lane integer opaque to the optimiser (an empty asm that "may
+// change" it), e.g. to stop loop-invariant code motion from hoisting and
+// keeping alive every address derived from it.
+#ifndef WXX_OPAQUE
+#define WXX_OPAQUE(x) asm volatile("" : "+v"(x))
+#endif
+
 WXX_API int wxx_fill_u32(void* dst, int64_t n, uint32_t bits);
 WXX_API int wxx_h2d(void* dst, const void* src, size_t bytes);
 WXX_API void* wxx_alloc(size_t bytes);

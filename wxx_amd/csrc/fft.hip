@@ -287,6 +287,319 @@ __global__ __launch_bounds__(Geo<LOGM>::NT) void irfft_kernel(const float2* __re
   run_passes<LOGM, 0, true, true>(v, buf, t, tw, out, 1.0f / G::M, live);
 }
 
+// ---- rows of M >= 2048 complex points: persistent workgroups -----------------
+// One workgroup of T = M / 32 threads owns one row at a time and walks rows
+// blockIdx.x, blockIdx.x + gridDim.x, ...  Each thread holds 32 points; the
+// log2(M) bits are split into ceil(log2(M) / 5) Stockham passes of 3..5 bits
+// (M = 8192: radix 32, 16, 16, i.e. two LDS exchanges instead of three).
+// Workgroups stay resident (two per CU at M = 8192) and drift out of step,
+// so one workgroup's HBM loads overlap another's LDS passes.  Each
+// thread's twiddles depend only on its lane, so the powers of two of every
+// pass twiddle are loaded once per workgroup and the other powers are formed
+// by at most four complex products.  The rfft untangling step handles bins
+// k and M - k together (one LDS pair read per two output bins).
+template <int LOGM>
+struct Big {
+  static constexpr int M = 1 << LOGM;
+  static constexpr int E = 32;
+  static constexpr int T = M / E;
+  static constexpr int NP = (LOGM + 4) / 5;
+  static constexpr int PM = M + (M >> 5);  // one pad slot per 32 points
+  __host__ __device__ static constexpr int bits(int p) {
+    return LOGM / NP + (p < LOGM % NP ? 1 : 0);
+  }
+  __host__ __device__ static constexpr int nsb(int p) {
+    int s = 0;
+    for (int q = 0; q < p; ++q) s += bits(q);
+    return s;
+  }
+  // pass twiddle tables back to back, then the untangling twiddles W_{2M}^k
+  __host__ __device__ static constexpr int off(int p) {
+    int o = 0;
+    for (int q = 0; q < p; ++q) o += (1 << nsb(q)) * ((1 << bits(q)) - 1);
+    return o;
+  }
+  __host__ __device__ static constexpr int table_size() { return off(NP) + M + 1; }
+  // twiddle-base registers per thread: (E / R) groups x bits for passes >= 1
+  __host__ __device__ static constexpr int tbo(int p) {
+    int o = 0;
+    for (int q = 1; q < p; ++q) o += (E >> bits(q)) * bits(q);
+    return o;
+  }
+  static constexpr int NTB = tbo(NP) > 0 ? tbo(NP) : 1;
+  static constexpr int MIN_BLOCKS = (160 * 1024) / (PM * 8) < 1 ? 1 : (160 * 1024) / (PM * 8);
+};
+
+__device__ __forceinline__ int bpad(int i) { return i + (i >> 5); }
+
+// cos(pi m / 16), m in [0, 32)
+__device__ constexpr float kCosPi16[32] = {
+    1.0f,
+    0.98078528040323044913f,
+    0.92387953251128675613f,
+    0.83146961230254523708f,
+    0.70710678118654752440f,
+    0.55557023301960222474f,
+    0.38268343236508977173f,
+    0.19509032201612826785f,
+    0.0f,
+    -0.19509032201612826785f,
+    -0.38268343236508977173f,
+    -0.55557023301960222474f,
+    -0.70710678118654752440f,
+    -0.83146961230254523708f,
+    -0.92387953251128675613f,
+    -0.98078528040323044913f,
+    -1.0f,
+    -0.98078528040323044913f,
+    -0.92387953251128675613f,
+    -0.83146961230254523708f,
+    -0.70710678118654752440f,
+    -0.55557023301960222474f,
+    -0.38268343236508977173f,
+    -0.19509032201612826785f,
+    0.0f,
+    0.19509032201612826785f,
+    0.38268343236508977173f,
+    0.55557023301960222474f,
+    0.70710678118654752440f,
+    0.83146961230254523708f,
+    0.92387953251128675613f,
+    0.98078528040323044913f};
+
+// v * exp(-i pi m / 16) (forward) or v * exp(+i pi m / 16) (inverse).
+template <bool INV>
+__device__ __forceinline__ float2 rot32(float2 v, int m) {
+  m &= 31;
+  if (m == 0) return v;
+  if (m == 16) return make_float2(-v.x, -v.y);
+  if (m == 8) return INV ? make_float2(-v.y, v.x) : make_float2(v.y, -v.x);
+  if (m == 24) return INV ? make_float2(v.y, -v.x) : make_float2(-v.y, v.x);
+  const float c = kCosPi16[m];
+  const float s = INV ? kCosPi16[(m + 24) & 31] : -kCosPi16[(m + 24) & 31];
+  return make_float2(v.x * c - v.y * s, v.x * s + v.y * c);
+}
+
+// In-register radix-2 decimation-in-frequency DFT of R <= 32 points; output
+// in bit-reversed order.
+template <int R, bool INV>
+__device__ __forceinline__ void dft32(float2* u) {
+  static_assert(R <= 32, "radix above 32 needs finer rotation constants");
+#pragma unroll
+  for (int s = R / 2; s >= 1; s >>= 1) {
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      if (j & s) continue;
+      const float2 a = u[j], b = u[j + s];
+      u[j] = make_float2(a.x + b.x, a.y + b.y);
+      u[j + s] = rot32<INV>(make_float2(a.x - b.x, a.y - b.y), (j & (s - 1)) * (16 / s));
+    }
+  }
+}
+
+// u[r] *= w^r for r in [1, R), from base[i] = w^(2^i): w^r is the product of
+// the bases of r's set bits (at most log2(R) - 1 products deep).
+template <int R>
+__device__ __forceinline__ void twiddle_powers(float2* u, const float2* base) {
+  float2 w[R];
+#pragma unroll
+  for (int r = 1; r < R; ++r) {
+    const int hb = 31 - __builtin_clz(r);  // constant after unrolling
+    w[r] = (r == (1 << hb)) ? base[hb] : cmul(w[r - (1 << hb)], base[hb]);
+    u[r] = cmul(u[r], w[r]);
+  }
+}
+
+// Twiddle bases of passes >= 1 for this thread (conjugated for the inverse).
+template <int LOGM, int P, bool INV>
+__device__ __forceinline__ void load_tw_bases(float2* twb, int t, const float2* __restrict__ tw) {
+  using G = Big<LOGM>;
+  if constexpr (P < G::NP) {
+    constexpr int BITS = G::bits(P), R = 1 << BITS, NS = 1 << G::nsb(P), Q = G::E / R;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const int k = (t + q * G::T) & (NS - 1);
+#pragma unroll
+      for (int i = 0; i < BITS; ++i) {
+        float2 w = tw[G::off(P) + ((1 << i) - 1) * NS + k];
+        if (INV) w.y = -w.y;
+        twb[G::tbo(P) + q * BITS + i] = w;
+      }
+    }
+    load_tw_bases<LOGM, P + 1, INV>(twb, t, tw);
+  }
+}
+
+// Passes P.. of one row (see run_passes for the Stockham indexing).  v holds
+// pass P's input (P == 0: loaded by the caller).  SYNC0: barrier before pass
+// 0 writes LDS (other threads may still read the row buffer).
+template <int LOGM, int P, bool INV, bool TO_GLOBAL, bool SYNC0>
+__device__ __forceinline__ void big_passes(float2* v, float2* buf, int t, const float2* twb,
+                                           float2* gout, float scale) {
+  using G = Big<LOGM>;
+  constexpr int BITS = G::bits(P), R = 1 << BITS, NSB = G::nsb(P), NS = 1 << NSB;
+  constexpr int GR = G::M / R, Q = G::E / R;
+  if constexpr (P > 0) {
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+#pragma unroll
+      for (int r = 0; r < R; ++r) v[q * R + r] = buf[bpad(t + q * G::T + r * GR)];
+  }
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    if constexpr (NS > 1) twiddle_powers<R>(v + q * R, twb + G::tbo(P) + q * BITS);
+    dft32<R, INV>(v + q * R);
+  }
+  constexpr bool LAST = P + 1 == G::NP;
+  if constexpr (LAST && TO_GLOBAL) {
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+#pragma unroll
+      for (int k = 0; k < R; ++k) {
+        const float2 z = v[q * R + bitrev(k, BITS)];
+        gout[t + q * G::T + k * GR] = make_float2(z.x * scale, z.y * scale);
+      }
+  } else {
+    if constexpr (P > 0 || SYNC0) __syncthreads();
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const int g = t + q * G::T;
+      const int base = ((g >> NSB) << (NSB + BITS)) + (g & (NS - 1));
+#pragma unroll
+      for (int k = 0; k < R; ++k) buf[bpad(base + k * NS)] = v[q * R + bitrev(k, BITS)];
+    }
+    __syncthreads();
+    if constexpr (!LAST) big_passes<LOGM, P + 1, INV, TO_GLOBAL, SYNC0>(v, buf, t, twb, gout, scale);
+  }
+}
+
+// Pass-0 input of one rfft row: z[m] = x[2m] + i x[2m+1], m = t + r T, zero
+// beyond in_len.
+template <int LOGM, bool VEC>
+__device__ __forceinline__ void rfft_big_load(float2* v, const float* __restrict__ xr, int t,
+                                              int64_t in_len) {
+  using G = Big<LOGM>;
+  constexpr int R0 = 1 << G::bits(0), GR0 = G::M / R0, Q0 = G::E / R0;
+#pragma unroll
+  for (int q = 0; q < Q0; ++q)
+#pragma unroll
+    for (int r = 0; r < R0; ++r) {
+      const int64_t j2 = 2 * (int64_t)(t + q * G::T + r * GR0);
+      float2 z = make_float2(0.f, 0.f);
+      if (VEC) {
+        if (j2 < in_len) z = *reinterpret_cast<const float2*>(xr + j2);
+      } else {
+        if (j2 < in_len) z.x = xr[j2];
+        if (j2 + 1 < in_len) z.y = xr[j2 + 1];
+      }
+      v[q * R0 + r] = z;
+    }
+}
+
+template <int LOGM, bool VEC>
+__global__ __launch_bounds__(Big<LOGM>::T, Big<LOGM>::MIN_BLOCKS) void rfft_big_kernel(
+    const float* __restrict__ x, float2* __restrict__ X, const float2* __restrict__ tw,
+    int64_t rows, int64_t in_len) {
+  using G = Big<LOGM>;
+  __shared__ float2 buf[G::PM];
+  float2 twb[G::NTB];
+  load_tw_bases<LOGM, 1, false>(twb, threadIdx.x, tw);
+  const float2* wu = tw + G::off(G::NP);
+  const float2 wt = wu[threadIdx.x];  // W_{2M}^t
+
+  float2 v[G::E];
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    // Hide the lane index from loop-invariant code motion: every LDS address
+    // below is a function of t, and hoisting them all out of the row loop
+    // would hold ~200 VGPRs; recomputed per row they fold into base + offset.
+    int t = threadIdx.x;
+    WXX_OPAQUE(t);
+    rfft_big_load<LOGM, VEC>(v, x + row * in_len, t, in_len);
+    big_passes<LOGM, 0, false, false, true>(v, buf, t, twb, nullptr, 1.f);
+    // untangle: bins k and M - k from Z[k], Z[M - k]
+    float2* Xr = X + row * (G::M + 1);
+#pragma unroll
+    for (int i = 0; i <= G::E / 2; ++i) {
+      const int k = t + i * G::T;
+      if (k > G::M / 2) break;
+      const float2 a = buf[bpad(k)];
+      const float2 b = buf[bpad((G::M - k) & (G::M - 1))];
+      const float2 e = make_float2(0.5f * (a.x + b.x), 0.5f * (a.y - b.y));
+      const float2 o = make_float2(0.5f * (a.y + b.y), 0.5f * (b.x - a.x));
+      const float2 w = cmul(wt, wu[i * G::T]);
+      const float2 wo = cmul(w, o);
+      Xr[k] = make_float2(e.x + wo.x, e.y + wo.y);
+      if (k != G::M / 2) Xr[G::M - k] = make_float2(e.x - wo.x, wo.y - e.y);
+    }
+    __syncthreads();  // the row buffer is free for the next row
+  }
+}
+
+// Offset (beyond the lane index t) of the position held in register e for
+// pass 0: e = q R0 + r holds point t + q T + r (M / R0).
+template <int LOGM>
+__host__ __device__ constexpr int big_pos0(int e) {
+  using G = Big<LOGM>;
+  constexpr int R0 = 1 << G::bits(0);
+  return (e / R0) * G::T + (e % R0) * (G::M / R0);
+}
+
+// Spectrum bins of one irfft row at this thread's pass-0 positions.
+template <int LOGM>
+__device__ __forceinline__ void irfft_big_load(float2* a, const float2* __restrict__ Xr, int t,
+                                               int64_t in_len) {
+  using G = Big<LOGM>;
+#pragma unroll
+  for (int e = 0; e < G::E; ++e) {
+    const int j = t + big_pos0<LOGM>(e);
+    a[e] = j < in_len ? Xr[j] : make_float2(0.f, 0.f);
+  }
+}
+
+template <int LOGM>
+__global__ __launch_bounds__(Big<LOGM>::T, Big<LOGM>::MIN_BLOCKS) void irfft_big_kernel(
+    const float2* __restrict__ X, float* __restrict__ x, const float2* __restrict__ tw,
+    int64_t rows, int64_t in_len) {
+  using G = Big<LOGM>;
+  __shared__ float2 buf[G::PM];
+  float2 twb[G::NTB];
+  load_tw_bases<LOGM, 1, true>(twb, threadIdx.x, tw);
+  const float2* wu = tw + G::off(G::NP);
+  const float2 wt = wu[threadIdx.x];
+
+  float2 v[G::E];
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    int t = threadIdx.x;  // opaque per row, as in rfft_big_kernel
+    WXX_OPAQUE(t);
+    const float2* Xr = X + row * in_len;
+    irfft_big_load<LOGM>(v, Xr, t, in_len);
+    const float2 nyq = G::M < in_len ? Xr[G::M] : make_float2(0.f, 0.f);
+    // exchange the bins through LDS to pair j with M - j
+#pragma unroll
+    for (int e = 0; e < G::E; ++e) buf[bpad(t + big_pos0<LOGM>(e))] = v[e];
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < G::E; ++e) {
+      const int j = t + big_pos0<LOGM>(e);
+      float2 a = v[e];
+      float2 b = j == 0 ? nyq : buf[bpad(G::M - j)];
+      if (j == 0) {
+        a.y = 0.f;
+        b.y = 0.f;
+      }
+      const float2 ee = make_float2(0.5f * (a.x + b.x), 0.5f * (a.y - b.y));
+      const float2 d = make_float2(0.5f * (a.x - b.x), 0.5f * (a.y + b.y));
+      const float2 w = cmul(wt, wu[big_pos0<LOGM>(e)]);  // o = d * conj(w)
+      const float2 o = make_float2(d.x * w.x + d.y * w.y, d.y * w.x - d.x * w.y);
+      v[e] = make_float2(ee.x - o.y, ee.y + o.x);
+    }
+    float2* out = reinterpret_cast<float2*>(x + row * (2 * (int64_t)G::M));
+    // SYNC0: every thread has read its pair partner before pass 0 overwrites LDS
+    big_passes<LOGM, 0, true, true, true>(v, buf, t, twb, out, 1.0f / G::M);
+    __syncthreads();  // last pass reads of this row are done
+  }
+}
+
 // n == 1: X[row] = x[row, 0] (or 0 for an empty row).
 __global__ __launch_bounds__(256) void rfft1_kernel(const float* __restrict__ x,
                                                     float2* __restrict__ X, int64_t rows,
@@ -329,6 +642,50 @@ const float2* twiddles(int logm) {
   return static_cast<float2*>(d);
 }
 
+template <int LOGM>
+const float2* big_twiddles() {
+  using G = Big<LOGM>;
+  std::lock_guard<std::mutex> lock(g_tw_mu);
+  const int key = 0x100 | LOGM;
+  auto it = g_tw.find(key);
+  if (it != g_tw.end()) return it->second;
+  std::vector<float2> h(G::table_size());
+  const double two_pi = 6.283185307179586476925286766559;
+  for (int p = 0; p < G::NP; ++p) {
+    const int64_t R = 1 << G::bits(p), NS = 1 << G::nsb(p);
+    for (int64_t r = 1; r < R; ++r)
+      for (int64_t k = 0; k < NS; ++k) {
+        const double a = -two_pi * (double)(r * k) / (double)(NS * R);
+        h[G::off(p) + (r - 1) * NS + k] = make_float2((float)std::cos(a), (float)std::sin(a));
+      }
+  }
+  for (int64_t k = 0; k <= G::M; ++k) {
+    const double a = -two_pi * (double)k / (double)(2 * G::M);
+    h[G::off(G::NP) + k] = make_float2((float)std::cos(a), (float)std::sin(a));
+  }
+  void* d = wxx_alloc(h.size() * sizeof(float2));
+  if (!d) return nullptr;
+  if (wxx_h2d(d, h.data(), h.size() * sizeof(float2)) != WXX_OK) {
+    wxx_free(d);
+    return nullptr;
+  }
+  g_tw[key] = static_cast<float2*>(d);
+  return static_cast<float2*>(d);
+}
+
+// Persistent grid: as many workgroups as fit on the device at once.
+template <typename K>
+unsigned persistent_grid(K kernel, int threads, int64_t rows) {
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess ||
+      per_cu < 1)
+    per_cu = 1;
+  const int64_t cus = wxx::num_cus() > 0 ? wxx::num_cus() : 256;
+  return (unsigned)std::max<int64_t>(1, std::min<int64_t>(rows, per_cu * cus));
+}
+
+constexpr int kBigMinLogM = 11;
+
 int log2_exact(int64_t n) {
   int l = 0;
   while ((int64_t(1) << l) < n) ++l;
@@ -338,6 +695,24 @@ int log2_exact(int64_t n) {
 template <int LOGM>
 void launch_rfft(const float* x, float2* X, const float2* tw, int64_t rows, int64_t in_len,
                  bool vec) {
+  if constexpr (LOGM >= kBigMinLogM) {
+    const float2* btw = big_twiddles<LOGM>();
+    if (!btw) {
+      wxx::set_error(WXX_E_OOM, "rfft twiddle table allocation failed");
+      return;
+    }
+    constexpr int T = Big<LOGM>::T;
+    if (vec) {
+      const unsigned g = persistent_grid(rfft_big_kernel<LOGM, true>, T, rows);
+      hipLaunchKernelGGL((rfft_big_kernel<LOGM, true>), dim3(g), dim3(T), 0, wxx::stream(), x, X,
+                         btw, rows, in_len);
+    } else {
+      const unsigned g = persistent_grid(rfft_big_kernel<LOGM, false>, T, rows);
+      hipLaunchKernelGGL((rfft_big_kernel<LOGM, false>), dim3(g), dim3(T), 0, wxx::stream(), x, X,
+                         btw, rows, in_len);
+    }
+    return;
+  }
   using G = Geo<LOGM>;
   const dim3 grid((unsigned)((rows + G::RPB - 1) / G::RPB));
   if (vec)
@@ -350,6 +725,18 @@ void launch_rfft(const float* x, float2* X, const float2* tw, int64_t rows, int6
 
 template <int LOGM>
 void launch_irfft(const float2* X, float* x, const float2* tw, int64_t rows, int64_t in_len) {
+  if constexpr (LOGM >= kBigMinLogM) {
+    const float2* btw = big_twiddles<LOGM>();
+    if (!btw) {
+      wxx::set_error(WXX_E_OOM, "irfft twiddle table allocation failed");
+      return;
+    }
+    constexpr int T = Big<LOGM>::T;
+    const unsigned g = persistent_grid(irfft_big_kernel<LOGM>, T, rows);
+    hipLaunchKernelGGL((irfft_big_kernel<LOGM>), dim3(g), dim3(T), 0, wxx::stream(), X, x, btw,
+                       rows, in_len);
+    return;
+  }
   using G = Geo<LOGM>;
   const dim3 grid((unsigned)((rows + G::RPB - 1) / G::RPB));
   hipLaunchKernelGGL((irfft_kernel<LOGM>), grid, dim3(G::NT), 0, wxx::stream(), X, x, tw, rows,
