@@ -1,0 +1,252 @@
+"""GPU: the nn models end to end.
+
+* BASELINE config 1 (toy GPT-2 1024/256/8/6, batch 4 x 128, dropout 0): loss,
+  every parameter gradient and one AdamW step against the float64 oracle
+  (oracle/models.py), with weights injected through load_state_dict.
+* Ports of the reference's model tests (tests/test_gpt.py, test_resnet.py,
+  test_hyena.py, test_clip_grad.py): shapes, gradients reaching every
+  parameter, causality, state_dict round trips, generation, parameter counts.
+"""
+
+import numpy as np
+import pytest
+
+from conftest import rng
+from oracle import models as om
+
+pytestmark = pytest.mark.gpu
+
+
+def W():
+    import wxx_amd
+
+    return wxx_amd
+
+
+def up(a):
+    return W().functional.from_numpy(np.asarray(a, np.float32))
+
+
+def up_u32(a):
+    return W().functional.from_numpy(np.asarray(a), np.uint32)
+
+
+def _close_to_scale(got, want, rel, name):
+    """|got - want| <= rel * max|want| for the whole tensor (fp32 sums over long
+    reductions against a float64 oracle)."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    scale = max(np.abs(want).max(), 1e-30)
+    err = np.abs(got - want).max()
+    assert err <= rel * scale, f"{name}: max err {err:.3g} vs scale {scale:.3g} (rel {err / scale:.3g})"
+    return err / scale
+
+
+def _gpt2_state(model, seed=1234):
+    """Config-1 weights: N(0, 0.02) for >= 2-D parameters, biases 0, LayerNorm
+    gamma 1 / beta 0 (nn/gpt.py:66-73), drawn from a seeded generator."""
+    r = np.random.default_rng(seed)
+    state = {}
+    for name, arr in model.state_dict().items():
+        if arr.ndim >= 2:
+            state[name] = r.normal(0, 0.02, arr.shape).astype(np.float32)
+        elif name.endswith(("weightg", "ln1.weight", "ln2.weight", "ln_f.weight")):
+            state[name] = np.ones(arr.shape, np.float32)
+        else:
+            state[name] = np.zeros(arr.shape, np.float32)
+    for name in list(state):  # LayerNorm aliases share their tensor
+        if name.endswith(".weight") and name[:-7] + ".weightg" in state:
+            state[name] = state[name[:-7] + ".weightg"]
+        if name.endswith(".bias") and name[:-5] + ".weightb" in state:
+            state[name] = state[name[:-5] + ".weightb"]
+    return state
+
+
+def _alias_free(state):
+    """Drop LayerNorm's alias names (weight/bias of a module that has weightg/weightb)."""
+    out = {}
+    for k, v in state.items():
+        if k.endswith(".weight") and k[:-7] + ".weightg" in state:
+            continue
+        if k.endswith(".bias") and k[:-5] + ".weightb" in state:
+            continue
+        out[k] = v
+    return out
+
+
+def test_gpt2_config1_train_step_matches_oracle(device):
+    wxx = W()
+    V, D, H, L, B, S = 1024, 256, 8, 6, 4, 128
+    model = wxx.nn.GPT2(V, D, H, L, dropout=0.0)
+    state = _gpt2_state(model)
+    model.load_state_dict(state)
+    x = rng(0).integers(0, V, (B, S)).astype(np.uint32)
+    y = rng(1).integers(0, V, (B, S)).astype(np.uint32)
+    opt = wxx.nn.AdamW(model.parameters(), lr=1e-3)
+
+    logits = model(up_u32(x))
+    loss = wxx.nn.CCELoss()(logits.reshape((B * S, V)), up_u32(y.reshape(-1)))
+    loss.backward()
+
+    params = {k: v.astype(np.float64) for k, v in _alias_free(state).items()}
+    ol, og = om.gpt2_loss_and_grads(params, x, y, H, L)
+    got_loss = float(loss.numpy().reshape(-1)[0])
+    assert abs(got_loss - ol) <= 1e-4 * abs(ol), (got_loss, ol)
+    gpu_grads = {}
+    for name, p in model.named_parameters():
+        assert p.grad is not None, name
+        if name in og:  # aliases are the same tensors as their first names
+            gpu_grads[name] = p.grad.numpy().astype(np.float64)
+            _close_to_scale(gpu_grads[name], og[name], 2e-4, name)
+
+    # One AdamW step: the device update of every parameter (aliases stepped
+    # twice, in list order) against the oracle's update from the same gradients.
+    order, first = [], {}
+    for name, p in model.named_parameters():
+        order.append(first.setdefault((p.buffer.ptr, p.offset), name))
+    opt.step()
+    states = [(np.zeros_like(params[k]), np.zeros_like(params[k])) for k in order]
+    want = om.adamw_sequence(params, gpu_grads, order, states, 1, 1e-3)
+    for name, p in model.named_parameters():
+        if name in want:
+            np.testing.assert_allclose(p.numpy(), want[name], rtol=0, atol=2e-6, err_msg=name)
+
+
+def test_gpt2_all_parameters_receive_grad(device):
+    wxx = W()
+    m = wxx.nn.GPT2(64, d_model=32, n_heads=4, n_layers=2, max_len=16, dropout=0.0)
+    x = up_u32(rng(2).integers(0, 64, (2, 6)))
+    out = m(x)
+    assert out.shape == [2, 6, 64]
+    assert np.isfinite(out.numpy()).all()
+    out.sum().backward()
+    missing = [n for n, p in m.named_parameters() if p.grad is None]
+    assert not missing, missing
+
+
+def test_gpt2_shape_error_and_state_dict_roundtrip(device, tmp_path):
+    wxx = W()
+    m = wxx.nn.GPT2(32, d_model=16, n_heads=2, n_layers=1, max_len=8)
+    with pytest.raises(ValueError):
+        m(up_u32(np.zeros((1, 9))))
+    state = m.state_dict()
+    path = wxx.save(m, tmp_path / "m")
+    m2 = wxx.nn.GPT2(32, d_model=16, n_heads=2, n_layers=1, max_len=8)
+    wxx.load(path, m2)
+    restored = m2.state_dict()
+    assert set(restored) == set(state)
+    for k, v in state.items():
+        assert np.array_equal(restored[k], v), k
+
+
+def test_gpt2_is_causal_and_mask(device):
+    wxx = W()
+    from wxx_amd.backend.context import inferenceMode
+
+    m = wxx.nn.GPT2(40, d_model=16, n_heads=2, n_layers=2, max_len=8)
+    ids = rng(3).integers(0, 40, (1, 6)).astype(np.uint32)
+    with inferenceMode():
+        before = m(up_u32(ids)).numpy()
+        ids2 = ids.copy()
+        ids2[0, -1] = (ids2[0, -1] + 1) % 40
+        after = m(up_u32(ids2)).numpy()
+    assert np.allclose(before[0, :-1], after[0, :-1], atol=1e-5)
+    assert not np.allclose(before[0, -1], after[0, -1])
+    mask = m.causal_mask(4).numpy()
+    assert mask.shape == (4, 4)
+    assert not np.any(np.tril(mask))
+    assert np.all(mask[np.triu_indices(4, k=1)] < -1e8)
+
+
+def test_gpt2_generate(device):
+    wxx = W()
+    from wxx_amd.backend import context
+
+    m = wxx.nn.GPT2(30, d_model=16, n_heads=2, n_layers=1, max_len=10)
+    prompt = rng(4).integers(0, 30, (2, 3)).astype(np.uint32)
+    out = m.generate(prompt, max_new_tokens=4, temperature=0.0)
+    assert out.shape == (2, 7) and out.dtype == np.uint32
+    assert np.array_equal(out[:, :3], prompt)
+    assert np.array_equal(out, m.generate(prompt, max_new_tokens=4, temperature=0.0))
+    assert m.generate(prompt, max_new_tokens=100, temperature=1.0).shape == (2, 10)
+    assert m.generate(prompt[0], max_new_tokens=2, temperature=1.0).shape == (1, 5)
+    assert context.MODE == 0
+
+
+def test_resnet18_forward_backward_and_bn_double_update(device):
+    wxx = W()
+    m = wxx.nn.ResNet18(num_classes=5)
+    x = up(rng(5).standard_normal((2, 3, 32, 32)))
+    out = m(x)
+    assert out.shape == [2, 5]
+    assert np.isfinite(out.numpy()).all()
+    out.sum().backward()
+    assert all(p.grad is not None for _, p in m.named_parameters())
+    # bn1 of each block runs twice per forward: two EMA updates from 0
+    rm = m.layer1._modules["0"].bn1.running_mean.numpy()
+    assert np.abs(rm).max() > 0
+    state = m.state_dict()
+    m2 = wxx.nn.ResNet18(num_classes=5)
+    m2.load_state_dict(state)
+    assert all(np.array_equal(m2.state_dict()[k], v) for k, v in state.items())
+
+
+def _hyena_expected(V, D, N, order, k=3, h=64, mlp_ratio=4, pe=8):
+    # structural count of reference tests/test_hyena.py:83-113
+    ffn = int(2 * (mlp_ratio * D) / 3)
+    fin = 2 * pe + 1
+    block = (D + (2 + order) * D * D + (k * D + D) + order * (fin * h + h + h * D + D)
+             + order * D + D + 3 * D * ffn)
+    return N * block + V * D + D
+
+
+def test_hyena_parameter_counts_and_tying(device):
+    wxx = W()
+    for order in (1, 2, 3, 4):
+        m = wxx.nn.Hyena(32, d_model=16, n_layers=2, order=order)
+        total = sum(int(np.prod(p.shape)) for _, p in m.parameters())
+        assert total == _hyena_expected(32, 16, 2, order)
+    m = wxx.nn.Hyena(2048, d_model=256, n_layers=6, order=4)
+    total = sum(int(np.prod(p.shape)) for _, p in m.parameters())
+    assert total == 6_444_288 + 6 * 4 * 2 * 8 * 64 == 6_468_864
+    assert m.head._embedding.weight is m.embed.weight
+    names = [n for n, _ in m.named_parameters()]
+    assert names.count("embed.weight") == 1 and not any(n.startswith("head.") for n in names)
+
+
+def test_hyena_forward_backward_causal(device):
+    wxx = W()
+    from wxx_amd.backend.context import inferenceMode
+
+    V, B, L = 40, 2, 32
+    m = wxx.nn.Hyena(V, d_model=16, n_layers=2, order=3)
+    ids = rng(6).integers(0, V, (B, L)).astype(np.uint32)
+    out = m(up_u32(ids))
+    assert out.shape == [B, L, V]
+    assert np.isfinite(out.numpy()).all()
+    out.sum().backward()
+    grads = [p.grad for _, p in m.named_parameters()]
+    assert all(g is not None for g in grads)
+    assert any(np.any(g.numpy() != 0) for g in grads)
+    with inferenceMode():
+        a = m(up_u32(ids)).numpy()
+        ids2 = ids.copy()
+        ids2[:, 16:] = (ids2[:, 16:] + 7) % V
+        b = m(up_u32(ids2)).numpy()
+    assert np.allclose(a[:, :16], b[:, :16], atol=1e-3)
+    assert not np.allclose(a[:, 16:], b[:, 16:])
+
+
+def test_clip_grad_norm_device_path_matches_host_path(device):
+    # reference tests/test_clip_grad.py: the fast path against the CPU formula
+    wxx = W()
+    m = wxx.nn.GPT2(50, d_model=16, n_heads=2, n_layers=2, max_len=8, dropout=0.0)
+    out = m(up_u32(rng(7).integers(0, 50, (2, 8))))
+    (out * 100.0).sum().backward()
+    grads = [(n, p.grad.numpy().astype(np.float64)) for n, p in m.named_parameters()]
+    want = np.sqrt(sum((g ** 2).sum() for _, g in grads))
+    total = wxx.nn.clip_grad_norm_(m.parameters(), 1.0)
+    assert abs(total - want) <= 1e-5 * want
+    coef = 1.0 / (want + 1e-6)
+    for (n, g0), (_, p) in zip(grads, m.named_parameters()):
+        np.testing.assert_allclose(p.grad.numpy(), g0 * coef, rtol=1e-5, atol=1e-9, err_msg=n)

@@ -8,7 +8,9 @@ first allocation.
 """
 
 from .Tensor import Parameter, Tensor
-from . import backend, functional
+from . import autograd, backend, functional, nn, serialization
 from .backend.device import get_device
+from .serialization import load, save
 
-__all__ = ["Tensor", "Parameter", "functional", "backend", "get_device"]
+__all__ = ["Tensor", "Parameter", "functional", "autograd", "backend", "nn", "serialization",
+           "get_device", "save", "load"]

@@ -90,8 +90,7 @@ class matmul(Function):
 class matmuladd(Function):
     def forward(self, tensor1, tensor2, tensor3):
         out = functional.matmul_add(tensor1, tensor2, tensor3)
-        out.requires_grad = any(self.needs_input_grad) or tensor1.requires_grad or \
-            tensor2.requires_grad or (tensor3 is not None and tensor3.requires_grad)
+        out.requires_grad = any(self.needs_input_grad)
         return self.attach(out, tensor1=tensor1, tensor2=tensor2)
 
     def backward(self, g):
