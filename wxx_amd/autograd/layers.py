@@ -9,12 +9,14 @@ class CrossEntropyLoss(Function):
 
     def forward(self, tensor1, tensor2):
         loss, grad = functional.cceloss(tensor1, tensor2)
-        loss.requires_grad = tensor1.requires_grad
+        loss.requires_grad = any(self.needs_input_grad)
         return self.attach(loss, grad=grad)
 
     def backward(self, g):
+        # one gradient: the Function is built with the logits only
+        # (CrossEntropyLoss(prediction), reference nn/loss.py:28)
         grad, self.grad = self.grad, None
-        return functional.pointwise(grad, g, 2), None
+        return functional.pointwise(grad, g, 2)
 
 
 class Dropout(Function):

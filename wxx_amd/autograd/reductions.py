@@ -8,6 +8,7 @@ backward broadcast the (scaled) output gradient with one strided kernel
 instead of multiplying a host-built ones tensor.
 """
 
+import builtins
 import math
 
 from .. import functional, validation
@@ -63,7 +64,7 @@ class mean(_reduction):
     def backward(self, g):
         if not self.needs_input_grad[0]:
             return None
-        n = math.prod(self.shape) // max(1, math.prod(g.shape))
+        n = math.prod(self.shape) // builtins.max(1, math.prod(g.shape))
         return self._broadcast(g, 1.0 / n)
 
 
