@@ -144,6 +144,17 @@ int wxx_softmax(const float* x, float* y, int64_t outer, int64_t C, int64_t inne
  * subtract / multiply chain of autograd softmax (autograd/reductions.py:25-35) */
 int wxx_softmax_backward(const float* y, const float* g, float* dx, int64_t outer, int64_t C,
                          int64_t inner);
+/* No single reference counterpart: the score path of MultiHeadAttention
+ * (nn/module.py:478-483: scores * 1/sqrt(d_head), + mask, softmax) fused into
+ * one row pass; y = softmax(x * scale + mask[row % mask_rows]); mask may be null,
+ * its rows mask_ld floats apart */
+int wxx_softmax_scale_mask(const float* x, const float* mask, float* y, int64_t rows, int64_t C,
+                           int64_t mask_rows, int64_t mask_ld, float scale);
+/* Gradient of wxx_softmax_scale_mask: dx = scale * y * (g - sum(g y)) — the
+ * softmax backward (autograd/reductions.py:25-35) times the scalar-multiply
+ * backward (autograd/pointwise.py mulscaler) in one pass */
+int wxx_softmax_backward_scale(const float* y, const float* g, float* dx, int64_t rows, int64_t C,
+                               float scale);
 /* functional.meanvarnorm (functional/normalization.py:82-145); row_cap 0 = all rows */
 int wxx_meanvarnorm(const float* x, const float* gamma, const float* beta, float* y,
                     float* mean, float* inv_std, int64_t outer, int64_t reduce, int64_t inner,

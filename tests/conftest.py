@@ -38,7 +38,8 @@ _EMU_HEAVY = ("test_matmul_config2_sizes", "test_softmax[shape2", "test_softmax[
               "test_adaptive_avgpool2d[shape0", "test_fft_many_rows_every_row[3000",
               "test_fft_many_rows_every_row[1100", "test_fft_many_rows_every_row[600",
               "test_gpt2_config1_train_step_matches_oracle", "test_resnet18_forward_backward",
-              "test_hyena_parameter_counts_and_tying")
+              "test_hyena_parameter_counts_and_tying", "test_softmax_scale_mask_fused[98304",
+              "test_matmul_split_k[True-False-768")
 
 
 def pytest_configure(config):

@@ -118,6 +118,9 @@ inline float __int_as_float(int v) { float f; std::memcpy(&f, &v, 4); return f; 
 inline float __uint_as_float(uint32_t v) { float f; std::memcpy(&f, &v, 4); return f; }
 inline int __float_as_int(float f) { int v; std::memcpy(&v, &f, 4); return v; }
 inline uint32_t __float_as_uint(float f) { uint32_t v; std::memcpy(&v, &f, 4); return v; }
+// Correctly rounded single operations (the host compile does not contract them).
+inline float __fmul_rn(float a, float b) { return a * b; }
+inline float __fadd_rn(float a, float b) { return a + b; }
 inline float rsqrtf(float x) { return 1.0f / std::sqrt(x); }
 inline float __expf(float x) { return std::exp(x); }
 

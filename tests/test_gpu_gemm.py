@@ -97,3 +97,34 @@ def test_matmul_errors(device):
         F().matmul_add(up(np.ones((2, 3, 4))), up(np.ones((3, 4, 2))), None)
     with pytest.raises(ValueError):
         F().matmul_add(a, up(np.ones((4, 2))), up(np.ones(3)))
+
+
+@pytest.mark.parametrize("ta,tb,M,N,K,bias_kind", [
+    (True, False, 768, 768, 8192, "none"),     # Linear dW at GPT-2 small: K = batch x seq
+    (True, False, 768, 3072, 8192, "vec"),
+    (False, False, 100, 70, 5000, "mat"),      # 64x64 tiles, split K
+    (False, True, 256, 200, 4097, "vec"),      # ragged K tail in the last split
+    (True, True, 130, 129, 2048, "none"),
+])
+def test_matmul_split_k(device, ta, tb, M, N, K, bias_kind):
+    # few output tiles over a long K: the K range is split across workgroups
+    # and the partials are added in split order by a second pass
+    r = rng(M + N + K)
+    A = r.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    B = r.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    bias = {"none": None, "vec": r.standard_normal(N), "mat": r.standard_normal((M, N))}[bias_kind]
+    got = F().matmul_add(up(A), up(B), None if bias is None else up(bias), transpose_A=ta,
+                         transpose_B=tb).numpy()
+    assert_close(got, og.matmul_add(A, B, bias, ta, tb), **tol(K))
+    again = F().matmul_add(up(A), up(B), None if bias is None else up(bias), transpose_A=ta,
+                           transpose_B=tb).numpy()
+    assert np.array_equal(got, again), "split-K result must be deterministic"
+
+
+def test_matmul_split_k_batched(device):
+    r = rng(99)
+    A = r.standard_normal((3, 64, 2048)).astype(np.float32)
+    B = r.standard_normal((3, 2048, 48)).astype(np.float32)
+    bias = r.standard_normal((3, 64, 48)).astype(np.float32)
+    got = F().matmul_add(up(A), up(B), up(bias)).numpy()
+    assert_close(got, og.matmul_add(A, B, bias), **tol(2048))

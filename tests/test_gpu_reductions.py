@@ -130,3 +130,31 @@ def test_broadcast_to(device, src, shape, scale):
     g = rng(22).standard_normal(src).astype(np.float32)
     got = F().broadcast_to(up(g), shape, scale).numpy()
     assert np.array_equal(got, (np.broadcast_to(g, shape) * np.float32(scale)).astype(np.float32))
+
+
+@pytest.mark.parametrize("rows,C,mask_rows,ld", [(96 * 16, 128, 128, 256), (7, 1024, 0, 0),
+                                                 (33, 37, 11, 37), (6, 5000, 3, 5000),
+                                                 (96 * 1024, 1024, 1024, 1024)])
+def test_softmax_scale_mask_fused(device, rows, C, mask_rows, ld):
+    # attention score path: softmax(x * scale + mask) and its gradient scale * dsoftmax
+    r = rng(rows + C)
+    x = (r.standard_normal((rows, C)) * 3).astype(np.float32)
+    scale = np.float32(0.125)
+    mask = None
+    if mask_rows:
+        big = np.where(r.random((mask_rows, ld)) < 0.3, -1e9, 0.0).astype(np.float32)
+        mask = big[:, :C]
+    shape = (rows // mask_rows, mask_rows, C) if mask_rows else (rows, C)  # (B*H, S, S) layout
+    tx = F().from_numpy(x.reshape(shape))
+    tm = None
+    if mask is not None:
+        tm = F().from_numpy(big).narrow(1, 0, C) if ld != C else F().from_numpy(mask)
+    y = F().softmax_scale_mask(tx, float(scale), tm).numpy().reshape(rows, C)
+    z = (x * scale).astype(np.float32)
+    if mask is not None:
+        z = (z + np.tile(mask, (rows // mask_rows + 1, 1))[:rows]).astype(np.float32)
+    want = oa.softmax(z, -1)
+    assert_close(y, want, rtol=1e-4, atol=1e-6)
+    g = r.standard_normal((rows, C)).astype(np.float32)
+    dx = F().softmax_backward_scale(F().from_numpy(y), F().from_numpy(g), float(scale)).numpy()
+    assert_close(dx, oa.softmax_backward(y, g, -1) * scale, rtol=1e-4, atol=1e-6)

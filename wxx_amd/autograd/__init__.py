@@ -42,7 +42,18 @@ from .pointwise import (
     sub,
     subscaler,
 )
-from .reductions import argmax, argmin, max, mean, min, softmax, std, sum, var
+from .reductions import (
+    argmax,
+    argmin,
+    max,
+    mean,
+    min,
+    scaled_masked_softmax,
+    softmax,
+    std,
+    sum,
+    var,
+)
 from .utils import (
     complex_conj,
     complex_mul,

@@ -32,6 +32,26 @@ class softmax(Function):
         return functional.softmax_backward(self.held_output(), g, self.dim)
 
 
+class scaled_masked_softmax(Function):
+    """``softmax(x * scale + mask)`` along the last axis as one Function (the
+    multiply, add and softmax Functions of the reference's attention score
+    path, nn/module.py:478-483); the mask receives no gradient."""
+
+    def forward(self, tensor1, scale, mask=None):
+        out = functional.softmax_scale_mask(tensor1, scale, mask)
+        out.requires_grad = tensor1.requires_grad
+        self.scale = scale
+        if out.requires_grad:
+            self.hold_output(out)
+        return self.attach(out)
+
+    def backward(self, g):
+        if not self.needs_input_grad[0]:
+            return None
+        y = self.held_output()
+        return functional.softmax_backward_scale(y, g, self.scale)
+
+
 class _reduction(Function):
     KIND = "sum"
 

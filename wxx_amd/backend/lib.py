@@ -65,6 +65,8 @@ SIGNATURES = {
     "wxx_maxmin_backward": (I32, [P, P, P, I64, I64, I64]),
     "wxx_softmax": (I32, [P, P, I64, I64, I64]),
     "wxx_softmax_backward": (I32, [P, P, P, I64, I64, I64]),
+    "wxx_softmax_scale_mask": (I32, [P, P, P, I64, I64, I64, I64, F32]),
+    "wxx_softmax_backward_scale": (I32, [P, P, P, I64, I64, F32]),
     # normalisation
     "wxx_meanvarnorm": (I32, [P, P, P, P, P, P, I64, I64, I64, F32, I64]),
     "wxx_meanvarnormdx": (I32, [P, P, P, P, P, P, I64, I64, I64, I64]),

@@ -41,6 +41,8 @@ struct GemmArgs {
   int bias_mode;
   int tiles_m, tiles_n;
   int vec_ok;  // all leading dims, batch strides and base pointers allow float4
+  int64_t kps;  // K elements per split (blockIdx.z); the whole K when not split
+  int64_t sZ;   // element stride between split partial outputs (0 when not split)
 };
 
 constexpr int kGroupM = 8;
@@ -92,11 +94,14 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
   const int64_t batch = blockIdx.y;
   const float* __restrict__ A = g.A + batch * g.sA;
   const float* __restrict__ B = g.B + batch * g.sB;
-  float* __restrict__ C = g.C + batch * g.sC;
+  float* __restrict__ C = g.C + batch * g.sC + (int64_t)blockIdx.z * g.sZ;
 
   const int64_t m0 = (int64_t)tile_m * BM;
   const int64_t n0 = (int64_t)tile_n * BN;
-  const int64_t M = g.M, N = g.N, K = g.K;
+  const int64_t M = g.M, N = g.N;
+  // this workgroup's K range [kbeg, K): the whole K, or one split of it
+  const int64_t kbeg = (int64_t)blockIdx.z * g.kps;
+  const int64_t K = min(g.K, kbeg + g.kps);
   const bool full_mn = g.vec_ok && (m0 + BM <= M) && (n0 + BN <= N);
 
   float4 ra[PA], rb[PB];
@@ -220,15 +225,15 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
   const int a_off = wm * WM + l32;
   const int b_off = wn * WN + l32;
 
-  const int64_t nk = (K + BK - 1) / BK;
-  load_chunk(0, full_mn && BK <= K);
+  const int64_t nk = (K - kbeg + BK - 1) / BK;
+  load_chunk(kbeg, full_mn && kbeg + BK <= K);
   store_chunk(0);
   __syncthreads();
 
   for (int64_t kc = 0; kc < nk; ++kc) {
     const int cur = (int)(kc & 1);
     if (kc + 1 < nk) {
-      const int64_t k1 = (kc + 1) * BK;
+      const int64_t k1 = kbeg + (kc + 1) * BK;
       load_chunk(k1, full_mn && k1 + BK <= K);
     }
     const float* as = As[cur];
@@ -281,10 +286,68 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
 }
 
 template <int BM, int BN, int BK, int WM, int WN>
-int launch_cfg(GemmArgs& g, int64_t batch, bool ta, bool tb) {
+int launch_tiles(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits);
+
+// Adds the split-K partials part[z][b][M][N] in split order (deterministic)
+// and applies the bias: C = sum_z part[z] + bias.
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmArgs g,
+                                                                  const float* __restrict__ part,
+                                                                  int splits, int64_t batch) {
+  const int64_t mn = g.M * g.N, n = mn * batch;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n;
+       e += (int64_t)gridDim.x * 256) {
+    float v = 0.f;
+    for (int z = 0; z < splits; ++z) v += part[(int64_t)z * n + e];
+    const int64_t b = e / mn, r = e - b * mn;
+    const int64_t row = r / g.N, col = r - row * g.N;
+    if (g.bias_mode == 1)
+      v += g.bias[col];
+    else if (g.bias_mode == 2)
+      v += g.bias[(row % g.bias_rows) * g.N + col];
+    else if (g.bias_mode == 3)
+      v += g.bias[b * g.sBias + r];
+    g.C[b * g.sC + row * g.ldc + col] = v;
+  }
+}
+
+template <int BM, int BN, int BK, int WM, int WN>
+int launch_cfg(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits = 1) {
   g.tiles_m = (int)((g.M + BM - 1) / BM);
   g.tiles_n = (int)((g.N + BN - 1) / BN);
-  dim3 grid((unsigned)(g.tiles_m * g.tiles_n), (unsigned)batch);
+  if (splits <= 1) {
+    g.kps = g.K > 0 ? g.K : 1;
+    g.sZ = 0;
+    return launch_tiles<BM, BN, BK, WM, WN>(g, batch, ta, tb, 1);
+  }
+  // Split K: partial products go to a scratch buffer (bias off), then one
+  // pass adds them in split order and applies the bias.
+  int64_t kps = (g.K + splits - 1) / splits;
+  kps = (kps + BK - 1) / BK * BK;
+  splits = (int)((g.K + kps - 1) / kps);
+  GemmArgs p = g;
+  const int64_t n = g.M * g.N * batch;
+  float* part = (float*)wxx::scratch_alloc(sizeof(float) * (size_t)n * splits);
+  if (!part) return wxx::set_error(WXX_E_OOM, "GEMM split-K partials");
+  p.C = part;
+  p.ldc = g.N;
+  p.sC = g.M * g.N;
+  p.sZ = n;
+  p.kps = kps;
+  p.bias_mode = 0;
+  int rc = launch_tiles<BM, BN, BK, WM, WN>(p, batch, ta, tb, splits);
+  if (rc == WXX_OK) {
+    hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3(wxx::grid_1d(n, 256, 8192)), dim3(256), 0,
+                       wxx::stream(), g, (const float*)part, splits, batch);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) rc = wxx::set_error(WXX_E_HIP, "split-K reduce: %s", hipGetErrorString(e));
+  }
+  wxx::scratch_free(part);
+  return rc;
+}
+
+template <int BM, int BN, int BK, int WM, int WN>
+int launch_tiles(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits) {
+  dim3 grid((unsigned)(g.tiles_m * g.tiles_n), (unsigned)batch, (unsigned)splits);
   hipStream_t s = wxx::stream();
   if (!ta && !tb)
     hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, false>), grid, dim3(256),
@@ -358,21 +421,33 @@ WXX_API int wxx_matmul_add(const float* A, const float* B, const float* bias, fl
     // Empty contraction: C = bias (or 0).  Reuse the kernel with K = 0: the
     // k-loop is skipped and the epilogue writes the bias.
   }
+  int splits = 1;
   if (tile == 0) {
     const int64_t cus = wxx::num_cus() > 0 ? wxx::num_cus() : 256;
     const int64_t t128 = ((g.M + 127) / 128) * ((g.N + 127) / 128) * nb;
     const int64_t t256 = ((g.M + 255) / 256) * ((g.N + 127) / 128) * nb;
-    if (t256 >= 2 * cus && g.K >= 256)
+    if (t256 >= 2 * cus && g.K >= 256) {
       tile = 3;
-    else if (t128 >= cus)
+    } else if (t128 >= cus) {
       tile = 2;
-    else
+    } else if (g.M >= 128 && g.N >= 128 && g.K >= 1024) {
+      // Few output tiles over a long K (weight gradients: K = batch x rows):
+      // 128x128 tiles with K split until the grid covers the CUs twice,
+      // keeping at least 256 K per split.
+      tile = 2;
+      splits = (int)std::min<int64_t>((2 * cus + t128 - 1) / t128, g.K / 256);
+    } else {
       tile = 1;
+      const int64_t t64 = ((g.M + 63) / 64) * ((g.N + 63) / 64) * nb;
+      if (t64 < cus && g.K >= 1024)
+        splits = (int)std::min<int64_t>((2 * cus + t64 - 1) / t64, g.K / 256);
+    }
+    splits = std::max(1, std::min(splits, 32));
   }
   switch (tile) {
-    case 1: return launch_cfg<64, 64, 16, 32, 32>(g, nb, transpose_A, transpose_B);
-    case 2: return launch_cfg<128, 128, 16, 64, 64>(g, nb, transpose_A, transpose_B);
-    case 3: return launch_cfg<256, 128, 16, 128, 64>(g, nb, transpose_A, transpose_B);
+    case 1: return launch_cfg<64, 64, 16, 32, 32>(g, nb, transpose_A, transpose_B, splits);
+    case 2: return launch_cfg<128, 128, 16, 64, 64>(g, nb, transpose_A, transpose_B, splits);
+    case 3: return launch_cfg<256, 128, 16, 128, 64>(g, nb, transpose_A, transpose_B, splits);
     default: return wxx::set_error(WXX_E_ARG, "bad tile %d", tile);
   }
 }

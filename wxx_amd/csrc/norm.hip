@@ -251,20 +251,31 @@ __global__ __launch_bounds__(kBlock) void norm_dg_partial_kernel(
   if (MODE == 0) part[((int64_t)split * 2 + 1) * R + r] = db;
 }
 
+// 64 features per workgroup: lane c of wave w adds splits w, w + 4, ... of
+// feature r (consecutive lanes read consecutive features), then the four
+// wave sums are added in wave order (a fixed order: deterministic).
 template <int MODE>
 __global__ __launch_bounds__(kBlock) void norm_dg_finalize_kernel(const float* __restrict__ part,
                                                                   float* __restrict__ dgamma,
                                                                   float* __restrict__ dbeta,
                                                                   int64_t R, int splits) {
-  const int64_t r = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-  if (r >= R) return;
+  __shared__ float sg[4][64], sb[4][64];
+  const int c = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t r = (int64_t)blockIdx.x * 64 + c;
   float dg = 0.f, db = 0.f;
-  for (int s = 0; s < splits; ++s) {
-    dg += part[((int64_t)s * 2 + 0) * R + r];
-    if (MODE == 0) db += part[((int64_t)s * 2 + 1) * R + r];
+  if (r < R) {
+    for (int s = w; s < splits; s += 4) {
+      dg += part[((int64_t)s * 2 + 0) * R + r];
+      if (MODE == 0) db += part[((int64_t)s * 2 + 1) * R + r];
+    }
   }
-  dgamma[r] = dg;
-  if (MODE == 0) dbeta[r] = db;
+  sg[w][c] = dg;
+  sb[w][c] = db;
+  __syncthreads();
+  if (w == 0 && r < R) {
+    dgamma[r] = ((sg[0][c] + sg[1][c]) + sg[2][c]) + sg[3][c];
+    if (MODE == 0) dbeta[r] = ((sb[0][c] + sb[1][c]) + sb[2][c]) + sb[3][c];
+  }
 }
 
 template <int MODE>
@@ -331,8 +342,8 @@ int launch_dg(const float* dy, const float* x, const float* mean, const float* i
   hipLaunchKernelGGL(norm_dg_partial_kernel<MODE>, dim3((unsigned)colblocks, (unsigned)splits),
                      dim3(kBlock), 0, s, dy, x, mean, inv, part, outer, R, inner, seg);
   WXX_LAUNCHED();
-  hipLaunchKernelGGL(norm_dg_finalize_kernel<MODE>, dim3((unsigned)colblocks), dim3(kBlock), 0,
-                     s, part, dgamma, dbeta, R, (int)splits);
+  hipLaunchKernelGGL(norm_dg_finalize_kernel<MODE>, dim3((unsigned)((R + 63) / 64)), dim3(kBlock),
+                     0, s, part, dgamma, dbeta, R, (int)splits);
   WXX_LAUNCHED();
   wxx::scratch_free(part);
   return WXX_OK;

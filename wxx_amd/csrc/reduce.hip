@@ -109,21 +109,32 @@ __global__ __launch_bounds__(kBlock) void reduce_cols_kernel(
     dst[(int64_t)split * nout + t] = acc;
 }
 
-// Sum `splits` partials per output in split order (deterministic).
-// layout 0: part[out * splits + s]; layout 1: part[s * nout + out].
+// Sum `splits` partials per output in a fixed order (deterministic).
+// layout 0: part[out * splits + s], one thread per output;
+// layout 1: part[s * nout + out], 64 outputs per workgroup: lane c of wave w
+// adds splits w, w + 4, ... (consecutive lanes read consecutive outputs) and
+// the four wave sums are added in wave order.
 __global__ __launch_bounds__(kBlock) void reduce_finalize_kernel(
     const float* __restrict__ part, float* __restrict__ out, int64_t nout, int splits,
     int layout, float scale) {
-  const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-  if (t >= nout) return;
-  float acc = 0.f;
   if (layout == 0) {
+    const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (t >= nout) return;
+    float acc = 0.f;
     const float* p = part + t * splits;
     for (int s = 0; s < splits; ++s) acc += p[s];
-  } else {
-    for (int s = 0; s < splits; ++s) acc += part[(int64_t)s * nout + t];
+    out[t] = acc * scale;
+    return;
   }
-  out[t] = acc * scale;
+  __shared__ float sw[4][64];
+  const int c = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t t = (int64_t)blockIdx.x * 64 + c;
+  float acc = 0.f;
+  if (t < nout)
+    for (int s = w; s < splits; s += 4) acc += part[(int64_t)s * nout + t];
+  sw[w][c] = acc;
+  __syncthreads();
+  if (w == 0 && t < nout) out[t] = (((sw[0][c] + sw[1][c]) + sw[2][c]) + sw[3][c]) * scale;
 }
 
 // --- max / min with argument -------------------------------------------------
@@ -273,8 +284,8 @@ int launch_reduce(const float* x, float* out, int64_t outer, int64_t R, int64_t 
                      s, x, dst, outer, R, inner, splits, seg, scale, splits == 1);
   WXX_LAUNCHED();
   if (splits > 1) {
-    hipLaunchKernelGGL(reduce_finalize_kernel, dim3(wxx::grid_1d(nout, kBlock)), dim3(kBlock), 0,
-                       s, part, out, nout, splits, 1, scale);
+    hipLaunchKernelGGL(reduce_finalize_kernel, dim3((unsigned)((nout + 63) / 64)), dim3(kBlock),
+                       0, s, part, out, nout, splits, 1, scale);
     WXX_LAUNCHED();
     wxx::scratch_free(part);
   }

@@ -15,10 +15,18 @@
 
 namespace {
 
-template <int TPR, int NCH, bool VEC>
+// PRE: the row is first mapped x -> x * scale + mask row (row % mask_rows),
+// mask rows mask_ld floats apart (the
+// attention score scaling and additive mask), with the two roundings of the
+// separate multiply and add kept (no fused multiply-add).
+template <int TPR, int NCH, bool VEC, bool PRE = false>
 __global__ __launch_bounds__(256) void softmax_rows_kernel(const float* __restrict__ x,
                                                             float* __restrict__ y, int64_t rows,
-                                                            int C) {
+                                                            int C,
+                                                            const float* __restrict__ mask = nullptr,
+                                                            int64_t mask_rows = 1,
+                                                            int64_t mask_ld = 0,
+                                                            float scale = 1.f) {
   __shared__ float red[4];
   constexpr int RPB = 256 / TPR;
   const int t = threadIdx.x % TPR;
@@ -27,6 +35,14 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(const float* __restri
   const float* xr = x + row * C;
   wxx::RowRegs<TPR, NCH, VEC> r;
   r.load(xr, C, t, -INFINITY);
+  if (PRE) {
+    wxx::RowRegs<TPR, NCH, VEC> mk;
+    if (mask) mk.load(mask + (row % mask_rows) * mask_ld, C, t, 0.f);
+#pragma unroll
+    for (int e = 0; e < NCH * 4; ++e)
+      if (r.valid(e, t, C))
+        r.v[e] = __fadd_rn(__fmul_rn(r.v[e], scale), mask ? mk.v[e] : 0.f);
+  }
   float m = -1e38f;
 #pragma unroll
   for (int e = 0; e < NCH * 4; ++e) m = fmaxf(m, r.v[e]);
@@ -103,11 +119,14 @@ __global__ __launch_bounds__(256) void softmax_cols_kernel(const float* __restri
 }
 
 // dx = y * (g - sum(g * y)) per row: one read of y and g, one write.
-template <int TPR, int NCH, bool VEC>
+// SCALED: dx is further multiplied by `scale` (the gradient through the
+// score scaling), as a separate rounding.
+template <int TPR, int NCH, bool VEC, bool SCALED = false>
 __global__ __launch_bounds__(256) void softmax_bwd_rows_kernel(const float* __restrict__ y,
                                                                 const float* __restrict__ g,
                                                                 float* __restrict__ dx,
-                                                                int64_t rows, int C) {
+                                                                int64_t rows, int C,
+                                                                float scale = 1.f) {
   __shared__ float red[4];
   constexpr int RPB = 256 / TPR;
   const int t = threadIdx.x % TPR;
@@ -121,7 +140,10 @@ __global__ __launch_bounds__(256) void softmax_bwd_rows_kernel(const float* __re
   for (int e = 0; e < NCH * 4; ++e) dot += vg.v[e] * vy.v[e];
   dot = wxx::RowReduce<TPR>::sum(dot, red);
 #pragma unroll
-  for (int e = 0; e < NCH * 4; ++e) vy.v[e] = vy.v[e] * (vg.v[e] - dot);
+  for (int e = 0; e < NCH * 4; ++e) {
+    vy.v[e] = vy.v[e] * (vg.v[e] - dot);
+    if (SCALED) vy.v[e] = __fmul_rn(vy.v[e], scale);
+  }
   vy.store(dx + row * C, C, t);
 }
 
@@ -197,6 +219,59 @@ WXX_API int wxx_softmax(const float* x, float* y, int64_t outer, int64_t C, int6
   }
   hipLaunchKernelGGL(softmax_cols_kernel, dim3(wxx::grid_1d(outer * inner, 256)), dim3(256), 0,
                      s, x, y, outer, C, inner);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// y = softmax along rows of (x * scale + mask[row % mask_rows]); mask may be
+// null, its rows are mask_ld floats apart.  The score path of MultiHeadAttention (reference
+// src/wxx/nn/module.py:478-483: matmul * (1/sqrt(d_head)), + mask, softmax)
+// in one pass over the scores instead of three.  Rows of C <= 16384 only.
+WXX_API int wxx_softmax_scale_mask(const float* x, const float* mask, float* y, int64_t rows,
+                                   int64_t C, int64_t mask_rows, int64_t mask_ld, float scale) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(x && y, "null pointer");
+  WXX_REQUIRE(rows >= 0 && C >= 1 && (!mask || (mask_rows >= 1 && mask_ld >= C)),
+              "bad softmax dims");
+  if (wxx::row_plan(C) == 0)
+    return wxx::set_error(WXX_E_UNSUPPORTED, "fused softmax rows of %lld", (long long)C);
+  if (rows == 0) return WXX_OK;
+  hipStream_t s = wxx::stream();
+  const bool vec = (C % 4 == 0) && (mask_ld % 4 == 0) &&
+                   ((((uintptr_t)x) | ((uintptr_t)y) | ((uintptr_t)mask)) % 16 == 0);
+  int rc = wxx::row_dispatch(C, vec, [&](auto tpr, auto nch, auto v) {
+    hipLaunchKernelGGL((softmax_rows_kernel<decltype(tpr)::value, decltype(nch)::value,
+                                            decltype(v)::value, true>),
+                       wxx::row_grid(decltype(tpr)::value, rows), dim3(256), 0, s, x, y, rows,
+                       (int)C, mask, mask ? mask_rows : 1, mask ? mask_ld : 0, scale);
+    return 0;
+  });
+  if (rc) return rc;
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// dx = scale * (y * (g - sum(g * y))) along rows: the softmax gradient of
+// wxx_softmax_scale_mask (the mask adds nothing to the gradient).  Rows of
+// C <= 16384 only.
+WXX_API int wxx_softmax_backward_scale(const float* y, const float* g, float* dx, int64_t rows,
+                                       int64_t C, float scale) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(y && g && dx, "null pointer");
+  WXX_REQUIRE(rows >= 0 && C >= 1, "bad softmax dims");
+  if (wxx::row_plan(C) == 0)
+    return wxx::set_error(WXX_E_UNSUPPORTED, "fused softmax rows of %lld", (long long)C);
+  if (rows == 0) return WXX_OK;
+  hipStream_t s = wxx::stream();
+  const bool vec = (C % 4 == 0) && ((((uintptr_t)y) | ((uintptr_t)g) | ((uintptr_t)dx)) % 16 == 0);
+  int rc = wxx::row_dispatch(C, vec, [&](auto tpr, auto nch, auto v) {
+    hipLaunchKernelGGL((softmax_bwd_rows_kernel<decltype(tpr)::value, decltype(nch)::value,
+                                                decltype(v)::value, true>),
+                       wxx::row_grid(decltype(tpr)::value, rows), dim3(256), 0, s, y, g, dx, rows,
+                       (int)C, scale);
+    return 0;
+  });
+  if (rc) return rc;
   WXX_LAUNCHED();
   return WXX_OK;
 }

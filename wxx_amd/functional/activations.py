@@ -156,3 +156,54 @@ def softmax_backward(y, grad, dim):
     if validation.numel(y.shape):
         call("wxx_softmax_backward", ptr(y), ptr(grad), ptr(out), outer, c, inner)
     return out
+
+
+def _fused_softmax_ok(x, mask):
+    if len(x.shape) < 1 or x.type != "f32" or x.shape[-1] > 16384:
+        return False
+    if mask is None:
+        return True
+    return (len(mask.shape) == 2 and mask.type == "f32" and mask.shape[1] == x.shape[-1]
+            and mask.stride[1] == 1 and len(x.shape) >= 2 and x.shape[-2] == mask.shape[0])
+
+
+def softmax_scale_mask(tensor1, scale, mask=None):
+    """``softmax(tensor1 * scale + mask, dim=-1)`` in one pass; ``mask`` is
+    None or a (rows, C) tensor broadcast over the leading dimensions (the
+    attention score path of the reference's MultiHeadAttention,
+    nn/module.py:478-483, whose three launches it replaces; same roundings)."""
+    if not tensor1.is_contiguous():
+        tensor1 = tensor1.contiguous()
+    if not _fused_softmax_ok(tensor1, mask):
+        from .pointwise import pointwise, scalarpointwise
+
+        z = scalarpointwise(tensor1, scale, 2)
+        if mask is not None:
+            z = pointwise(z, mask, 0)
+        return softmax(z, -1)
+    C = tensor1.shape[-1]
+    rows = validation.numel(tensor1.shape) // C
+    out = empty(tensor1.shape, requires_grad=tensor1.requires_grad)
+    if rows:
+        call("wxx_softmax_scale_mask", ptr(tensor1), ptr(mask) if mask is not None else None,
+             ptr(out), rows, C, mask.shape[0] if mask is not None else 1,
+             mask.stride[0] if mask is not None else 0, float(scale))
+    return out
+
+
+def softmax_backward_scale(y, grad, scale):
+    """Gradient of :func:`softmax_scale_mask`: ``scale * y * (grad - sum(grad * y))``."""
+    if not y.is_contiguous():
+        y = y.contiguous()
+    if not grad.is_contiguous():
+        grad = grad.contiguous()
+    C = y.shape[-1]
+    if C > 16384:
+        from .pointwise import scalarpointwise
+
+        return scalarpointwise(softmax_backward(y, grad, -1), scale, 2)
+    rows = validation.numel(y.shape) // C
+    out = empty(y.shape)
+    if rows:
+        call("wxx_softmax_backward_scale", ptr(y), ptr(grad), ptr(out), rows, C, float(scale))
+    return out

@@ -5,7 +5,7 @@ import math
 import random
 
 from .. import validation
-from ._common import call, empty, ptr
+from ._common import Tensor, call, empty, ptr
 
 
 def adamw(tensor1, grad, exp_avg, exp_avg_sq, step, lr, beta1, beta2, eps, weight_decay, bc1,
@@ -77,22 +77,39 @@ def scale_multi(tensors, coef):
     call("wxx_scale_multi", ptrs, sizes, count, float(coef))
 
 
+def _same_values(t):
+    """A new tensor object over ``t``'s (contiguous) storage."""
+    out = Tensor(list(t.shape), buffer=t.buffer, offset=t.offset, dtype=t.type)
+    out._base = t
+    return out
+
+
 def dropout(tensor1, p):
-    """Inverted dropout; returns ``(y, seed)`` with a fresh 32-bit seed per call."""
+    """Inverted dropout; returns ``(y, seed)`` with a fresh 32-bit seed per call.
+
+    At ``p == 0`` every element is kept with scale exactly 1, so the result is
+    the input's values: the seed is still drawn (the host RNG advances exactly
+    as in the reference) and a view of the input is returned without a launch.
+    """
     if not tensor1.is_contiguous():
         tensor1 = tensor1.contiguous()
     n = math.prod(tensor1.shape)
     scale = 1 / (1 - p)
     r = random.randint(0, 2**32 - 1)
+    if p == 0:
+        return _same_values(tensor1), r
     out = empty(tensor1.shape)
     call("wxx_dropout", ptr(tensor1), ptr(out), n, r, float(p), float(scale))
     return out, r
 
 
 def dropoutdx(tensor1, p, seed):
-    """Gradient of :func:`dropout` with the forward call's ``seed``."""
+    """Gradient of :func:`dropout` with the forward call's ``seed`` (the
+    gradient's own values at ``p == 0``)."""
     if not tensor1.is_contiguous():
         tensor1 = tensor1.contiguous()
+    if p == 0:
+        return _same_values(tensor1)
     n = math.prod(tensor1.shape)
     out = empty(tensor1.shape)
     call("wxx_dropout", ptr(tensor1), ptr(out), n, int(seed) & 0xFFFFFFFF, float(p),

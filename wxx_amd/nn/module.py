@@ -375,11 +375,16 @@ class MultiHeadAttention(Module):
         q = self._heads(self.q(x), b, seq)
         k = self._heads(self.k(x), b, seq)
         v = self._heads(self.v(x), b, seq)
-        score = autograd.matmul(q, k).forward(q, k, transpose_b=True) * (
-            1.0 / math.sqrt(self.head_dim))
-        if mask is not None:
-            score = score + mask
-        attn = self.drop(score.softmax(dim=-1))
+        score = autograd.matmul(q, k).forward(q, k, transpose_b=True)
+        scale = 1.0 / math.sqrt(self.head_dim)
+        if mask is None or (len(mask.shape) == 2 and not mask.requires_grad):
+            # scale, mask add and softmax as one pass over the scores (same
+            # roundings as the three separate ops)
+            attn = autograd.scaled_masked_softmax(score).forward(score, scale, mask)
+        else:
+            score = score * scale
+            attn = (score + mask).softmax(dim=-1)
+        attn = self.drop(attn)
         out = autograd.matmul(attn, v).forward(attn, v)
         out = (out.reshape((b, self.n_heads, seq, self.head_dim)).permute(0, 2, 1, 3)
                .reshape((b, seq, self.d_model)))
