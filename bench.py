@@ -16,13 +16,16 @@ called directly, so the average is the kernel's own duration and agrees with
 reports every kernel of the step, and ``extra`` the HBM-bound kernels of the
 other configs measured on the same box (config 4's standalone batched real
 FFT / inverse FFT on [2048 x 16384], a row sum over [8192 x 4096]) and a
-256 MiB device-to-device copy as the achievable-bandwidth reference.
+256 MiB device-to-device copy as the achievable-bandwidth reference; and
+the GPT-2 train steps of configs 1 and 5 (forward, CCE loss, backward,
+clip_grad_norm_, AdamW, LR schedule) in tokens/s, timed on the host clock
+between device synchronisations.
 ``cpu_baseline`` times the oracle's exact-order fp32 GEMM restatement
 (oracle/csrc/gemm_ref.c, OpenMP on the host cores) on a bounded row sample of
 the 4096^3 GEMM, on rank 0 at N=1 only.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--reps R] [--no-cpu]
-                       [--only NAME]
+                       [--no-train] [--only NAME]
 """
 
 import argparse
@@ -62,6 +65,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--only", default=None, help="run only this component (profiling)")
+    p.add_argument("--no-train", action="store_true", help="skip the GPT-2 train-step extras")
     return p.parse_args()
 
 
@@ -170,6 +174,57 @@ class Kernels:
                                 0)
 
 
+# BASELINE configs 1 and 5: GPT-2 train steps (tokens / s), dropout 0.
+GPT2_CONFIGS = {
+    "gpt2_train_config1": dict(V=1024, D=256, H=8, L=6, B=4, S=128, max_len=256),
+    "gpt2_train_config5": dict(V=50304, D=768, H=12, L=12, B=8, S=1024, max_len=1024),
+}
+GPT2_FLOP = {"gpt2_train_config1": 1.651e10, "gpt2_train_config5": 7.001e12}
+
+
+def gpt2_train_step(lib, name, steps, warmup):
+    """Full train step: forward, CCELoss, backward, clip_grad_norm_(1.0), AdamW,
+    WarmupCosineLR (README.md:50-51 schedule), zero_grad.  Synthetic uniform
+    token ids; random-init weights.  Timed with the host clock around
+    ``steps`` steps between device synchronisations."""
+    import wxx_amd as wxx
+
+    c = GPT2_CONFIGS[name]
+    m = wxx.nn.GPT2(c["V"], c["D"], c["H"], c["L"], max_len=c["max_len"], dropout=0.0)
+    opt = wxx.nn.AdamW(m.parameters(), lr=1e-3)
+    sched = wxx.nn.WarmupCosineLR(opt, warmup_steps=100, total_steps=5000, min_lr=1e-5)
+    lossf = wxx.nn.CCELoss()
+    r = np.random.default_rng(50)
+    x = wxx.functional.from_numpy(r.integers(0, c["V"], (c["B"], c["S"])), np.uint32)
+    y = wxx.functional.from_numpy(r.integers(0, c["V"], (c["B"] * c["S"],)), np.uint32)
+
+    def step():
+        logits = m(x)
+        loss = lossf(logits.reshape((c["B"] * c["S"], c["V"])), y)
+        loss.backward()
+        wxx.nn.clip_grad_norm_(m.parameters(), 1.0)
+        opt.step()
+        sched.step()
+        opt.zero_grad()
+        return loss
+
+    for _ in range(warmup):
+        step()
+    lib.call("wxx_sync")
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss = step()
+    lib.call("wxx_sync")
+    dt = (time.perf_counter() - t0) / steps
+    tokens = c["B"] * c["S"]
+    return {"tokens_per_s": tokens / dt, "ms": dt * 1e3, "steps_timed": steps,
+            "tflops": GPT2_FLOP[name] / dt / 1e12,
+            "frac_of_peak": GPT2_FLOP[name] / dt / 1e12 / PEAK_FP32_TFLOPS,
+            "loss": float(loss.numpy().reshape(-1)[0]),
+            "model": f"GPT2(vocab {c['V']}, d {c['D']}, heads {c['H']}, layers {c['L']}), "
+                     f"batch {c['B']} x seq {c['S']}, dropout 0"}
+
+
 STEP = [n for n, *_ in GEMMS] + ["softmax", "layernorm"]
 EXTRA = ["row_sum", "rfft_2048x16384", "irfft_2048x16384", "copy_256MiB"]
 
@@ -186,6 +241,10 @@ def main():
     device.ensure_device()
     ks = Kernels(lib)
     names = STEP + EXTRA
+    if args.only in GPT2_CONFIGS:
+        print(json.dumps({"only": args.only,
+                          "component": gpt2_train_step(lib, args.only, args.steps, args.warmup)}))
+        return
     if args.only:
         names = [args.only]
 
@@ -277,6 +336,9 @@ def main():
         "extra": {n: comps[n] for n in EXTRA},
         "wall_s": wall_s,
     }
+    if not args.no_train:
+        for name in GPT2_CONFIGS:
+            out["extra"][name] = gpt2_train_step(lib, name, steps=5, warmup=2)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_gemm_baseline(args.cpu_seconds)
     print(json.dumps(out))

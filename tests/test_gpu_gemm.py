@@ -128,3 +128,27 @@ def test_matmul_split_k_batched(device):
     bias = r.standard_normal((3, 64, 48)).astype(np.float32)
     got = F().matmul_add(up(A), up(B), up(bias)).numpy()
     assert_close(got, og.matmul_add(A, B, bias), **tol(2048))
+
+
+@pytest.mark.parametrize("code", [1, 2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("splits", [1, 3])
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+def test_matmul_every_tile_code(device, code, splits, ta, tb):
+    # each tile / K-chunk / buffering variant of the kernel on a ragged shape
+    # (edge tiles in M and N, a K tail shorter than the chunk) and an aligned one
+    import ctypes as C
+
+    from wxx_amd.backend import lib
+    from wxx_amd.functional._common import empty
+
+    for M, N, K in [(300, 270, 133), (256, 256, 512)]:
+        r = rng(M + 3 * code + splits)
+        A = r.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+        B = r.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+        bias = r.standard_normal(N).astype(np.float32)
+        tA, tB, tbias = up(A), up(B), up(bias)
+        out = empty([M, N])
+        P = C.c_void_p
+        lib.call("wxx_matmul_add", P(tA.data_ptr()), P(tB.data_ptr()), P(tbias.data_ptr()),
+                 P(out.data_ptr()), M, N, K, 1, 0, 0, 0, 1, int(ta), int(tb), code + 256 * splits)
+        assert_close(out.numpy(), og.matmul_add(A, B, bias, ta, tb), **tol(K))

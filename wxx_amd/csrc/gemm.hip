@@ -14,15 +14,21 @@
 //  * 256-thread workgroups (4 wavefronts) own a BM x BN tile; each wave owns
 //    a WM x WN sub-tile computed with v_mfma_f32_32x32x2f32 (64 FLOP/clk per
 //    SIMD, the fp32 matrix peak of 157.3 TFLOP/s at 256 CUs);
-//  * A and B tiles are staged k-major in LDS ([BK][BM] and [BK][BN]) and
-//    double buffered: the global loads of chunk k+1 are in flight while the
-//    MFMAs of chunk k run, one barrier per chunk;
+//  * A and B tiles are staged k-major in LDS ([BK][BM] and [BK][BN]); the
+//    global loads of chunk k+1 are in flight in registers while the MFMAs of
+//    chunk k run, and the LDS tile is double buffered (one barrier per
+//    chunk) or, for the 32-deep chunk variant, single (two barriers, half
+//    the LDS);
 //  * within an MFMA the two K lanes (lane / 32) take k and k + BK/2 of the
 //    chunk, so a lane's A/B fragment is one conflict-free ds_read_b32;
 //  * tile ids are remapped so that consecutive tiles land on the same XCD
 //    (each of the 8 XCDs has its own L2) and walked in GROUP_M row groups;
-//  * full interior tiles use float4 global loads without bounds checks,
-//    edge tiles and ragged K fall back to guarded scalar loads.
+//  * interior tiles run a loop body with float4 global loads and no bounds
+//    checks (chosen once per workgroup, so the loop carries no branches);
+//    edge tiles and a ragged last K chunk use guarded scalar loads;
+//  * long K over few output tiles is split across workgroups (grid z) into
+//    partials that a second pass adds in split order, so results do not
+//    depend on timing.
 #include "common.h"
 
 namespace {
@@ -64,15 +70,17 @@ struct GemmCfg {
   static_assert(PA >= 1 && PB >= 1, "tile too small for 256 threads");
 };
 
-template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB>
+// NBUF = 2: double-buffered LDS tiles, one barrier per K chunk; NBUF = 1: one
+// LDS tile (half the LDS, so more workgroups per CU), two barriers per chunk.
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, int NBUF>
 __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
   using Cfg = GemmCfg<BM, BN, BK, WM, WN, TA, TB>;
   constexpr int TM = Cfg::TM, TN = Cfg::TN;
   constexpr int LDA_S = Cfg::LDA_S, LDB_S = Cfg::LDB_S;
   constexpr int PA = Cfg::PA, PB = Cfg::PB;
 
-  __shared__ __attribute__((aligned(16))) float As[2][BK * LDA_S];
-  __shared__ __attribute__((aligned(16))) float Bs[2][BK * LDB_S];
+  __shared__ __attribute__((aligned(16))) float As[NBUF][BK * LDA_S];
+  __shared__ __attribute__((aligned(16))) float Bs[NBUF][BK * LDB_S];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -107,7 +115,10 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
   float4 ra[PA], rb[PB];
 
   // ---- global -> registers for the K chunk starting at k0 ---------------
-  auto load_chunk = [&](int64_t k0, bool fast) {
+  // fast: the chunk lies inside M, N and K and float4 loads are aligned, so
+  // no per-element guard is needed (a compile-time choice of the caller).
+  auto load_chunk = [&](int64_t k0, auto fast_tag) {
+    constexpr bool fast = decltype(fast_tag)::value;
 #pragma unroll
     for (int p = 0; p < PA; ++p) {
       const int f = p * 256 + tid;  // float4 index within the A tile
@@ -225,19 +236,9 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
   const int a_off = wm * WM + l32;
   const int b_off = wn * WN + l32;
 
-  const int64_t nk = (K - kbeg + BK - 1) / BK;
-  load_chunk(kbeg, full_mn && kbeg + BK <= K);
-  store_chunk(0);
-  __syncthreads();
-
-  for (int64_t kc = 0; kc < nk; ++kc) {
-    const int cur = (int)(kc & 1);
-    if (kc + 1 < nk) {
-      const int64_t k1 = kbeg + (kc + 1) * BK;
-      load_chunk(k1, full_mn && k1 + BK <= K);
-    }
-    const float* as = As[cur];
-    const float* bs = Bs[cur];
+  auto compute_chunk = [&](int buf) {
+    const float* as = As[buf];
+    const float* bs = Bs[buf];
 #pragma unroll
     for (int s = 0; s < BK / 2; ++s) {
       const int kk = s + half * (BK / 2);
@@ -252,9 +253,39 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
         for (int b = 0; b < TN; ++b)
           acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a], bf[b], acc[a][b], 0, 0, 0);
     }
-    if (kc + 1 < nk) store_chunk(cur ^ 1);
+  };
+
+  // K chunks [kbeg, K) of BK.  Interior tiles (full_mn) load every chunk but
+  // a ragged last one without guards; edge tiles always use guarded loads.
+  // The branch on full_mn is taken once, so each loop body is branch-free.
+  const int64_t nk = (K - kbeg + BK - 1) / BK;
+  auto main_loop = [&](auto full_tag) {
+    constexpr bool FULL = decltype(full_tag)::value;
+    const int64_t nfast = FULL ? (K - kbeg) / BK : 0;  // chunks loadable without guards
+    auto load = [&](int64_t kc) {
+      if (FULL && kc < nfast)
+        load_chunk(kbeg + kc * BK, std::true_type{});
+      else
+        load_chunk(kbeg + kc * BK, std::false_type{});
+    };
+    load(0);
+    store_chunk(0);
     __syncthreads();
-  }
+    for (int64_t kc = 0; kc < nk; ++kc) {
+      const int cur = NBUF == 2 ? (int)(kc & 1) : 0;
+      if (kc + 1 < nk) load(kc + 1);
+      compute_chunk(cur);
+      if (kc + 1 < nk) {
+        if (NBUF == 1) __syncthreads();  // every wave is done reading the tile
+        store_chunk(NBUF == 2 ? cur ^ 1 : 0);
+      }
+      __syncthreads();
+    }
+  };
+  if (full_mn)
+    main_loop(std::true_type{});
+  else
+    main_loop(std::false_type{});
 
   // ---- epilogue: D[i][j] of a 32x32 tile sits in lane j + 32*((i/4)%2),
   //      register (i%4) + 4*(i/8) --------------------------------------------
@@ -285,7 +316,7 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
   }
 }
 
-template <int BM, int BN, int BK, int WM, int WN>
+template <int BM, int BN, int BK, int WM, int WN, int NBUF>
 int launch_tiles(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits);
 
 // Adds the split-K partials part[z][b][M][N] in split order (deterministic)
@@ -310,14 +341,14 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmArgs g,
   }
 }
 
-template <int BM, int BN, int BK, int WM, int WN>
+template <int BM, int BN, int BK, int WM, int WN, int NBUF = 2>
 int launch_cfg(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits = 1) {
   g.tiles_m = (int)((g.M + BM - 1) / BM);
   g.tiles_n = (int)((g.N + BN - 1) / BN);
   if (splits <= 1) {
     g.kps = g.K > 0 ? g.K : 1;
     g.sZ = 0;
-    return launch_tiles<BM, BN, BK, WM, WN>(g, batch, ta, tb, 1);
+    return launch_tiles<BM, BN, BK, WM, WN, NBUF>(g, batch, ta, tb, 1);
   }
   // Split K: partial products go to a scratch buffer (bias off), then one
   // pass adds them in split order and applies the bias.
@@ -334,7 +365,7 @@ int launch_cfg(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits = 1) {
   p.sZ = n;
   p.kps = kps;
   p.bias_mode = 0;
-  int rc = launch_tiles<BM, BN, BK, WM, WN>(p, batch, ta, tb, splits);
+  int rc = launch_tiles<BM, BN, BK, WM, WN, NBUF>(p, batch, ta, tb, splits);
   if (rc == WXX_OK) {
     hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3(wxx::grid_1d(n, 256, 8192)), dim3(256), 0,
                        wxx::stream(), g, (const float*)part, splits, batch);
@@ -345,22 +376,22 @@ int launch_cfg(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits = 1) {
   return rc;
 }
 
-template <int BM, int BN, int BK, int WM, int WN>
+template <int BM, int BN, int BK, int WM, int WN, int NBUF>
 int launch_tiles(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits) {
   dim3 grid((unsigned)(g.tiles_m * g.tiles_n), (unsigned)batch, (unsigned)splits);
   hipStream_t s = wxx::stream();
   if (!ta && !tb)
-    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, false>), grid, dim3(256),
-                       0, s, g);
+    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, false, NBUF>), grid,
+                       dim3(256), 0, s, g);
   else if (!ta && tb)
-    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, true>), grid, dim3(256),
-                       0, s, g);
+    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, true, NBUF>), grid,
+                       dim3(256), 0, s, g);
   else if (ta && !tb)
-    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, false>), grid, dim3(256),
-                       0, s, g);
+    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, false, NBUF>), grid,
+                       dim3(256), 0, s, g);
   else
-    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, true>), grid, dim3(256),
-                       0, s, g);
+    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, true, NBUF>), grid,
+                       dim3(256), 0, s, g);
   WXX_LAUNCHED();
   return WXX_OK;
 }
@@ -371,7 +402,9 @@ inline bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 // Replaces functional.matmul_add (reference src/wxx/functional/utils.py:378-499).
 // Strides are in elements; sA / sB == 0 marks an unbatched operand.
-// tile: 0 = choose automatically, 1 = 64x64, 2 = 128x128, 3 = 256x128.
+// tile: 0 = choose automatically, 1 = 64x64, 2 = 128x128, 3 = 256x128; 4-8 select
+// alternative tile / K-chunk / buffering shapes of the same kernel.  With an
+// explicit tile code, bits 8-15 give the number of K splits (0 or 1: none).
 WXX_API int wxx_matmul_add(const float* A, const float* B, const float* bias, float* C,
                            int64_t M, int64_t N, int64_t K, int64_t batch, int64_t sA,
                            int64_t sB, int64_t sBias, int bias_mode, int transpose_A,
@@ -421,26 +454,36 @@ WXX_API int wxx_matmul_add(const float* A, const float* B, const float* bias, fl
     // Empty contraction: C = bias (or 0).  Reuse the kernel with K = 0: the
     // k-loop is skipped and the epilogue writes the bias.
   }
-  int splits = 1;
+  int splits = (tile >> 8) & 0xff;
+  tile &= 0xff;
+  WXX_REQUIRE(splits <= 64, "bad split count %d", splits);
+  splits = std::max(splits, 1);
   if (tile == 0) {
+    // Measured on MI355X (fp32 GEMM shapes of GPT-2 small and BASELINE
+    // config 2): 128x128 tiles are the fastest once they cover the CUs;
+    // the 32-deep single-buffered variant wins for long K; 64x64 tiles win
+    // for thin operands (attention's N = 64 / K = 64 products) and when the
+    // grid would otherwise leave CUs idle; K is split only when the output
+    // tiles cannot cover the CUs twice and every split keeps >= 1024 of K.
     const int64_t cus = wxx::num_cus() > 0 ? wxx::num_cus() : 256;
     const int64_t t128 = ((g.M + 127) / 128) * ((g.N + 127) / 128) * nb;
-    const int64_t t256 = ((g.M + 255) / 256) * ((g.N + 127) / 128) * nb;
-    if (t256 >= 2 * cus && g.K >= 256) {
-      tile = 3;
+    const int64_t t64 = ((g.M + 63) / 64) * ((g.N + 63) / 64) * nb;
+    const int64_t kmax = std::max<int64_t>(g.K / 1024, 1);
+    if (g.M <= 64 || g.N <= 64 || g.K <= 128) {
+      tile = 1;
+      if (t64 < 2 * cus) splits = (int)std::min<int64_t>((8 * cus + t64 - 1) / t64, kmax);
     } else if (t128 >= cus) {
-      tile = 2;
-    } else if (g.M >= 128 && g.N >= 128 && g.K >= 1024) {
-      // Few output tiles over a long K (weight gradients: K = batch x rows):
-      // 128x128 tiles with K split until the grid covers the CUs twice,
-      // keeping at least 256 K per split.
-      tile = 2;
-      splits = (int)std::min<int64_t>((2 * cus + t128 - 1) / t128, g.K / 256);
+      tile = g.K >= 4096 ? 4 : 2;
+      if (t128 < 2 * cus && g.K >= 2048) {
+        tile = 2;
+        splits = 2;
+      }
+    } else if (2 * t128 >= cus && g.K >= 4096) {
+      tile = 4;
+      splits = (int)std::min<int64_t>((4 * cus + t128 - 1) / t128, kmax);
     } else {
       tile = 1;
-      const int64_t t64 = ((g.M + 63) / 64) * ((g.N + 63) / 64) * nb;
-      if (t64 < cus && g.K >= 1024)
-        splits = (int)std::min<int64_t>((2 * cus + t64 - 1) / t64, g.K / 256);
+      if (t64 < 2 * cus) splits = (int)std::min<int64_t>((8 * cus + t64 - 1) / t64, kmax);
     }
     splits = std::max(1, std::min(splits, 32));
   }
@@ -448,6 +491,12 @@ WXX_API int wxx_matmul_add(const float* A, const float* B, const float* bias, fl
     case 1: return launch_cfg<64, 64, 16, 32, 32>(g, nb, transpose_A, transpose_B, splits);
     case 2: return launch_cfg<128, 128, 16, 64, 64>(g, nb, transpose_A, transpose_B, splits);
     case 3: return launch_cfg<256, 128, 16, 128, 64>(g, nb, transpose_A, transpose_B, splits);
+    // alternative shapes of the same kernel (K chunk 32, single LDS buffer)
+    case 4: return launch_cfg<128, 128, 32, 64, 64, 1>(g, nb, transpose_A, transpose_B, splits);
+    case 5: return launch_cfg<256, 128, 32, 128, 64, 1>(g, nb, transpose_A, transpose_B, splits);
+    case 6: return launch_cfg<128, 128, 32, 64, 64, 2>(g, nb, transpose_A, transpose_B, splits);
+    case 7: return launch_cfg<256, 128, 32, 128, 64, 2>(g, nb, transpose_A, transpose_B, splits);
+    case 8: return launch_cfg<128, 256, 16, 64, 128>(g, nb, transpose_A, transpose_B, splits);
     default: return wxx::set_error(WXX_E_ARG, "bad tile %d", tile);
   }
 }
