@@ -17,9 +17,9 @@ reports every kernel of the step, and ``extra`` the HBM-bound kernels of the
 other configs measured on the same box (config 4's standalone batched real
 FFT / inverse FFT on [2048 x 16384], a row sum over [8192 x 4096]) and a
 256 MiB device-to-device copy as the achievable-bandwidth reference; and
-the GPT-2 train steps of configs 1 and 5 (forward, CCE loss, backward,
-clip_grad_norm_, AdamW, LR schedule) in tokens/s, timed on the host clock
-between device synchronisations.
+the train steps of configs 1 and 5 (GPT-2), 3 (ResNet18) and 4 (Hyena):
+forward, CCE loss, backward, clip_grad_norm_, AdamW, LR schedule, in tokens/s
+or images/s, timed on the host clock between device synchronisations.
 ``cpu_baseline`` times the oracle's exact-order fp32 GEMM restatement
 (oracle/csrc/gemm_ref.c, OpenMP on the host cores) on a bounded row sample of
 the 4096^3 GEMM, on rank 0 at N=1 only.
@@ -65,7 +65,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--only", default=None, help="run only this component (profiling)")
-    p.add_argument("--no-train", action="store_true", help="skip the GPT-2 train-step extras")
+    p.add_argument("--no-train", action="store_true", help="skip the train-step extras")
     return p.parse_args()
 
 
@@ -174,33 +174,61 @@ class Kernels:
                                 0)
 
 
-# BASELINE configs 1 and 5: GPT-2 train steps (tokens / s), dropout 0.
-GPT2_CONFIGS = {
-    "gpt2_train_config1": dict(V=1024, D=256, H=8, L=6, B=4, S=128, max_len=256),
-    "gpt2_train_config5": dict(V=50304, D=768, H=12, L=12, B=8, S=1024, max_len=1024),
+# BASELINE train-step configs: GPT-2 (1, 5), ResNet18 (3), Hyena (4); dropout 0.
+TRAIN_CONFIGS = {
+    "gpt2_train_config1": dict(kind="gpt2", V=1024, D=256, H=8, L=6, B=4, S=128, max_len=256,
+                               flop=1.651e10),
+    "resnet18_train_config3": dict(kind="resnet18", classes=10, B=128, HW=32),
+    "hyena_train_config4": dict(kind="hyena", V=1024, D=256, L=6, order=4, B=8, S=8192),
+    "gpt2_train_config5": dict(kind="gpt2", V=50304, D=768, H=12, L=12, B=8, S=1024,
+                               max_len=1024, flop=7.001e12),
 }
-GPT2_FLOP = {"gpt2_train_config1": 1.651e10, "gpt2_train_config5": 7.001e12}
 
 
-def gpt2_train_step(lib, name, steps, warmup):
+def _train_setup(wxx, c, r):
+    """Model, optimizer, inputs and a loss closure for one BASELINE train config
+    (random-init weights, synthetic inputs of the config's shape)."""
+    F = wxx.functional
+    lossf = wxx.nn.CCELoss()
+    if c["kind"] == "gpt2":
+        m = wxx.nn.GPT2(c["V"], c["D"], c["H"], c["L"], max_len=c["max_len"], dropout=0.0)
+        x = F.from_numpy(r.integers(0, c["V"], (c["B"], c["S"])), np.uint32)
+        y = F.from_numpy(r.integers(0, c["V"], (c["B"] * c["S"],)), np.uint32)
+        loss = lambda: lossf(m(x).reshape((c["B"] * c["S"], c["V"])), y)  # noqa: E731
+        units, unit = c["B"] * c["S"], "tokens"
+        desc = (f"GPT2(vocab {c['V']}, d {c['D']}, heads {c['H']}, layers {c['L']}), "
+                f"batch {c['B']} x seq {c['S']}, dropout 0")
+    elif c["kind"] == "resnet18":
+        m = wxx.nn.ResNet18(num_classes=c["classes"])
+        x = F.from_numpy(r.standard_normal((c["B"], 3, c["HW"], c["HW"]), dtype=np.float32))
+        y = F.from_numpy(r.integers(0, c["classes"], (c["B"],)), np.uint32)
+        loss = lambda: lossf(m(x), y)  # noqa: E731
+        units, unit = c["B"], "images"
+        desc = f"ResNet18(num_classes {c['classes']}), batch {c['B']} x 3x{c['HW']}x{c['HW']}"
+    else:
+        m = wxx.nn.Hyena(c["V"], d_model=c["D"], n_layers=c["L"], order=c["order"])
+        x = F.from_numpy(r.integers(0, c["V"], (c["B"], c["S"])), np.uint32)
+        y = F.from_numpy(r.integers(0, c["V"], (c["B"] * c["S"],)), np.uint32)
+        loss = lambda: lossf(m(x).reshape((c["B"] * c["S"], c["V"])), y)  # noqa: E731
+        units, unit = c["B"] * c["S"], "tokens"
+        desc = (f"Hyena(vocab {c['V']}, d {c['D']}, layers {c['L']}, order {c['order']}), "
+                f"batch {c['B']} x seq {c['S']}")
+    return m, loss, units, unit, desc
+
+
+def train_step(lib, name, steps, warmup):
     """Full train step: forward, CCELoss, backward, clip_grad_norm_(1.0), AdamW,
-    WarmupCosineLR (README.md:50-51 schedule), zero_grad.  Synthetic uniform
-    token ids; random-init weights.  Timed with the host clock around
-    ``steps`` steps between device synchronisations."""
+    WarmupCosineLR (README.md:50-51 schedule), zero_grad.  Timed with the host
+    clock around ``steps`` steps between device synchronisations."""
     import wxx_amd as wxx
 
-    c = GPT2_CONFIGS[name]
-    m = wxx.nn.GPT2(c["V"], c["D"], c["H"], c["L"], max_len=c["max_len"], dropout=0.0)
+    c = TRAIN_CONFIGS[name]
+    m, lossfn, units, unit, desc = _train_setup(wxx, c, np.random.default_rng(50))
     opt = wxx.nn.AdamW(m.parameters(), lr=1e-3)
     sched = wxx.nn.WarmupCosineLR(opt, warmup_steps=100, total_steps=5000, min_lr=1e-5)
-    lossf = wxx.nn.CCELoss()
-    r = np.random.default_rng(50)
-    x = wxx.functional.from_numpy(r.integers(0, c["V"], (c["B"], c["S"])), np.uint32)
-    y = wxx.functional.from_numpy(r.integers(0, c["V"], (c["B"] * c["S"],)), np.uint32)
 
     def step():
-        logits = m(x)
-        loss = lossf(logits.reshape((c["B"] * c["S"], c["V"])), y)
+        loss = lossfn()
         loss.backward()
         wxx.nn.clip_grad_norm_(m.parameters(), 1.0)
         opt.step()
@@ -216,13 +244,12 @@ def gpt2_train_step(lib, name, steps, warmup):
         loss = step()
     lib.call("wxx_sync")
     dt = (time.perf_counter() - t0) / steps
-    tokens = c["B"] * c["S"]
-    return {"tokens_per_s": tokens / dt, "ms": dt * 1e3, "steps_timed": steps,
-            "tflops": GPT2_FLOP[name] / dt / 1e12,
-            "frac_of_peak": GPT2_FLOP[name] / dt / 1e12 / PEAK_FP32_TFLOPS,
-            "loss": float(loss.numpy().reshape(-1)[0]),
-            "model": f"GPT2(vocab {c['V']}, d {c['D']}, heads {c['H']}, layers {c['L']}), "
-                     f"batch {c['B']} x seq {c['S']}, dropout 0"}
+    out = {f"{unit}_per_s": units / dt, "ms": dt * 1e3, "steps_timed": steps,
+           "loss": float(loss.numpy().reshape(-1)[0]), "model": desc}
+    if "flop" in c:
+        out["tflops"] = c["flop"] / dt / 1e12
+        out["frac_of_peak"] = out["tflops"] / PEAK_FP32_TFLOPS
+    return out
 
 
 STEP = [n for n, *_ in GEMMS] + ["softmax", "layernorm"]
@@ -241,9 +268,9 @@ def main():
     device.ensure_device()
     ks = Kernels(lib)
     names = STEP + EXTRA
-    if args.only in GPT2_CONFIGS:
+    if args.only in TRAIN_CONFIGS:
         print(json.dumps({"only": args.only,
-                          "component": gpt2_train_step(lib, args.only, args.steps, args.warmup)}))
+                          "component": train_step(lib, args.only, args.steps, args.warmup)}))
         return
     if args.only:
         names = [args.only]
@@ -337,8 +364,8 @@ def main():
         "wall_s": wall_s,
     }
     if not args.no_train:
-        for name in GPT2_CONFIGS:
-            out["extra"][name] = gpt2_train_step(lib, name, steps=5, warmup=2)
+        for name in TRAIN_CONFIGS:
+            out["extra"][name] = train_step(lib, name, steps=5, warmup=2)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_gemm_baseline(args.cpu_seconds)
     print(json.dumps(out))

@@ -234,6 +234,12 @@ int wxx_unfolddx(const float* dy, float* dx, int64_t prefix, int64_t length, int
 int wxx_rfft(const float* x, void* X, int64_t rows, int64_t in_len, int64_t n);
 /* functional.irfft (fft.py:566-645): rows x in_len -> rows x n; n = 2^k, 2 <= n <= 32768 */
 int wxx_irfft(const void* X, float* x, int64_t rows, int64_t in_len, int64_t n);
+/* functional.irfft(..., length=L) and the Hyena crop irfft(...)[..., :L]
+ * (nn/hyena.py:208-216): the first out_len samples of each row (row stride
+ * out_len), times post_scale after the 1/n normalisation (the rfft backward's
+ * factor n, autograd/utils.py:549-718). */
+int wxx_irfft_crop(const void* X, float* x, int64_t rows, int64_t in_len, int64_t n,
+                   int64_t out_len, float post_scale);
 /* functional.complex_mul (fft.py:168-213, op 0) and complex_add_inplace
  * (fft.py:216-245, op 1); strides in complex elements, 0 = broadcast */
 int wxx_complex_binary(void* out, const void* a, const void* b, int rank, const int64_t* shape,

@@ -369,3 +369,45 @@ def test_unfold_argument_errors(device):
             x.unfold(dim, 2)
     with pytest.raises(ValueError):
         f32(np.zeros((2,) * 6)).unfold(0, 2)
+
+
+# ---- slice gradients reaching one tensor ----------------------------------------
+
+
+def test_chunk_gradients_tile_the_input(device):
+    a = rng(70).standard_normal((3, 8, 12)).astype(np.float32)
+    x = f32(a, True)
+    ws = [rng(71 + i).standard_normal((3, 8, 3)).astype(np.float32) for i in range(4)]
+    parts = x.chunk(4, dim=-1)
+    loss = None
+    for p, w in zip(parts, ws):
+        t = (p * f32(w)).sum()
+        loss = t if loss is None else loss + t
+    loss.backward()
+    np.testing.assert_array_equal(x.grad.numpy(), np.concatenate(ws, axis=-1))
+
+
+def test_partial_and_overlapping_slice_gradients(device):
+    a = rng(72).standard_normal((4, 10)).astype(np.float32)
+    # only chunks 0 and 2 of 5 used: zeros elsewhere
+    x = f32(a, True)
+    c = x.chunk(5, dim=1)
+    w0, w2 = (rng(73 + i).standard_normal((4, 2)).astype(np.float32) for i in range(2))
+    ((c[0] * f32(w0)).sum() + (c[2] * f32(w2)).sum()).backward()
+    want = np.zeros((4, 10), np.float32)
+    want[:, 0:2], want[:, 4:6] = w0, w2
+    np.testing.assert_array_equal(x.grad.numpy(), want)
+    # overlapping slices, a dense use of the same tensor, and a slice along another dim
+    y = f32(a, True)
+    u = rng(75).standard_normal((4, 3)).astype(np.float32)
+    v = rng(76).standard_normal((4, 4)).astype(np.float32)
+    d = rng(77).standard_normal((4, 10)).astype(np.float32)
+    r = rng(78).standard_normal((2, 10)).astype(np.float32)
+    loss = ((y[:, 0:3] * f32(u)).sum() + (y.slice(1, 2, 4) * f32(v)).sum()
+            + (y * f32(d)).sum() + (y.slice(0, 1, 2) * f32(r)).sum())
+    loss.backward()
+    want = d.astype(np.float64).copy()
+    want[:, 0:3] += u
+    want[:, 2:6] += v
+    want[1:3, :] += r
+    np.testing.assert_allclose(y.grad.numpy(), want, rtol=1e-6, atol=1e-6)

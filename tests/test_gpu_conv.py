@@ -168,7 +168,11 @@ def test_adaptive_avgpool2d(device, shape, out):
 
 
 @pytest.mark.parametrize("B,D,L,K,view", [(2, 5, 17, 3, False), (8, 256, 8192, 3, True),
-                                           (1, 3, 2, 4, False)])
+                                           (1, 3, 2, 4, False),
+                                           (3, 70, 130, 5, True),    # partial channel / position tiles
+                                           (2, 65, 200, 8, False),   # largest tiled kernel size
+                                           (2, 9, 40, 9, True),      # untiled kernels (K > 8)
+                                           (5, 130, 64, 1, True)])
 def test_causal_conv1d(device, B, D, L, K, view):
     r = rng(D)
     w = r.standard_normal((D, K)).astype(np.float32)

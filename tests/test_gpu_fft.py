@@ -191,3 +191,43 @@ def test_complex_support_ops(device):
     assert not t.is_contiguous()
     assert np.array_equal(F().complex_contiguous(t).numpy(), a[:, ::3])
     assert np.array_equal(F().complex_conj(t).numpy(), np.conj(a[:, ::3]))
+
+
+@pytest.mark.parametrize("n,length", [(16, 16), (16, 8), (16, 5), (64, 33), (4096, 2048),
+                                      (16384, 8192), (16384, 8191), (16384, 1)])
+@pytest.mark.parametrize("scale", [1.0, 16384.0])
+def test_irfft_crop_equals_full_transform_sliced(device, n, length, scale):
+    # the cropping inverse transform writes exactly the values of the full
+    # transform's first `length` samples (times `scale`), bit for bit
+    r = rng(n + length)
+    rows, nb = 5, n // 2 + 1
+    X = (r.standard_normal((rows, nb)) + 1j * r.standard_normal((rows, nb))).astype(np.complex64)
+    full = F().irfft(upc(X), n).numpy()
+    want = full[:, :length]
+    if scale != 1.0:
+        want = want * np.float32(scale)
+    got = F().irfft(upc(X), n, length=length, scale=scale).numpy()
+    assert got.shape == (rows, length)
+    np.testing.assert_array_equal(got, want)
+    with pytest.raises(ValueError):
+        F().irfft(upc(X), n, length=n + 1)
+
+
+@pytest.mark.parametrize("L,n", [(8, 16), (7, 16), (2048, 4096), (8192, 16384)])
+def test_fft_conv_crop_autograd_matches_sliced_path(device, L, n):
+    # the Hyena long convolution with the fused crop: output and both input
+    # gradients identical to irfft(...)[..., :L] through the slice backward
+    r = rng(L)
+    X = r.standard_normal((2, 3, L)).astype(np.float32)
+    H = r.standard_normal((3, L)).astype(np.float32)
+    G = r.standard_normal((2, 3, L)).astype(np.float32)
+    res = []
+    for fused in (True, False):
+        x, h = up(X), up(H)
+        x.requires_grad = h.requires_grad = True
+        spec = x.rfft(n).complex_mul(h.rfft(n))
+        y = spec.irfft(n, L) if fused else spec.irfft(n)[..., :L]
+        (y * up(G)).sum().backward()
+        res.append((y.numpy(), x.grad.numpy(), h.grad.numpy()))
+    for a, b in zip(*res):
+        np.testing.assert_array_equal(a, b)

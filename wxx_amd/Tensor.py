@@ -590,10 +590,10 @@ class Tensor:
 
         return autograd.rfft(self).forward(self, n)
 
-    def irfft(self, n=None):
+    def irfft(self, n=None, length=None):
         from . import autograd
 
-        return autograd.irfft(self).forward(self, n)
+        return autograd.irfft(self).forward(self, n, length)
 
     def complex_mul(self, other):
         from . import autograd

@@ -17,10 +17,13 @@ class Conv2D(Function):
         x, w, bias = self.tensor1, self.W, self.bias
         self.tensor1 = self.W = self.bias = None
         args = (self.stride, self.padding, self.dilation, self.Xshape, self.wshape)
-        dw = functional.conv2ddw(grad_output, x, *args)
-        dx = functional.conv2ddx(grad_output, w, *args)
+        # a gradient nobody asked for is not computed (the network input's dX)
+        dw = functional.conv2ddw(grad_output, x, *args) if self.needs_input_grad[1] else None
+        dx = functional.conv2ddx(grad_output, w, *args) if self.needs_input_grad[0] else None
         if bias is None:
             return dx, dw
+        if not self.needs_input_grad[2]:
+            return dx, dw, None
         if len(grad_output.shape) == 4:
             db = grad_output.sum(axis=(2, 3)).sum(axis=0)
         else:

@@ -15,7 +15,60 @@ from .. import functional
 from ..backend.context import inferenceMode
 
 
+class SliceGrad:
+    """A gradient that is zero outside slices of a tensor of ``shape``: each
+    part ``(dim, start, g)`` holds ``g`` at ``[start, start + len)`` along
+    ``dim``.  The backward of narrow / chunk / a basic slice returns one;
+    gradients reaching the same tensor from several slices are merged here
+    and written into one buffer when the tensor's backward runs, instead of
+    a zero-filled full-size tensor per slice added together.  The values
+    are those of the dense sum (x + 0 == x), up to the sign of a zero."""
+
+    __slots__ = ("shape", "parts")
+
+    def __init__(self, shape, dim, start, g):
+        self.shape = list(shape)
+        self.parts = [(dim, start, g)]
+
+    def merged(self, other):
+        out = SliceGrad.__new__(SliceGrad)
+        out.shape = self.shape
+        out.parts = self.parts + other.parts
+        return out
+
+    def dense(self):
+        from ..Tensor import Tensor
+        from ..functional._common import empty
+
+        dims = {d for d, _, _ in self.parts}
+        disjoint = covered = False
+        if len(dims) == 1:
+            (d,) = dims
+            spans = sorted((st, st + g.shape[d]) for _, st, g in self.parts)
+            disjoint = all(a[1] <= b[0] for a, b in zip(spans, spans[1:]))
+            covered = disjoint and spans[0][0] == 0 and spans[-1][1] == self.shape[d] and all(
+                a[1] == b[0] for a, b in zip(spans, spans[1:]))
+        if disjoint:
+            out = empty(self.shape) if covered else Tensor(self.shape, value=0.0)
+            for d, st, g in self.parts:
+                functional.assign(out.narrow(d, st, g.shape[d]), g)
+            return out
+        # overlapping slices: add each part into a zero tensor, in arrival order
+        out = Tensor(self.shape, value=0.0)
+        for d, st, g in self.parts:
+            view = out.narrow(d, st, g.shape[d])
+            functional.assign(view, functional.pointwise(view, g, 0))
+        return out
+
+
+def _dense(g):
+    return g.dense() if isinstance(g, SliceGrad) else g
+
+
 def _add(acc, grad):
+    if isinstance(acc, SliceGrad) and isinstance(grad, SliceGrad) and acc.shape == grad.shape:
+        return acc.merged(grad)
+    acc, grad = _dense(acc), _dense(grad)
     if getattr(acc, "type", "f32") == "c64":
         return functional.complex_add(acc, grad)
     return functional.pointwise(acc, grad, 0)
@@ -56,6 +109,7 @@ def run_backward(root):
                     t.creator.inputs = None
                     t.creator = None
                 continue
+            g = _dense(g)
             fn = t.creator
             if fn is not None:
                 pg = fn.backward(g)

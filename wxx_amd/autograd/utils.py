@@ -14,6 +14,7 @@ import math
 from .. import functional, validation
 from ..backend.dispatch import _sum_to_shape
 from ..Tensor import Tensor
+from .engine import SliceGrad
 from .function import Function
 
 
@@ -160,8 +161,9 @@ class narrow(Function):
     def backward(self, g):
         if not self.needs_input_grad[0]:
             return None
-        if self.in_type == "f32" and len(self.in_shape) <= validation.MAX_RANK:
-            return functional.scatter_zeros(g, self.in_shape, self.dim, self.start)
+        if self.in_type == "f32" and g.type == "f32":
+            # deferred: the engine writes the slices of one tensor into one buffer
+            return SliceGrad(self.in_shape, self.dim, self.start, g)
         dx = Tensor(self.in_shape, value=0, dtype=self.in_type)
         functional.assign(dx.narrow(self.dim, self.start, self.length), g)
         return dx
@@ -205,8 +207,8 @@ class getitem(Function):
         if not self.needs_input_grad[0]:
             return None
         target = _single_slice(self.index, self.in_shape)
-        if target is not None and self.in_type == "f32":
-            return functional.scatter_zeros(g, self.in_shape, target[0], target[1])
+        if target is not None and self.in_type == "f32" and g.type == "f32":
+            return SliceGrad(self.in_shape, target[0], target[1], g)
         dx = Tensor(self.in_shape, value=0, dtype=self.in_type)
         functional.assign(dx._basic_getitem(self._full_index()), g)
         return dx
@@ -362,14 +364,20 @@ class rfft(Function):
         if not self.needs_input_grad[0]:
             return None
         w = functional.complex_weights(_rfft_backward_weights(self.N))
-        ga = functional.irfft(functional.complex_mul(g, w), self.N)
-        ga = functional.scalarpointwise(ga, float(self.N), 2)
+        # irfft(g w, N) * N cropped to the input length, in one kernel (the
+        # crop and the factor N give the same values as separate passes)
+        ga = functional.irfft(functional.complex_mul(g, w), self.N,
+                              length=min(self.in_len, self.N), scale=float(self.N))
         return _match_last_dim_real(ga, self.in_len)
 
 
 class irfft(Function):
-    def forward(self, tensor1, n=None):
-        out = functional.irfft(tensor1, n)
+    """``length`` keeps the first ``length`` output samples (the crop
+    ``irfft(x, n)[..., :length]``); its backward is the rfft of the cropped
+    gradient zero-padded to n, which rfft's own padding provides."""
+
+    def forward(self, tensor1, n=None, length=None):
+        out = functional.irfft(tensor1, n, length=length)
         self.N = 2 * (tensor1.shape[-1] - 1) if n is None else int(n)
         self.in_len = tensor1.shape[-1]
         out.requires_grad = tensor1.requires_grad

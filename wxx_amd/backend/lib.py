@@ -93,6 +93,7 @@ SIGNATURES = {
     # FFT / complex
     "wxx_rfft": (I32, [P, P, I64, I64, I64]),
     "wxx_irfft": (I32, [P, P, I64, I64, I64]),
+    "wxx_irfft_crop": (I32, [P, P, I64, I64, I64, I64, F32]),
     "wxx_complex_binary": (I32, [P, P, P, I32, P, P, P, P, I32, I32, I32]),
     "wxx_complex_conj": (I32, [P, P, I32, P, P, P]),
     "wxx_complex_pad": (I32, [P, P, I64, I64, I64]),

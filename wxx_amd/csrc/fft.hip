@@ -149,13 +149,67 @@ __device__ __forceinline__ void pass_math(float2* v, int t, const float2* __rest
   }
 }
 
+// Destination of an inverse transform's real output row: samples [0, lim) of
+// the row starting at p, each scaled by scale and then by post (two roundings,
+// the same values a separate scaling pass would give).  mode 0: the whole row
+// (lim = 2M, float2 stores); 1: an even lim (float2 stores below lim); 2: an
+// odd lim (scalar stores below lim).
+struct RowOut {
+  float* p;
+  int64_t lim;
+  float scale, post;
+  int mode;
+  int lim32, half;  // lim and lim / 2 as 32-bit ints for the store guards
+};
+
+// Stores the real pair z (samples 2j, 2j + 1) of row o; CROP is o.mode,
+// fixed at compile time so the uncropped kernel keeps plain float2 stores.
+template <int CROP>
+__device__ __forceinline__ void row_store(const RowOut& o, int j, float2 z) {
+  z = make_float2((z.x * o.scale) * o.post, (z.y * o.scale) * o.post);
+  if (CROP == 0) {
+    reinterpret_cast<float2*>(o.p)[j] = z;
+  } else if (CROP == 1) {
+    if (j < o.half) reinterpret_cast<float2*>(o.p)[j] = z;  // half = lim / 2
+  } else {
+    const int i = 2 * j;
+    if (i < o.lim32) o.p[i] = z.x;
+    if (i + 1 < o.lim32) o.p[i + 1] = z.y;
+  }
+}
+
+// The last Stockham pass stores point (q, k) of thread t at sample pair
+// j = u + k * GR with u = t + q * T in [0, GR).  An even crop keeps pairs
+// j < half: every k below half / GR, and u < half % GR at k = half / GR, so
+// the guards are uniform branches plus one lane compare per q.
+template <int CROP, int Q, int R, int BITS, int T, int GR>
+__device__ __forceinline__ void last_pass_store(const RowOut& o, const float2* v, int t) {
+  if constexpr (CROP == 1) {
+    const int kfull = o.half / GR, rem = o.half % GR;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const int u = t + q * T;
+      const bool tail = u < rem;
+#pragma unroll
+      for (int k = 0; k < R; ++k)
+        if (k < kfull || (k == kfull && tail))
+          row_store<0>(o, u + k * GR, v[q * R + bitrev(k, BITS)]);
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+#pragma unroll
+      for (int k = 0; k < R; ++k) row_store<CROP>(o, t + q * T + k * GR, v[q * R + bitrev(k, BITS)]);
+  }
+}
+
 // Passes P.. of the transform.  On entry v holds pass P's input points
 // (P == 0: loaded by the caller).  On exit the transform is in buf in natural
-// order (TO_GLOBAL false) or written to gout * scale (TO_GLOBAL true).
-template <int LOGM, int P, bool INV, bool TO_GLOBAL>
+// order (TO_GLOBAL false) or stored to the row o (TO_GLOBAL true).
+template <int LOGM, int P, bool INV, bool TO_GLOBAL, int CROP = 0>
 __device__ __forceinline__ void run_passes(float2* v, float2* buf, int t,
-                                           const float2* __restrict__ tw, float2* gout,
-                                           float scale, bool live) {
+                                           const float2* __restrict__ tw, const RowOut& o,
+                                           bool live) {
   using G = Geo<LOGM>;
   constexpr Plan pl{LOGM};
   constexpr int BITS = pl.bits(P), R = 1 << BITS, NSB = pl.ns_bits(P), NS = 1 << NSB;
@@ -170,15 +224,7 @@ __device__ __forceinline__ void run_passes(float2* v, float2* buf, int t,
   constexpr bool LAST = P + 1 == pl.npass();
   if constexpr (LAST && TO_GLOBAL) {
     // Last pass: NS == GR, so the output position of (group g, k) is g + k*GR.
-    if (live) {
-#pragma unroll
-      for (int q = 0; q < G::E / R; ++q)
-#pragma unroll
-        for (int k = 0; k < R; ++k) {
-          const float2 z = v[q * R + bitrev(k, BITS)];
-          gout[t + q * G::T + k * GR] = make_float2(z.x * scale, z.y * scale);
-        }
-    }
+    if (live) last_pass_store<CROP, G::E / R, R, BITS, G::T, GR>(o, v, t);
   } else {
     if constexpr (P > 0) __syncthreads();  // every thread has read its pass input
 #pragma unroll
@@ -189,7 +235,7 @@ __device__ __forceinline__ void run_passes(float2* v, float2* buf, int t,
       for (int k = 0; k < R; ++k) buf[lds_pad(base + k * NS)] = v[q * R + bitrev(k, BITS)];
     }
     __syncthreads();
-    if constexpr (!LAST) run_passes<LOGM, P + 1, INV, TO_GLOBAL>(v, buf, t, tw, gout, scale, live);
+    if constexpr (!LAST) run_passes<LOGM, P + 1, INV, TO_GLOBAL, CROP>(v, buf, t, tw, o, live);
   }
 }
 
@@ -227,7 +273,7 @@ __global__ __launch_bounds__(Geo<LOGM>::NT) void rfft_kernel(const float* __rest
       }
       v[q * R0 + r] = z;
     }
-  run_passes<LOGM, 0, false, false>(v, buf, t, tw, nullptr, 1.f, live);
+  run_passes<LOGM, 0, false, false>(v, buf, t, tw, RowOut{}, live);
 
   if (!live) return;
   const float2* wu = tw + pl.offset(pl.npass());
@@ -243,11 +289,12 @@ __global__ __launch_bounds__(Geo<LOGM>::NT) void rfft_kernel(const float* __rest
 }
 
 // X: rows x in_len c64 one-sided spectrum; x: rows x n f32 (n = 2M).
-template <int LOGM>
+template <int LOGM, int CROP>
 __global__ __launch_bounds__(Geo<LOGM>::NT) void irfft_kernel(const float2* __restrict__ X,
                                                               float* __restrict__ x,
                                                               const float2* __restrict__ tw,
-                                                              int64_t rows, int64_t in_len) {
+                                                              int64_t rows, int64_t in_len,
+                                                              RowOut ro) {
   using G = Geo<LOGM>;
   constexpr Plan pl{LOGM};
   __shared__ float2 lds[G::RPB * G::PM];
@@ -283,8 +330,8 @@ __global__ __launch_bounds__(Geo<LOGM>::NT) void irfft_kernel(const float2* __re
       const float2 o = make_float2(d.x * w.x + d.y * w.y, d.y * w.x - d.x * w.y);
       v[q * R0 + r] = make_float2(e.x - o.y, e.y + o.x);
     }
-  float2* out = reinterpret_cast<float2*>(x + (live ? row : 0) * (2 * (int64_t)G::M));
-  run_passes<LOGM, 0, true, true>(v, buf, t, tw, out, 1.0f / G::M, live);
+  ro.p = x + (live ? row : 0) * ro.lim;
+  run_passes<LOGM, 0, true, true, CROP>(v, buf, t, tw, ro, live);
 }
 
 // ---- rows of M >= 2048 complex points: persistent workgroups -----------------
@@ -433,9 +480,9 @@ __device__ __forceinline__ void load_tw_bases(float2* twb, int t, const float2* 
 // Passes P.. of one row (see run_passes for the Stockham indexing).  v holds
 // pass P's input (P == 0: loaded by the caller).  SYNC0: barrier before pass
 // 0 writes LDS (other threads may still read the row buffer).
-template <int LOGM, int P, bool INV, bool TO_GLOBAL, bool SYNC0>
+template <int LOGM, int P, bool INV, bool TO_GLOBAL, bool SYNC0, int CROP = 0>
 __device__ __forceinline__ void big_passes(float2* v, float2* buf, int t, const float2* twb,
-                                           float2* gout, float scale) {
+                                           const RowOut& o) {
   using G = Big<LOGM>;
   constexpr int BITS = G::bits(P), R = 1 << BITS, NSB = G::nsb(P), NS = 1 << NSB;
   constexpr int GR = G::M / R, Q = G::E / R;
@@ -452,13 +499,7 @@ __device__ __forceinline__ void big_passes(float2* v, float2* buf, int t, const 
   }
   constexpr bool LAST = P + 1 == G::NP;
   if constexpr (LAST && TO_GLOBAL) {
-#pragma unroll
-    for (int q = 0; q < Q; ++q)
-#pragma unroll
-      for (int k = 0; k < R; ++k) {
-        const float2 z = v[q * R + bitrev(k, BITS)];
-        gout[t + q * G::T + k * GR] = make_float2(z.x * scale, z.y * scale);
-      }
+    last_pass_store<CROP, Q, R, BITS, G::T, GR>(o, v, t);
   } else {
     if constexpr (P > 0 || SYNC0) __syncthreads();
 #pragma unroll
@@ -469,7 +510,7 @@ __device__ __forceinline__ void big_passes(float2* v, float2* buf, int t, const 
       for (int k = 0; k < R; ++k) buf[bpad(base + k * NS)] = v[q * R + bitrev(k, BITS)];
     }
     __syncthreads();
-    if constexpr (!LAST) big_passes<LOGM, P + 1, INV, TO_GLOBAL, SYNC0>(v, buf, t, twb, gout, scale);
+    if constexpr (!LAST) big_passes<LOGM, P + 1, INV, TO_GLOBAL, SYNC0, CROP>(v, buf, t, twb, o);
   }
 }
 
@@ -515,7 +556,7 @@ __global__ __launch_bounds__(Big<LOGM>::T, Big<LOGM>::MIN_BLOCKS) void rfft_big_
     int t = threadIdx.x;
     WXX_OPAQUE(t);
     rfft_big_load<LOGM, VEC>(v, x + row * in_len, t, in_len);
-    big_passes<LOGM, 0, false, false, true>(v, buf, t, twb, nullptr, 1.f);
+    big_passes<LOGM, 0, false, false, true>(v, buf, t, twb, RowOut{});
     // untangle: bins k and M - k from Z[k], Z[M - k]
     float2* Xr = X + row * (G::M + 1);
 #pragma unroll
@@ -556,10 +597,10 @@ __device__ __forceinline__ void irfft_big_load(float2* a, const float2* __restri
   }
 }
 
-template <int LOGM>
+template <int LOGM, int CROP>
 __global__ __launch_bounds__(Big<LOGM>::T, Big<LOGM>::MIN_BLOCKS) void irfft_big_kernel(
     const float2* __restrict__ X, float* __restrict__ x, const float2* __restrict__ tw,
-    int64_t rows, int64_t in_len) {
+    int64_t rows, int64_t in_len, RowOut ro) {
   using G = Big<LOGM>;
   __shared__ float2 buf[G::PM];
   float2 twb[G::NTB];
@@ -593,9 +634,9 @@ __global__ __launch_bounds__(Big<LOGM>::T, Big<LOGM>::MIN_BLOCKS) void irfft_big
       const float2 o = make_float2(d.x * w.x + d.y * w.y, d.y * w.x - d.x * w.y);
       v[e] = make_float2(ee.x - o.y, ee.y + o.x);
     }
-    float2* out = reinterpret_cast<float2*>(x + row * (2 * (int64_t)G::M));
+    ro.p = x + row * ro.lim;
     // SYNC0: every thread has read its pair partner before pass 0 overwrites LDS
-    big_passes<LOGM, 0, true, true, true>(v, buf, t, twb, out, 1.0f / G::M);
+    big_passes<LOGM, 0, true, true, true, CROP>(v, buf, t, twb, ro);
     __syncthreads();  // last pass reads of this row are done
   }
 }
@@ -723,8 +764,10 @@ void launch_rfft(const float* x, float2* X, const float2* tw, int64_t rows, int6
                        rows, in_len);
 }
 
-template <int LOGM>
-void launch_irfft(const float2* X, float* x, const float2* tw, int64_t rows, int64_t in_len) {
+template <int LOGM, int CROP>
+void launch_irfft_mode(const float2* X, float* x, const float2* tw, int64_t rows, int64_t in_len,
+                       RowOut ro) {
+  ro.scale = 1.0f / (float)(1 << LOGM);
   if constexpr (LOGM >= kBigMinLogM) {
     const float2* btw = big_twiddles<LOGM>();
     if (!btw) {
@@ -732,15 +775,26 @@ void launch_irfft(const float2* X, float* x, const float2* tw, int64_t rows, int
       return;
     }
     constexpr int T = Big<LOGM>::T;
-    const unsigned g = persistent_grid(irfft_big_kernel<LOGM>, T, rows);
-    hipLaunchKernelGGL((irfft_big_kernel<LOGM>), dim3(g), dim3(T), 0, wxx::stream(), X, x, btw,
-                       rows, in_len);
+    const unsigned g = persistent_grid(irfft_big_kernel<LOGM, CROP>, T, rows);
+    hipLaunchKernelGGL((irfft_big_kernel<LOGM, CROP>), dim3(g), dim3(T), 0, wxx::stream(), X, x,
+                       btw, rows, in_len, ro);
     return;
   }
   using G = Geo<LOGM>;
   const dim3 grid((unsigned)((rows + G::RPB - 1) / G::RPB));
-  hipLaunchKernelGGL((irfft_kernel<LOGM>), grid, dim3(G::NT), 0, wxx::stream(), X, x, tw, rows,
-                     in_len);
+  hipLaunchKernelGGL((irfft_kernel<LOGM, CROP>), grid, dim3(G::NT), 0, wxx::stream(), X, x, tw,
+                     rows, in_len, ro);
+}
+
+template <int LOGM>
+void launch_irfft(const float2* X, float* x, const float2* tw, int64_t rows, int64_t in_len,
+                  RowOut ro) {
+  if (ro.mode == 0)
+    launch_irfft_mode<LOGM, 0>(X, x, tw, rows, in_len, ro);
+  else if (ro.mode == 1)
+    launch_irfft_mode<LOGM, 1>(X, x, tw, rows, in_len, ro);
+  else
+    launch_irfft_mode<LOGM, 2>(X, x, tw, rows, in_len, ro);
 }
 
 template <int L = 0>
@@ -754,15 +808,23 @@ void dispatch_rfft(int logm, const float* x, float2* X, const float2* tw, int64_
 
 template <int L = 0>
 void dispatch_irfft(int logm, const float2* X, float* x, const float2* tw, int64_t rows,
-                    int64_t in_len) {
+                    int64_t in_len, const RowOut& ro) {
   if constexpr (L <= kMaxLogM) {
-    if (logm == L) return launch_irfft<L>(X, x, tw, rows, in_len);
-    dispatch_irfft<L + 1>(logm, X, x, tw, rows, in_len);
+    if (logm == L) return launch_irfft<L>(X, x, tw, rows, in_len, ro);
+    dispatch_irfft<L + 1>(logm, X, x, tw, rows, in_len, ro);
   }
 }
 
 // ---- complex elementwise --------------------------------------------------
 // op 0: out = a * b, op 1: out = a + b; conj flags conjugate an operand.
+__device__ __forceinline__ float2 complex_op(float2 u, float2 w, int op, int conj_a,
+                                             int conj_b) {
+  if (conj_a) u.y = -u.y;
+  if (conj_b) w.y = -w.y;
+  return op == 0 ? cmul(u, w) : make_float2(u.x + w.x, u.y + w.y);
+}
+
+template <bool WIDE>
 __global__ __launch_bounds__(256) void complex_binary_kernel(float2* __restrict__ out,
                                                              const float2* __restrict__ a,
                                                              const float2* __restrict__ b,
@@ -771,11 +833,29 @@ __global__ __launch_bounds__(256) void complex_binary_kernel(float2* __restrict_
   const int64_t step = (int64_t)gridDim.x * 256;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += step) {
     int64_t off[3];
-    wxx::offsets64<3>(nd, i, off);
-    float2 u = a[off[1]], w = b[off[2]];
-    if (conj_a) u.y = -u.y;
-    if (conj_b) w.y = -w.y;
-    out[off[0]] = op == 0 ? cmul(u, w) : make_float2(u.x + w.x, u.y + w.y);
+    if (WIDE)
+      wxx::offsets64<3>(nd, i, off);
+    else
+      wxx::offsets<3>(nd, i, off);
+    out[off[0]] = complex_op(a[off[1]], b[off[2]], op, conj_a, conj_b);
+  }
+}
+
+// Rank <= 2 after collapsing (rows x columns, e.g. a (B, D, F) spectrum times
+// a (D, F) filter): rows on grid y, columns on grid x, no index division.
+__global__ __launch_bounds__(256) void complex_binary_rows_kernel(
+    float2* __restrict__ out, const float2* __restrict__ a, const float2* __restrict__ b,
+    wxx::ND nd, int64_t rows, int64_t cols, int op, int conj_a, int conj_b) {
+  const int r0 = nd.rank == 2 ? 0 : -1;  // stride slot of the row dimension
+  const int c0 = nd.rank - 1;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    const int64_t ro = r0 < 0 ? 0 : r * nd.stride[0][r0];
+    const int64_t ra = r0 < 0 ? 0 : r * nd.stride[1][r0];
+    const int64_t rb = r0 < 0 ? 0 : r * nd.stride[2][r0];
+    for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < cols;
+         c += (int64_t)gridDim.x * 256)
+      out[ro + c * nd.stride[0][c0]] = complex_op(a[ra + c * nd.stride[1][c0]],
+                                                  b[rb + c * nd.stride[2][c0]], op, conj_a, conj_b);
   }
 }
 
@@ -832,22 +912,40 @@ WXX_API int wxx_rfft(const float* x, void* X, int64_t rows, int64_t in_len, int6
 }
 
 // Replaces functional.irfft (fft.py:566-645): rows x in_len c64 one-sided
-// spectrum -> rows x n f32, n a power of two >= 2.
-WXX_API int wxx_irfft(const void* X, float* x, int64_t rows, int64_t in_len, int64_t n) {
+// spectrum -> rows x out_len f32, the first out_len of the n samples of each
+// row (n a power of two >= 2), each multiplied by post_scale after the 1/n
+// normalisation.  out_len < n fuses the crop irfft(...)[..., :L] of the Hyena
+// long convolution (nn/hyena.py:208-216); post_scale fuses the factor n of the
+// rfft backward (autograd/utils.py:549-718).
+WXX_API int wxx_irfft_crop(const void* X, float* x, int64_t rows, int64_t in_len, int64_t n,
+                           int64_t out_len, float post_scale) {
   WXX_CHECK_INIT();
   WXX_REQUIRE(x && X, "null pointer");
   WXX_REQUIRE(rows >= 0 && in_len >= 0, "bad irfft dims");
   const int logn = log2_exact(n);
   WXX_REQUIRE(logn >= 1, "irfft length must be a power of two >= 2, got %lld", (long long)n);
+  WXX_REQUIRE(out_len >= 1 && out_len <= n, "irfft output length %lld not in [1, %lld]",
+              (long long)out_len, (long long)n);
   if (rows == 0) return WXX_OK;
   if (logn - 1 > kMaxLogM)
     return wxx::set_error(WXX_E_UNSUPPORTED, "irfft length %lld above %d", (long long)n,
                           2 << kMaxLogM);
   const float2* tw = twiddles(logn - 1);
   if (!tw) return wxx::set_error(WXX_E_OOM, "irfft twiddle table allocation failed");
-  dispatch_irfft(logn - 1, static_cast<const float2*>(X), x, tw, rows, in_len);
+  RowOut ro{};
+  ro.lim = out_len;
+  ro.lim32 = (int)out_len;
+  ro.half = (int)(out_len / 2);
+  ro.post = post_scale;
+  ro.mode = out_len == n ? 0 : (out_len % 2 == 0 ? 1 : 2);
+  dispatch_irfft(logn - 1, static_cast<const float2*>(X), x, tw, rows, in_len, ro);
   WXX_LAUNCHED();
   return WXX_OK;
+}
+
+// functional.irfft without a crop: rows x n.
+WXX_API int wxx_irfft(const void* X, float* x, int64_t rows, int64_t in_len, int64_t n) {
+  return wxx_irfft_crop(X, x, rows, in_len, n, n, 1.0f);
 }
 
 // Replaces functional.complex_mul (fft.py:168-213, op 0, conj flags) and
@@ -865,9 +963,24 @@ WXX_API int wxx_complex_binary(void* out, const void* a, const void* b, int rank
   if (n == 0) return WXX_OK;
   const int64_t* ss[3] = {s_out, s_a, s_b};
   const wxx::ND nd = wxx::collapse(rank, shape, ss, 3);
-  hipLaunchKernelGGL(complex_binary_kernel, dim3(wxx::grid_1d(n, 256, 16384)), dim3(256), 0,
-                     wxx::stream(), static_cast<float2*>(out), static_cast<const float2*>(a),
-                     static_cast<const float2*>(b), nd, n, op, conj_a ? 1 : 0, conj_b ? 1 : 0);
+  float2* o = static_cast<float2*>(out);
+  const float2* pa = static_cast<const float2*>(a);
+  const float2* pb = static_cast<const float2*>(b);
+  const int ca = conj_a ? 1 : 0, cb = conj_b ? 1 : 0;
+  if (nd.rank <= 2) {
+    const int64_t cols = nd.shape[nd.rank - 1], rows = n / cols;
+    const int64_t gy = std::min<int64_t>(rows, 65535);
+    const int64_t gx = std::min<int64_t>((cols + 255) / 256, std::max<int64_t>(64, 16384 / gy));
+    const dim3 grid((unsigned)gx, (unsigned)gy);
+    hipLaunchKernelGGL(complex_binary_rows_kernel, grid, dim3(256), 0, wxx::stream(), o, pa, pb,
+                       nd, rows, cols, op, ca, cb);
+  } else if (n < (int64_t(1) << 31)) {
+    hipLaunchKernelGGL(complex_binary_kernel<false>, dim3(wxx::grid_1d(n, 256, 16384)), dim3(256),
+                       0, wxx::stream(), o, pa, pb, nd, n, op, ca, cb);
+  } else {
+    hipLaunchKernelGGL(complex_binary_kernel<true>, dim3(wxx::grid_1d(n, 256, 16384)), dim3(256),
+                       0, wxx::stream(), o, pa, pb, nd, n, op, ca, cb);
+  }
   WXX_LAUNCHED();
   return WXX_OK;
 }

@@ -278,6 +278,35 @@ __global__ __launch_bounds__(kBlock) void norm_dg_finalize_kernel(const float* _
   }
 }
 
+// Middle level for many splits: workgroup (f, gi) adds splits
+// [gi * chunk, (gi + 1) * chunk) of 64 features in the finalize kernel's
+// order and writes one partial in the same layout, so the finalize kernel
+// then adds ceil(splits / chunk) partials instead of every split.
+template <int MODE>
+__global__ __launch_bounds__(kBlock) void norm_dg_combine_kernel(const float* __restrict__ part,
+                                                                 float* __restrict__ out,
+                                                                 int64_t R, int splits, int chunk) {
+  __shared__ float sg[4][64], sb[4][64];
+  const int c = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t r = (int64_t)blockIdx.x * 64 + c;
+  const int s0 = blockIdx.y * chunk, s1 = min(splits, s0 + chunk);
+  float dg = 0.f, db = 0.f;
+  if (r < R) {
+    for (int s = s0 + w; s < s1; s += 4) {
+      dg += part[((int64_t)s * 2 + 0) * R + r];
+      if (MODE == 0) db += part[((int64_t)s * 2 + 1) * R + r];
+    }
+  }
+  sg[w][c] = dg;
+  sb[w][c] = db;
+  __syncthreads();
+  if (w == 0 && r < R) {
+    out[((int64_t)blockIdx.y * 2 + 0) * R + r] = ((sg[0][c] + sg[1][c]) + sg[2][c]) + sg[3][c];
+    if (MODE == 0)
+      out[((int64_t)blockIdx.y * 2 + 1) * R + r] = ((sb[0][c] + sb[1][c]) + sb[2][c]) + sb[3][c];
+  }
+}
+
 template <int MODE>
 int launch_fwd(const float* x, const float* g, const float* b, float* y, float* mean,
                float* inv, int64_t outer, int64_t R, int64_t inner, float eps,
@@ -342,10 +371,27 @@ int launch_dg(const float* dy, const float* x, const float* mean, const float* i
   hipLaunchKernelGGL(norm_dg_partial_kernel<MODE>, dim3((unsigned)colblocks, (unsigned)splits),
                      dim3(kBlock), 0, s, dy, x, mean, inv, part, outer, R, inner, seg);
   WXX_LAUNCHED();
+  const float* fin = part;
+  int64_t nfin = splits;
+  float* part2 = nullptr;
+  constexpr int64_t kChunk = 32;
+  if (splits > 2 * kChunk) {
+    nfin = (splits + kChunk - 1) / kChunk;
+    part2 = (float*)wxx::scratch_alloc(sizeof(float) * 2 * R * nfin);
+    if (!part2) {
+      wxx::scratch_free(part);
+      return wxx::set_error(WXX_E_OOM, "norm dg partials");
+    }
+    hipLaunchKernelGGL(norm_dg_combine_kernel<MODE>, dim3((unsigned)((R + 63) / 64), (unsigned)nfin),
+                       dim3(kBlock), 0, s, (const float*)part, part2, R, (int)splits, (int)kChunk);
+    WXX_LAUNCHED();
+    fin = part2;
+  }
   hipLaunchKernelGGL(norm_dg_finalize_kernel<MODE>, dim3((unsigned)((R + 63) / 64)), dim3(kBlock),
-                     0, s, part, dgamma, dbeta, R, (int)splits);
+                     0, s, fin, dgamma, dbeta, R, (int)nfin);
   WXX_LAUNCHED();
   wxx::scratch_free(part);
+  if (part2) wxx::scratch_free(part2);
   return WXX_OK;
 }
 

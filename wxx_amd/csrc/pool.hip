@@ -24,9 +24,12 @@
 //
 // MI355X design: the pools are one thread per output (or per input cell for
 // the backward, a gather with no atomics, so results are deterministic),
-// 32-bit index math.  The causal conv's weight / bias gradients are reduced
-// per channel by whole workgroups (the reference gives each (d, k) one
-// thread that walks B*L elements serially).
+// 32-bit index math.  The causal conv works on 64-channel x 64-position
+// tiles staged through LDS, so a transposed input view is read coalesced and
+// the output written coalesced; its weight / bias gradients take all KS + 1
+// sums in one pass over dy and x per tile, then add the per-workgroup
+// partials in a fixed order (the reference gives each (d, k) one thread that
+// walks B*L elements serially).
 #include "common.h"
 
 namespace {
@@ -240,6 +243,177 @@ __global__ __launch_bounds__(kBlock) void causal_conv1d_dw_kernel(const float* _
   }
 }
 
+// ---- tiled causal conv: 64 channels x 64 positions of one batch row per
+// workgroup, the x window (64 + KS - 1 positions) staged in LDS with loads
+// that run along whichever of the view's channel / position axes is unit
+// stride (Hyena passes transposed (B, L, D) projections, channel-contiguous).
+constexpr int kCT = 64;        // channels and positions per tile
+constexpr int kCMaxKS = 8;     // kernel sizes handled by the tiled kernels
+constexpr int kCW = kCT + kCMaxKS + 1;  // LDS row pitch, odd: a column read is conflict-free
+
+// Stages x[b, d0 + dd, n0 - (KS - 1) + nn] (zero outside the tensor and for
+// n < 0) into xs[dd][nn], dd < 64, nn < 64 + KS - 1.  The window is walked as
+// a fixed 64 x kCX grid (columns >= 64 + KS - 1 skipped) so the loop has a
+// constant trip count: every load is issued before the first LDS store.
+constexpr int kCX = kCT + kCMaxKS;                        // window columns walked
+constexpr int kStage = (kCT * kCX + kBlock - 1) / kBlock;  // loads per thread
+
+__device__ __forceinline__ void conv_stage_x(float (*xs)[kCW], const float* __restrict__ x,
+                                             const View3& v, int64_t b, int d0, int n0, int D,
+                                             int L, int KS) {
+  const int W = kCT + KS - 1;
+  const float* xb = x + v.off + b * v.sb;
+  const bool chan_fast = v.sc == 1 && v.sl != 1;  // lanes along channels when those are unit stride
+  float r[kStage];
+#pragma unroll
+  for (int it = 0; it < kStage; ++it) {
+    const int i = threadIdx.x + it * kBlock;
+    const int dd = chan_fast ? i % kCT : i / kCX, nn = chan_fast ? i / kCT : i % kCX;
+    const int d = d0 + dd, n = n0 - (KS - 1) + nn;
+    r[it] = (i < kCT * kCX && nn < W && d < D && n >= 0 && n < L)
+                ? xb[(int64_t)d * v.sc + (int64_t)n * v.sl]
+                : 0.f;
+  }
+#pragma unroll
+  for (int it = 0; it < kStage; ++it) {
+    const int i = threadIdx.x + it * kBlock;
+    const int dd = chan_fast ? i % kCT : i / kCX, nn = chan_fast ? i / kCT : i % kCX;
+    if (i < kCT * kCX && nn < W) xs[dd][nn] = r[it];
+  }
+}
+
+// y[b, d, n] for one (b, 64-channel, 64-position) tile; grid (L tiles, D tiles, B).
+__global__ __launch_bounds__(kBlock) void causal_conv1d_tiled_kernel(
+    const float* __restrict__ x, View3 v, const float* __restrict__ w,
+    const float* __restrict__ bias, float* __restrict__ y, int D, int L, int KS) {
+  __shared__ float xs[kCT][kCW];
+  const int n0 = blockIdx.x * kCT, d0 = blockIdx.y * kCT;
+  const int64_t b = blockIdx.z;
+  conv_stage_x(xs, x, v, b, d0, n0, D, L, KS);
+  __syncthreads();
+  const int nn = threadIdx.x % kCT;
+  const int n = n0 + nn;
+  if (n >= L) return;
+#pragma unroll 4
+  for (int dd = threadIdx.x / kCT; dd < kCT; dd += kBlock / kCT) {
+    const int d = d0 + dd;
+    if (d >= D) break;
+    float acc = bias[d];
+    for (int k = 0; k < KS; ++k)  // same order and terms as the untiled kernel
+      if (n >= k) acc = fmaf(w[d * KS + k], xs[dd][nn + KS - 1 - k], acc);
+    y[(b * D + d) * (int64_t)L + n] = acc;
+  }
+}
+
+// dx[b, d, n] = sum_k w[d, k] dy[b, d, n + k]: one row chunk of 4 * 256
+// positions per workgroup, grid (chunks, rows).
+__global__ __launch_bounds__(kBlock) void causal_conv1d_dx_rows_kernel(
+    const float* __restrict__ dy, const float* __restrict__ w, float* __restrict__ dx, int D,
+    int L, int KS, int64_t rows) {
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    const int d = (int)(r % D);
+    const float* g = dy + r * L;
+    float* o = dx + r * L;
+    for (int i = 0; i < 4; ++i) {
+      const int n = (blockIdx.x * 4 + i) * kBlock + threadIdx.x;
+      if (n >= L) break;
+      float acc = 0.f;
+      if (KS <= kCMaxKS) {
+#pragma unroll
+        for (int k = 0; k < kCMaxKS; ++k)  // unrolled: the tap loads issue together
+          if (k < KS && n + k < L) acc = fmaf(w[d * KS + k], g[n + k], acc);
+      } else {
+        for (int k = 0; k < KS; ++k)
+          if (n + k < L) acc = fmaf(w[d * KS + k], g[n + k], acc);
+      }
+      o[n] = acc;
+    }
+  }
+}
+
+// Weight / bias gradient partials: workgroup (s, t) sums the (b, position)
+// tiles s, s + S, s + 2S, ... of channel tile t in one pass over dy and x,
+// all KS + 1 sums at once (k == KS: the bias).  Lane = channel, the four
+// waves take 16 positions each; the waves' sums are added in wave order.
+// part[s][d][k], reduced over s in order by causal_conv1d_dw_finalize_kernel.
+__global__ __launch_bounds__(kBlock) void causal_conv1d_dw_tiled_kernel(
+    const float* __restrict__ dy, const float* __restrict__ x, View3 v,
+    float* __restrict__ part, int B, int D, int L, int KS) {
+  __shared__ float xs[kCT][kCW];
+  __shared__ float gs[kCT][kCT + 1];
+  __shared__ float red[kBlock / kCT][kCT][kCMaxKS + 1];
+  const int d0 = blockIdx.y * kCT;
+  const int ntl = (L + kCT - 1) / kCT;
+  const int64_t tiles = (int64_t)B * ntl;
+  const int dd = threadIdx.x % kCT, wv = threadIdx.x / kCT;
+  float acc[kCMaxKS + 1];
+#pragma unroll
+  for (int k = 0; k <= kCMaxKS; ++k) acc[k] = 0.f;
+  for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    const int64_t b = tile / ntl;
+    const int n0 = (int)(tile % ntl) * kCT;
+    __syncthreads();  // previous tile's LDS reads are done
+    float rg[kCT * kCT / kBlock];
+#pragma unroll
+    for (int it = 0; it < kCT * kCT / kBlock; ++it) {
+      const int i = threadIdx.x + it * kBlock;
+      const int nn = i % kCT, c = i / kCT;
+      const int d = d0 + c, n = n0 + nn;
+      rg[it] = (d < D && n < L) ? dy[(b * D + d) * (int64_t)L + n] : 0.f;
+    }
+    conv_stage_x(xs, x, v, b, d0, n0, D, L, KS);
+#pragma unroll
+    for (int it = 0; it < kCT * kCT / kBlock; ++it) {
+      const int i = threadIdx.x + it * kBlock;
+      gs[i / kCT][i % kCT] = rg[it];
+    }
+    __syncthreads();
+    for (int j = 0; j < kCT / 4; ++j) {
+      const int nn = wv * (kCT / 4) + j;
+      const float g = gs[dd][nn];
+      const int n = n0 + nn;
+#pragma unroll
+      for (int k = 0; k < kCMaxKS; ++k)
+        if (k < KS && n >= k) acc[k] = fmaf(g, xs[dd][nn + KS - 1 - k], acc[k]);
+      acc[kCMaxKS] += g;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k <= kCMaxKS; ++k) red[wv][dd][k] = acc[k];
+  __syncthreads();
+  for (int i = threadIdx.x; i < kCT * (KS + 1); i += kBlock) {
+    const int c = i / (KS + 1), k = i % (KS + 1);
+    const int kk = k == KS ? kCMaxKS : k;
+    if (d0 + c < D) {
+      float t = red[0][c][kk];
+      for (int q = 1; q < kBlock / kCT; ++q) t += red[q][c][kk];
+      part[((int64_t)blockIdx.x * D + d0 + c) * (KS + 1) + k] = t;
+    }
+  }
+}
+
+// dw[d, k] (k < KS) and db[d] (k == KS): one wave per output; lane l adds
+// splits l, l + 64, ... and the lanes are combined by a fixed butterfly, so
+// the order is the same on every run.
+__global__ __launch_bounds__(kBlock) void causal_conv1d_dw_finalize_kernel(
+    const float* __restrict__ part, float* __restrict__ dw, float* __restrict__ db, int D,
+    int KS, int splits) {
+  const int i = blockIdx.x * (kBlock / 64) + threadIdx.x / 64;
+  const int lane = threadIdx.x & 63;
+  if (i >= D * (KS + 1)) return;
+  float t = 0.f;
+  for (int s = lane; s < splits; s += 64) t += part[(int64_t)s * D * (KS + 1) + i];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off, 64);
+  if (lane == 0) {
+    const int d = i / (KS + 1), k = i % (KS + 1);
+    if (k == KS)
+      db[d] = t;
+    else
+      dw[d * KS + k] = t;
+  }
+}
+
 int pool_setup(PoolArgs& a, int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH, int64_t KW,
                int64_t sh, int64_t sw, int64_t ph, int64_t pw) {
   WXX_REQUIRE(B >= 0 && C >= 0 && H >= 1 && W >= 1 && KH >= 1 && KW >= 1 && sh >= 1 && sw >= 1 &&
@@ -354,8 +528,15 @@ WXX_API int wxx_causal_conv1d(const float* x, int64_t x_off, int64_t sb, int64_t
   const int64_t total = B * D * L;
   if (total == 0) return WXX_OK;
   View3 v{x_off, sb, sc, sl};
-  hipLaunchKernelGGL(causal_conv1d_kernel, dim3(wxx::grid_1d(total, kBlock, 65536)), dim3(kBlock),
-                     0, wxx::stream(), x, v, w, bias, y, (int)D, (int)L, (int)KS, total);
+  if (KS <= kCMaxKS && B <= 65535 && D <= 65535 * kCT) {
+    const dim3 grid((unsigned)((L + kCT - 1) / kCT), (unsigned)((D + kCT - 1) / kCT), (unsigned)B);
+    hipLaunchKernelGGL(causal_conv1d_tiled_kernel, grid, dim3(kBlock), 0, wxx::stream(), x, v, w,
+                       bias, y, (int)D, (int)L, (int)KS);
+  } else {
+    hipLaunchKernelGGL(causal_conv1d_kernel, dim3(wxx::grid_1d(total, kBlock, 65536)),
+                       dim3(kBlock), 0, wxx::stream(), x, v, w, bias, y, (int)D, (int)L, (int)KS,
+                       total);
+  }
   WXX_LAUNCHED();
   return WXX_OK;
 }
@@ -375,13 +556,35 @@ WXX_API int wxx_causal_conv1d_backward(const float* dy, const float* x, int64_t 
               "causal_conv1d_backward: bad shape");
   const int64_t total = B * D * L;
   hipStream_t s = wxx::stream();
-  if (total > 0)
-    hipLaunchKernelGGL(causal_conv1d_dx_kernel, dim3(wxx::grid_1d(total, kBlock, 65536)),
-                       dim3(kBlock), 0, s, dy, w, dx, (int)D, (int)L, (int)KS, total);
+  if (total > 0) {
+    const int64_t rows = B * D;
+    const dim3 grid((unsigned)((L + 4 * kBlock - 1) / (4 * kBlock)),
+                    (unsigned)std::min<int64_t>(rows, 65535));
+    hipLaunchKernelGGL(causal_conv1d_dx_rows_kernel, grid, dim3(kBlock), 0, s, dy, w, dx, (int)D,
+                       (int)L, (int)KS, rows);
+  }
   if (dw) {
     View3 v{x_off, sb, sc, sl};
-    hipLaunchKernelGGL(causal_conv1d_dw_kernel, dim3((unsigned)(D * (KS + 1))), dim3(kBlock), 0,
-                       s, dy, x, v, dw, db, (int)B, (int)D, (int)L, (int)KS);
+    const int64_t dtiles = (D + kCT - 1) / kCT;
+    const int64_t tiles = B * ((L + kCT - 1) / kCT);
+    if (KS <= kCMaxKS && tiles > 0 && dtiles <= 65535) {
+      // about four workgroups per CU, at least 4 (b, position) tiles each
+      const int64_t cus = wxx::num_cus() > 0 ? wxx::num_cus() : 256;
+      int64_t splits = std::max<int64_t>(1, (4 * cus + dtiles - 1) / dtiles);
+      splits = std::min<int64_t>(splits, std::max<int64_t>(1, tiles / 4));
+      float* part = (float*)wxx::scratch_alloc(sizeof(float) * (size_t)(splits * D * (KS + 1)));
+      if (!part) return wxx::set_error(WXX_E_OOM, "causal_conv1d dw partials");
+      hipLaunchKernelGGL(causal_conv1d_dw_tiled_kernel, dim3((unsigned)splits, (unsigned)dtiles),
+                         dim3(kBlock), 0, s, dy, x, v, part, (int)B, (int)D, (int)L, (int)KS);
+      hipLaunchKernelGGL(causal_conv1d_dw_finalize_kernel,
+                         dim3((unsigned)((D * (KS + 1) + kBlock / 64 - 1) / (kBlock / 64))),
+                         dim3(kBlock), 0,
+                         s, (const float*)part, dw, db, (int)D, (int)KS, (int)splits);
+      wxx::scratch_free(part);
+    } else {
+      hipLaunchKernelGGL(causal_conv1d_dw_kernel, dim3((unsigned)(D * (KS + 1))), dim3(kBlock), 0,
+                         s, dy, x, v, dw, db, (int)B, (int)D, (int)L, (int)KS);
+    }
   }
   WXX_LAUNCHED();
   return WXX_OK;

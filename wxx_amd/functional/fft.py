@@ -7,6 +7,8 @@ transform of a row stays in LDS) instead of the reference's
 ``log2(n) + 2`` launches for n > 1024.
 """
 
+import ctypes as C
+
 import numpy as np
 
 from .. import validation
@@ -179,11 +181,15 @@ def rfft(tensor1, n=None):
     return out, n
 
 
-def irfft(tensor1, n=None):
+def irfft(tensor1, n=None, length=None, scale=1.0):
     """Inverse real FFT along the last dimension (reference fft.py:566-645).
 
     ``tensor1`` is a one-sided spectrum; bins at or beyond ``n // 2 + 1`` are
     ignored, missing bins count as zero.  Default ``n = 2 * (in_len - 1)``.
+    ``length`` (default ``n``) keeps only the first ``length`` samples of each
+    row, the same values as ``irfft(tensor1, n)[..., :length]`` without the
+    intermediate; ``scale`` multiplies the result (after the 1/n
+    normalisation, as a separate multiply would).
     """
     if tensor1.type != "c64":
         raise TypeError("irfft expects a complex64 tensor")
@@ -196,9 +202,16 @@ def irfft(tensor1, n=None):
     _check_pow2(n)
     if n < 2:
         raise ValueError("irfft length must be at least 2")
+    length = n if length is None else int(length)
+    if not 1 <= length <= n:
+        raise ValueError(f"irfft length must be in [1, {n}], got {length}")
     rows = validation.numel(shape[:-1])
-    out = empty(shape[:-1] + [n], requires_grad=tensor1.requires_grad)
-    call("wxx_irfft", ptr(tensor1), ptr(out), rows, in_len, n)
+    out = empty(shape[:-1] + [length], requires_grad=tensor1.requires_grad)
+    if length == n and scale == 1.0:
+        call("wxx_irfft", ptr(tensor1), ptr(out), rows, in_len, n)
+    else:
+        call("wxx_irfft_crop", ptr(tensor1), ptr(out), rows, in_len, n, length,
+             C.c_float(scale))
     return out
 
 

@@ -92,8 +92,8 @@ class HyenaOperator(Module):
         """Linear convolution of (B, D, L) with (D, L) through the FFT."""
         length = x.shape[-1]
         n = self._fft_size(length)
-        out = x.rfft(n).complex_mul(h.rfft(n)).irfft(n)
-        return out[..., :length] if n != length else out
+        # irfft(...)[..., :length] as one cropping inverse transform
+        return x.rfft(n).complex_mul(h.rfft(n)).irfft(n, min(length, n))
 
     def _decay_window(self, stage, length):
         return autograd.decay_window(self.decay).forward(self.decay, stage, length)
