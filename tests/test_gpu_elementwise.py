@@ -96,11 +96,26 @@ def test_clamp_equal_masked_fill(device):
     assert np.array_equal(F().equal_number(u, 2).numpy(), (np.arange(10) % 3 == 2).astype(np.float32))
 
 
-def test_mul_backward(device):
-    g, a, b = (rng(i).standard_normal((7, 9)).astype(np.float32) for i in (11, 12, 13))
+@pytest.mark.parametrize("shape", [(7, 9), (8, 256, 64)])  # scalar and float4 paths
+def test_mul_backward(device, shape):
+    g, a, b = (rng(i).standard_normal(shape).astype(np.float32) for i in (11, 12, 13))
     da, db = F().mul_backward(up(g), up(a), up(b))
     ea, eb = oe.mul_backward(g, a, b)
     assert np.array_equal(da.numpy(), ea) and np.array_equal(db.numpy(), eb)
+
+
+@pytest.mark.parametrize("B,L,D,parts", [(2, 70, 33, 3), (3, 128, 64, 4)])
+def test_assign_transposed_source_into_slice(device, B, L, D, parts):
+    # a (B, D, L) tensor viewed as (B, L, D) written into a channel slice of a
+    # (B, L, parts * D) buffer: the LDS-tiled transpose with a strided destination
+    g = rng(18).standard_normal((B, D, L)).astype(np.float32)
+    buf = rng(19).standard_normal((B, L, parts * D)).astype(np.float32)
+    t = up(buf)
+    src = F().permute(up(g), 0, 2, 1)
+    F().assign(t.narrow(2, D, D), src)
+    want = buf.copy()
+    want[:, :, D:2 * D] = g.transpose(0, 2, 1)
+    assert np.array_equal(t.numpy(), want)
 
 
 @pytest.mark.parametrize("shape,perm", [((4, 6, 8), (0, 2, 1)), ((8, 1024, 12, 64), (0, 2, 1, 3)),

@@ -365,7 +365,7 @@ class rfft(Function):
             return None
         w = functional.complex_weights(_rfft_backward_weights(self.N))
         # irfft(g w, N) * N cropped to the input length, in one kernel (the
-        # crop and the factor N give the same values as separate passes)
+        # crop and the factor N are the same arithmetic as separate passes)
         ga = functional.irfft(functional.complex_mul(g, w), self.N,
                               length=min(self.in_len, self.N), scale=float(self.N))
         return _match_last_dim_real(ga, self.in_len)

@@ -268,6 +268,21 @@ __global__ __launch_bounds__(kBlock) void mul_backward_kernel(const float* __res
   }
 }
 
+__global__ __launch_bounds__(kBlock) void mul_backward4_kernel(const float4* __restrict__ g,
+                                                               const float4* __restrict__ a,
+                                                               const float4* __restrict__ b,
+                                                               float4* __restrict__ da,
+                                                               float4* __restrict__ db,
+                                                               int64_t n4) {
+  int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t step = (int64_t)gridDim.x * kBlock;
+  for (; i < n4; i += step) {
+    const float4 gv = g[i], av = a[i], bv = b[i];
+    da[i] = make_float4(gv.x * bv.x, gv.y * bv.y, gv.z * bv.z, gv.w * bv.w);
+    db[i] = make_float4(gv.x * av.x, gv.y * av.y, gv.z * av.z, gv.w * av.w);
+  }
+}
+
 // ---- layout -------------------------------------------------------------------
 // dst (operand 0) and src (operand 1) both strided; element type T.
 template <typename T, bool BIG>
@@ -298,17 +313,18 @@ __global__ __launch_bounds__(kBlock) void fill_strided_kernel(T* __restrict__ ds
   }
 }
 
-// Tiled transpose of the two innermost collapsed dims (gather case where the
-// source's innermost stride is not 1): read 64x64 tiles coalesced, write
-// coalesced through LDS.
+// Tiled transpose of the two innermost collapsed dims (the source is unit
+// stride along rows, the destination along columns): read 64x64 tiles
+// coalesced, write coalesced through LDS.
 template <typename T>
 __global__ __launch_bounds__(kBlock) void transpose_tile_kernel(T* __restrict__ dst,
                                                                 const T* __restrict__ src,
                                                                 int64_t batch, int64_t rows,
                                                                 int64_t cols, int64_t sb,
-                                                                int64_t sr, int64_t sc) {
-  // dst[b][r][c] = src[b*sb + r*sr + c*sc], with sr == 1 expected (fast read
-  // along r).  Tile: 64 (r) x 64 (c).
+                                                                int64_t sr, int64_t sc,
+                                                                int64_t db, int64_t dr) {
+  // dst[b*db + r*dr + c] = src[b*sb + r*sr + c*sc], with sr == 1 expected
+  // (fast read along r).  Tile: 64 (r) x 64 (c).
   __shared__ T tile[64][65];
   const int64_t b = blockIdx.z;
   const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
@@ -320,7 +336,7 @@ __global__ __launch_bounds__(kBlock) void transpose_tile_kernel(T* __restrict__ 
   __syncthreads();
   for (int k = ty; k < 64; k += 4) {
     const int64_t r = r0 + k, c = c0 + tx;
-    if (r < rows && c < cols) dst[(b * rows + r) * cols + c] = tile[tx][k];
+    if (r < rows && c < cols) dst[b * db + r * dr + c] = tile[tx][k];
   }
 }
 
@@ -549,8 +565,14 @@ WXX_API int wxx_mul_backward(const float* g, const float* a, const float* b, flo
   WXX_CHECK_INIT();
   WXX_REQUIRE(g && a && b && da && db, "null pointer");
   if (n <= 0) return WXX_OK;
-  hipLaunchKernelGGL(mul_backward_kernel, dim3(grid_for(n)), dim3(kBlock), 0, wxx::stream(), g,
-                     a, b, da, db, n);
+  if (n % 4 == 0 && ((uintptr_t)g | (uintptr_t)a | (uintptr_t)b | (uintptr_t)da | (uintptr_t)db) %
+                            16 == 0)
+    hipLaunchKernelGGL(mul_backward4_kernel, dim3(grid_for(n / 4)), dim3(kBlock), 0,
+                       wxx::stream(), (const float4*)g, (const float4*)a, (const float4*)b,
+                       (float4*)da, (float4*)db, n / 4);
+  else
+    hipLaunchKernelGGL(mul_backward_kernel, dim3(grid_for(n)), dim3(kBlock), 0, wxx::stream(), g,
+                       a, b, da, db, n);
   WXX_LAUNCHED();
   return WXX_OK;
 }
@@ -571,25 +593,25 @@ WXX_API int wxx_copy_strided(void* dst, const void* src, int itemsize, int rank,
   const int64_t* ss[2] = {s_dst, s_src};
   ND nd = collapse(rank, shape, ss, 2);
   hipStream_t s = wxx::stream();
-  // Transpose-shaped gather: destination dense, source innermost stride != 1
-  // but unit stride on the next dim -> LDS-tiled transpose.
+  // Transpose-shaped copy: destination unit stride along the innermost dim,
+  // source unit stride along the next one -> LDS-tiled transpose (the
+  // destination may be a strided view, e.g. a slice being assigned).
   if (nd.rank >= 2 && nd.rank <= 3 && nd.stride[0][nd.rank - 1] == 1 &&
-      nd.stride[1][nd.rank - 2] == 1 && nd.stride[1][nd.rank - 1] != 1 &&
-      nd.stride[0][nd.rank - 2] == nd.shape[nd.rank - 1] &&
-      (nd.rank == 2 || nd.stride[0][0] == nd.shape[1] * nd.shape[2])) {
+      nd.stride[1][nd.rank - 2] == 1 && nd.stride[1][nd.rank - 1] != 1) {
     const int64_t rows = nd.shape[nd.rank - 2], cols = nd.shape[nd.rank - 1];
     const int64_t batch = nd.rank == 3 ? nd.shape[0] : 1;
     const int64_t sb = nd.rank == 3 ? nd.stride[1][0] : 0;
+    const int64_t db = nd.rank == 3 ? nd.stride[0][0] : 0, dr = nd.stride[0][nd.rank - 2];
     if (batch <= 65535 && (rows + 63) / 64 <= 65535) {
       dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64), (unsigned)batch);
       if (itemsize == 4)
         hipLaunchKernelGGL(transpose_tile_kernel<uint32_t>, grid, dim3(kBlock), 0, s,
                            (uint32_t*)dst, (const uint32_t*)src, batch, rows, cols, sb,
-                           nd.stride[1][nd.rank - 2], nd.stride[1][nd.rank - 1]);
+                           nd.stride[1][nd.rank - 2], nd.stride[1][nd.rank - 1], db, dr);
       else
         hipLaunchKernelGGL(transpose_tile_kernel<uint64_t>, grid, dim3(kBlock), 0, s,
                            (uint64_t*)dst, (const uint64_t*)src, batch, rows, cols, sb,
-                           nd.stride[1][nd.rank - 2], nd.stride[1][nd.rank - 1]);
+                           nd.stride[1][nd.rank - 2], nd.stride[1][nd.rank - 1], db, dr);
       WXX_LAUNCHED();
       return WXX_OK;
     }

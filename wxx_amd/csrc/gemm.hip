@@ -23,9 +23,10 @@
 //    chunk, so a lane's A/B fragment is one conflict-free ds_read_b32;
 //  * tile ids are remapped so that consecutive tiles land on the same XCD
 //    (each of the 8 XCDs has its own L2) and walked in GROUP_M row groups;
-//  * interior tiles run a loop body with float4 global loads and no bounds
-//    checks (chosen once per workgroup, so the loop carries no branches);
-//    edge tiles and a ragged last K chunk use guarded scalar loads;
+//  * interior tiles run a loop body with no bounds checks, float4 global
+//    loads when the operands are 16-byte aligned and scalar loads otherwise
+//    (chosen once per workgroup, so the loop carries no branches); edge
+//    tiles and a ragged last K chunk use guarded scalar loads;
 //  * long K over few output tiles is split across workgroups (grid z) into
 //    partials that a second pass adds in split order, so results do not
 //    depend on timing.
@@ -110,15 +111,16 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
   // this workgroup's K range [kbeg, K): the whole K, or one split of it
   const int64_t kbeg = (int64_t)blockIdx.z * g.kps;
   const int64_t K = min(g.K, kbeg + g.kps);
-  const bool full_mn = g.vec_ok && (m0 + BM <= M) && (n0 + BN <= N);
+  const bool interior = (m0 + BM <= M) && (n0 + BN <= N);
 
   float4 ra[PA], rb[PB];
 
   // ---- global -> registers for the K chunk starting at k0 ---------------
-  // fast: the chunk lies inside M, N and K and float4 loads are aligned, so
-  // no per-element guard is needed (a compile-time choice of the caller).
-  auto load_chunk = [&](int64_t k0, auto fast_tag) {
-    constexpr bool fast = decltype(fast_tag)::value;
+  // mode (a compile-time choice of the caller): 0 = guarded scalar loads;
+  // the chunk lies inside M, N and K, so no per-element guard is needed,
+  // with 1 = float4 loads (aligned operands) or 2 = scalar loads.
+  auto load_chunk = [&](int64_t k0, auto mode_tag) {
+    constexpr int mode = decltype(mode_tag)::value;
 #pragma unroll
     for (int p = 0; p < PA; ++p) {
       const int f = p * 256 + tid;  // float4 index within the A tile
@@ -128,8 +130,10 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
         i = m0 + f / KV;
         k = k0 + (f % KV) * 4;
         const float* src = A + i * g.lda + k;
-        if (fast) {
+        if (mode == 1) {
           ra[p] = *reinterpret_cast<const float4*>(src);
+        } else if (mode == 2) {
+          ra[p] = make_float4(src[0], src[1], src[2], src[3]);
         } else {
           float v[4];
 #pragma unroll
@@ -141,8 +145,10 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
         i = m0 + (f % IV) * 4;
         k = k0 + f / IV;
         const float* src = A + k * g.lda + i;
-        if (fast) {
+        if (mode == 1) {
           ra[p] = *reinterpret_cast<const float4*>(src);
+        } else if (mode == 2) {
+          ra[p] = make_float4(src[0], src[1], src[2], src[3]);
         } else {
           float v[4];
 #pragma unroll
@@ -160,8 +166,10 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
         j = n0 + (f % JV) * 4;
         k = k0 + f / JV;
         const float* src = B + k * g.ldb + j;
-        if (fast) {
+        if (mode == 1) {
           rb[p] = *reinterpret_cast<const float4*>(src);
+        } else if (mode == 2) {
+          rb[p] = make_float4(src[0], src[1], src[2], src[3]);
         } else {
           float v[4];
 #pragma unroll
@@ -173,8 +181,10 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
         j = n0 + f / KV;
         k = k0 + (f % KV) * 4;
         const float* src = B + j * g.ldb + k;
-        if (fast) {
+        if (mode == 1) {
           rb[p] = *reinterpret_cast<const float4*>(src);
+        } else if (mode == 2) {
+          rb[p] = make_float4(src[0], src[1], src[2], src[3]);
         } else {
           float v[4];
 #pragma unroll
@@ -255,18 +265,19 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
     }
   };
 
-  // K chunks [kbeg, K) of BK.  Interior tiles (full_mn) load every chunk but
-  // a ragged last one without guards; edge tiles always use guarded loads.
-  // The branch on full_mn is taken once, so each loop body is branch-free.
+  // K chunks [kbeg, K) of BK.  Interior tiles load every chunk but a ragged
+  // last one without guards (float4 when the operands allow it, else
+  // scalar); edge tiles always use guarded loads.  The choice is made once
+  // per workgroup, so each loop body is branch-free.
   const int64_t nk = (K - kbeg + BK - 1) / BK;
-  auto main_loop = [&](auto full_tag) {
-    constexpr bool FULL = decltype(full_tag)::value;
-    const int64_t nfast = FULL ? (K - kbeg) / BK : 0;  // chunks loadable without guards
+  auto main_loop = [&](auto mode_tag) {
+    constexpr int LM = decltype(mode_tag)::value;  // load mode of the full chunks
+    const int64_t nfast = LM != 0 ? (K - kbeg) / BK : 0;  // chunks loadable without guards
     auto load = [&](int64_t kc) {
-      if (FULL && kc < nfast)
-        load_chunk(kbeg + kc * BK, std::true_type{});
+      if (LM != 0 && kc < nfast)
+        load_chunk(kbeg + kc * BK, std::integral_constant<int, LM>{});
       else
-        load_chunk(kbeg + kc * BK, std::false_type{});
+        load_chunk(kbeg + kc * BK, std::integral_constant<int, 0>{});
     };
     load(0);
     store_chunk(0);
@@ -282,10 +293,12 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
       __syncthreads();
     }
   };
-  if (full_mn)
-    main_loop(std::true_type{});
+  if (interior && g.vec_ok)
+    main_loop(std::integral_constant<int, 1>{});
+  else if (interior)
+    main_loop(std::integral_constant<int, 2>{});
   else
-    main_loop(std::false_type{});
+    main_loop(std::integral_constant<int, 0>{});
 
   // ---- epilogue: D[i][j] of a 32x32 tile sits in lane j + 32*((i/4)%2),
   //      register (i%4) + 4*(i/8) --------------------------------------------

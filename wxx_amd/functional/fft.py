@@ -187,9 +187,9 @@ def irfft(tensor1, n=None, length=None, scale=1.0):
     ``tensor1`` is a one-sided spectrum; bins at or beyond ``n // 2 + 1`` are
     ignored, missing bins count as zero.  Default ``n = 2 * (in_len - 1)``.
     ``length`` (default ``n``) keeps only the first ``length`` samples of each
-    row, the same values as ``irfft(tensor1, n)[..., :length]`` without the
-    intermediate; ``scale`` multiplies the result (after the 1/n
-    normalisation, as a separate multiply would).
+    row, ``irfft(tensor1, n)[..., :length]`` computed by the same arithmetic
+    without the full-length intermediate; ``scale`` multiplies the result
+    after the 1/n normalisation, as a separate multiply would.
     """
     if tensor1.type != "c64":
         raise TypeError("irfft expects a complex64 tensor")
