@@ -149,13 +149,12 @@ __device__ __forceinline__ void pass_math(float2* v, int t, const float2* __rest
   }
 }
 
-// Destination of an inverse transform's real output row: samples [0, lim) of
-// the row starting at p, each scaled by scale and then by post (two roundings,
+// Output of an inverse transform's real row (the row pointer is passed
+// alongside): samples [0, lim) of the row, each scaled by scale and then by post (two roundings,
 // the same values a separate scaling pass would give).  mode 0: the whole row
 // (lim = 2M, float2 stores); 1: an even lim (float2 stores below lim); 2: an
 // odd lim (scalar stores below lim).
 struct RowOut {
-  float* p;
   int64_t lim;
   float scale, post;
   int mode;
@@ -165,16 +164,17 @@ struct RowOut {
 // Stores the real pair z (samples 2j, 2j + 1) of row o; CROP is o.mode,
 // fixed at compile time so the uncropped kernel keeps plain float2 stores.
 template <int CROP>
-__device__ __forceinline__ void row_store(const RowOut& o, int j, float2 z) {
+__device__ __forceinline__ void row_store(const RowOut& o, float* __restrict__ p, int j,
+                                          float2 z) {
   z = make_float2((z.x * o.scale) * o.post, (z.y * o.scale) * o.post);
   if (CROP == 0) {
-    reinterpret_cast<float2*>(o.p)[j] = z;
+    reinterpret_cast<float2*>(p)[j] = z;
   } else if (CROP == 1) {
-    if (j < o.half) reinterpret_cast<float2*>(o.p)[j] = z;  // half = lim / 2
+    if (j < o.half) reinterpret_cast<float2*>(p)[j] = z;  // half = lim / 2
   } else {
     const int i = 2 * j;
-    if (i < o.lim32) o.p[i] = z.x;
-    if (i + 1 < o.lim32) o.p[i + 1] = z.y;
+    if (i < o.lim32) p[i] = z.x;
+    if (i + 1 < o.lim32) p[i + 1] = z.y;
   }
 }
 
@@ -183,7 +183,8 @@ __device__ __forceinline__ void row_store(const RowOut& o, int j, float2 z) {
 // j < half: every k below half / GR, and u < half % GR at k = half / GR, so
 // the guards are uniform branches plus one lane compare per q.
 template <int CROP, int Q, int R, int BITS, int T, int GR>
-__device__ __forceinline__ void last_pass_store(const RowOut& o, const float2* v, int t) {
+__device__ __forceinline__ void last_pass_store(const RowOut& o, float* __restrict__ p,
+                                                const float2* v, int t) {
   if constexpr (CROP == 1) {
     const int kfull = o.half / GR, rem = o.half % GR;
 #pragma unroll
@@ -193,13 +194,14 @@ __device__ __forceinline__ void last_pass_store(const RowOut& o, const float2* v
 #pragma unroll
       for (int k = 0; k < R; ++k)
         if (k < kfull || (k == kfull && tail))
-          row_store<0>(o, u + k * GR, v[q * R + bitrev(k, BITS)]);
+          row_store<0>(o, p, u + k * GR, v[q * R + bitrev(k, BITS)]);
     }
   } else {
 #pragma unroll
     for (int q = 0; q < Q; ++q)
 #pragma unroll
-      for (int k = 0; k < R; ++k) row_store<CROP>(o, t + q * T + k * GR, v[q * R + bitrev(k, BITS)]);
+      for (int k = 0; k < R; ++k)
+        row_store<CROP>(o, p, t + q * T + k * GR, v[q * R + bitrev(k, BITS)]);
   }
 }
 
@@ -209,7 +211,7 @@ __device__ __forceinline__ void last_pass_store(const RowOut& o, const float2* v
 template <int LOGM, int P, bool INV, bool TO_GLOBAL, int CROP = 0>
 __device__ __forceinline__ void run_passes(float2* v, float2* buf, int t,
                                            const float2* __restrict__ tw, const RowOut& o,
-                                           bool live) {
+                                           float* __restrict__ orow, bool live) {
   using G = Geo<LOGM>;
   constexpr Plan pl{LOGM};
   constexpr int BITS = pl.bits(P), R = 1 << BITS, NSB = pl.ns_bits(P), NS = 1 << NSB;
@@ -224,7 +226,7 @@ __device__ __forceinline__ void run_passes(float2* v, float2* buf, int t,
   constexpr bool LAST = P + 1 == pl.npass();
   if constexpr (LAST && TO_GLOBAL) {
     // Last pass: NS == GR, so the output position of (group g, k) is g + k*GR.
-    if (live) last_pass_store<CROP, G::E / R, R, BITS, G::T, GR>(o, v, t);
+    if (live) last_pass_store<CROP, G::E / R, R, BITS, G::T, GR>(o, orow, v, t);
   } else {
     if constexpr (P > 0) __syncthreads();  // every thread has read its pass input
 #pragma unroll
@@ -235,7 +237,8 @@ __device__ __forceinline__ void run_passes(float2* v, float2* buf, int t,
       for (int k = 0; k < R; ++k) buf[lds_pad(base + k * NS)] = v[q * R + bitrev(k, BITS)];
     }
     __syncthreads();
-    if constexpr (!LAST) run_passes<LOGM, P + 1, INV, TO_GLOBAL, CROP>(v, buf, t, tw, o, live);
+    if constexpr (!LAST)
+      run_passes<LOGM, P + 1, INV, TO_GLOBAL, CROP>(v, buf, t, tw, o, orow, live);
   }
 }
 
@@ -273,7 +276,7 @@ __global__ __launch_bounds__(Geo<LOGM>::NT) void rfft_kernel(const float* __rest
       }
       v[q * R0 + r] = z;
     }
-  run_passes<LOGM, 0, false, false>(v, buf, t, tw, RowOut{}, live);
+  run_passes<LOGM, 0, false, false>(v, buf, t, tw, RowOut{}, nullptr, live);
 
   if (!live) return;
   const float2* wu = tw + pl.offset(pl.npass());
@@ -330,8 +333,7 @@ __global__ __launch_bounds__(Geo<LOGM>::NT) void irfft_kernel(const float2* __re
       const float2 o = make_float2(d.x * w.x + d.y * w.y, d.y * w.x - d.x * w.y);
       v[q * R0 + r] = make_float2(e.x - o.y, e.y + o.x);
     }
-  ro.p = x + (live ? row : 0) * ro.lim;
-  run_passes<LOGM, 0, true, true, CROP>(v, buf, t, tw, ro, live);
+  run_passes<LOGM, 0, true, true, CROP>(v, buf, t, tw, ro, x + (live ? row : 0) * ro.lim, live);
 }
 
 // ---- rows of M >= 2048 complex points: persistent workgroups -----------------
@@ -378,6 +380,11 @@ struct Big {
 };
 
 __device__ __forceinline__ int bpad(int i) { return i + (i >> 5); }
+// bpad(x + c) == bpad(x) + bpad_c(c) for every LDS index the persistent
+// kernels form (c a multiple of 32, or a Stockham write offset k * NS below
+// the next pass's group size); keeping bpad(x) per row and the constant part
+// separate lets the constant fold into the ds instruction's offset field.
+__host__ __device__ constexpr int bpad_c(int c) { return c + (c >> 5); }
 
 // cos(pi m / 16), m in [0, 32)
 __device__ constexpr float kCosPi16[32] = {
@@ -482,15 +489,16 @@ __device__ __forceinline__ void load_tw_bases(float2* twb, int t, const float2* 
 // 0 writes LDS (other threads may still read the row buffer).
 template <int LOGM, int P, bool INV, bool TO_GLOBAL, bool SYNC0, int CROP = 0>
 __device__ __forceinline__ void big_passes(float2* v, float2* buf, int t, const float2* twb,
-                                           const RowOut& o) {
+                                           const RowOut& o, float* __restrict__ orow) {
   using G = Big<LOGM>;
   constexpr int BITS = G::bits(P), R = 1 << BITS, NSB = G::nsb(P), NS = 1 << NSB;
   constexpr int GR = G::M / R, Q = G::E / R;
   if constexpr (P > 0) {
+    const int tb = bpad(t);
 #pragma unroll
     for (int q = 0; q < Q; ++q)
 #pragma unroll
-      for (int r = 0; r < R; ++r) v[q * R + r] = buf[bpad(t + q * G::T + r * GR)];
+      for (int r = 0; r < R; ++r) v[q * R + r] = buf[tb + bpad_c(q * G::T + r * GR)];
   }
 #pragma unroll
   for (int q = 0; q < Q; ++q) {
@@ -499,24 +507,25 @@ __device__ __forceinline__ void big_passes(float2* v, float2* buf, int t, const 
   }
   constexpr bool LAST = P + 1 == G::NP;
   if constexpr (LAST && TO_GLOBAL) {
-    last_pass_store<CROP, Q, R, BITS, G::T, GR>(o, v, t);
+    last_pass_store<CROP, Q, R, BITS, G::T, GR>(o, orow, v, t);
   } else {
     if constexpr (P > 0 || SYNC0) __syncthreads();
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
       const int g = t + q * G::T;
-      const int base = ((g >> NSB) << (NSB + BITS)) + (g & (NS - 1));
+      const int base = bpad(((g >> NSB) << (NSB + BITS)) + (g & (NS - 1)));
 #pragma unroll
-      for (int k = 0; k < R; ++k) buf[bpad(base + k * NS)] = v[q * R + bitrev(k, BITS)];
+      for (int k = 0; k < R; ++k) buf[base + bpad_c(k * NS)] = v[q * R + bitrev(k, BITS)];
     }
     __syncthreads();
-    if constexpr (!LAST) big_passes<LOGM, P + 1, INV, TO_GLOBAL, SYNC0, CROP>(v, buf, t, twb, o);
+    if constexpr (!LAST)
+      big_passes<LOGM, P + 1, INV, TO_GLOBAL, SYNC0, CROP>(v, buf, t, twb, o, orow);
   }
 }
 
 // Pass-0 input of one rfft row: z[m] = x[2m] + i x[2m+1], m = t + r T, zero
 // beyond in_len.
-template <int LOGM, bool VEC>
+template <int LOGM, bool VEC, bool FULL>
 __device__ __forceinline__ void rfft_big_load(float2* v, const float* __restrict__ xr, int t,
                                               int64_t in_len) {
   using G = Big<LOGM>;
@@ -527,7 +536,9 @@ __device__ __forceinline__ void rfft_big_load(float2* v, const float* __restrict
     for (int r = 0; r < R0; ++r) {
       const int64_t j2 = 2 * (int64_t)(t + q * G::T + r * GR0);
       float2 z = make_float2(0.f, 0.f);
-      if (VEC) {
+      if (VEC && FULL) {  // the row covers every sample: no guards
+        z = *reinterpret_cast<const float2*>(xr + j2);
+      } else if (VEC) {
         if (j2 < in_len) z = *reinterpret_cast<const float2*>(xr + j2);
       } else {
         if (j2 < in_len) z.x = xr[j2];
@@ -555,16 +566,20 @@ __global__ __launch_bounds__(Big<LOGM>::T, Big<LOGM>::MIN_BLOCKS) void rfft_big_
     // would hold ~200 VGPRs; recomputed per row they fold into base + offset.
     int t = threadIdx.x;
     WXX_OPAQUE(t);
-    rfft_big_load<LOGM, VEC>(v, x + row * in_len, t, in_len);
-    big_passes<LOGM, 0, false, false, true>(v, buf, t, twb, RowOut{});
+    if (in_len >= 2 * G::M)
+      rfft_big_load<LOGM, VEC, true>(v, x + row * in_len, t, in_len);
+    else
+      rfft_big_load<LOGM, VEC, false>(v, x + row * in_len, t, in_len);
+    big_passes<LOGM, 0, false, false, true>(v, buf, t, twb, RowOut{}, nullptr);
     // untangle: bins k and M - k from Z[k], Z[M - k]
     float2* Xr = X + row * (G::M + 1);
+    const int tb = bpad(t), nb = -t + ((-t) >> 5);  // bpad(t), and bpad(a - t) - bpad_c(a)
 #pragma unroll
     for (int i = 0; i <= G::E / 2; ++i) {
       const int k = t + i * G::T;
       if (k > G::M / 2) break;
-      const float2 a = buf[bpad(k)];
-      const float2 b = buf[bpad((G::M - k) & (G::M - 1))];
+      const float2 a = buf[tb + bpad_c(i * G::T)];
+      const float2 b = buf[k == 0 ? 0 : nb + bpad_c(G::M - i * G::T)];  // bin (M - k) mod M
       const float2 e = make_float2(0.5f * (a.x + b.x), 0.5f * (a.y - b.y));
       const float2 o = make_float2(0.5f * (a.y + b.y), 0.5f * (b.x - a.x));
       const float2 w = cmul(wt, wu[i * G::T]);
@@ -586,14 +601,14 @@ __host__ __device__ constexpr int big_pos0(int e) {
 }
 
 // Spectrum bins of one irfft row at this thread's pass-0 positions.
-template <int LOGM>
+template <int LOGM, bool FULL>
 __device__ __forceinline__ void irfft_big_load(float2* a, const float2* __restrict__ Xr, int t,
                                                int64_t in_len) {
   using G = Big<LOGM>;
 #pragma unroll
   for (int e = 0; e < G::E; ++e) {
     const int j = t + big_pos0<LOGM>(e);
-    a[e] = j < in_len ? Xr[j] : make_float2(0.f, 0.f);
+    a[e] = (FULL || j < in_len) ? Xr[j] : make_float2(0.f, 0.f);  // FULL: in_len >= M
   }
 }
 
@@ -613,17 +628,24 @@ __global__ __launch_bounds__(Big<LOGM>::T, Big<LOGM>::MIN_BLOCKS) void irfft_big
     int t = threadIdx.x;  // opaque per row, as in rfft_big_kernel
     WXX_OPAQUE(t);
     const float2* Xr = X + row * in_len;
-    irfft_big_load<LOGM>(v, Xr, t, in_len);
+    if (in_len >= G::M)
+      irfft_big_load<LOGM, true>(v, Xr, t, in_len);
+    else
+      irfft_big_load<LOGM, false>(v, Xr, t, in_len);
     const float2 nyq = G::M < in_len ? Xr[G::M] : make_float2(0.f, 0.f);
     // exchange the bins through LDS to pair j with M - j
+    const int tb = bpad(t), nb = -t + ((-t) >> 5);  // bpad(t), and bpad(a - t) - bpad_c(a)
 #pragma unroll
-    for (int e = 0; e < G::E; ++e) buf[bpad(t + big_pos0<LOGM>(e))] = v[e];
+    for (int e = 0; e < G::E; ++e) buf[tb + bpad_c(big_pos0<LOGM>(e))] = v[e];
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < G::E; ++e) {
       const int j = t + big_pos0<LOGM>(e);
       float2 a = v[e];
-      float2 b = j == 0 ? nyq : buf[bpad(G::M - j)];
+      // select the LDS index, then the value (a select between &nyq and the
+      // LDS slot would become a generic pointer and flat loads)
+      float2 b = buf[j == 0 ? 0 : nb + bpad_c(G::M - big_pos0<LOGM>(e))];
+      if (j == 0) b = nyq;
       if (j == 0) {
         a.y = 0.f;
         b.y = 0.f;
@@ -634,9 +656,8 @@ __global__ __launch_bounds__(Big<LOGM>::T, Big<LOGM>::MIN_BLOCKS) void irfft_big
       const float2 o = make_float2(d.x * w.x + d.y * w.y, d.y * w.x - d.x * w.y);
       v[e] = make_float2(ee.x - o.y, ee.y + o.x);
     }
-    ro.p = x + row * ro.lim;
     // SYNC0: every thread has read its pair partner before pass 0 overwrites LDS
-    big_passes<LOGM, 0, true, true, true, CROP>(v, buf, t, twb, ro);
+    big_passes<LOGM, 0, true, true, true, CROP>(v, buf, t, twb, ro, x + row * ro.lim);
     __syncthreads();  // last pass reads of this row are done
   }
 }
