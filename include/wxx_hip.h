@@ -66,10 +66,20 @@ int wxx_timer_elapsed(int start, int stop, float* ms);
 /* ---- A: GEMM — functional.matmul_add (functional/utils.py:378-499) +
  *      shaders/matmul.wgsl.  sA/sB = batch strides (0 = unbatched);
  *      bias_mode 0 none, 1 (N,), 2 (M,N), 3 (batch,M,N); tile 0 = auto, else a
- *      tile code (1-8) plus 256 x the number of K splits. ---- */
+ *      tile code (1-10) plus 256 x the number of K splits. ---- */
 int wxx_matmul_add(const float* A, const float* B, const float* bias, float* C, int64_t M,
                    int64_t N, int64_t K, int64_t batch, int64_t sA, int64_t sB, int64_t sBias,
                    int bias_mode, int transpose_A, int transpose_B, int tile);
+/* No counterpart in the reference: the products of causal attention with
+ * their exactly-zero triangles skipped (same results as wxx_matmul_add, no
+ * bias).  tri 1: C square, tiles wholly above the diagonal set to 0 (Q K^T,
+ * dO V^T); tri 2: op(A) square lower triangular (P V, dS K); tri 3: op(A)
+ * square upper triangular (P^T dO, dS^T Q); tri 4: as 1 with the tiles above
+ * the diagonal left unwritten.  Used by nn MultiHeadAttention under GPT-2's
+ * causal mask (nn/module.py:447-495, nn/gpt.py:75-96). */
+int wxx_matmul_tri(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K,
+                   int64_t batch, int64_t sA, int64_t sB, int transpose_A, int transpose_B,
+                   int tri);
 
 /* ---- B: convolution and pooling (functional/convolution.py), NCHW f32.
  *      Output size Ho = (H + 2ph - dh(KH-1) - 1)/sh + 1 (conv), (H + 2ph - KH)/sh + 1 (pool). */
@@ -156,6 +166,14 @@ int wxx_softmax_scale_mask(const float* x, const float* mask, float* y, int64_t 
  * backward (autograd/pointwise.py mulscaler) in one pass */
 int wxx_softmax_backward_scale(const float* y, const float* g, float* dx, int64_t rows, int64_t C,
                                float scale);
+/* No counterpart in the reference: softmax_scale_mask / its gradient under
+ * GPT-2's causal mask (-1e9 above the diagonal, 0 on and below it): row
+ * i = row % S reads columns j <= i only; the entries above the diagonal are
+ * 0 (left unwritten when skip = 1). */
+int wxx_softmax_causal(const float* x, float* y, int64_t rows, int64_t C, int64_t S, float scale,
+                       int skip);
+int wxx_softmax_backward_causal(const float* y, const float* g, float* dx, int64_t rows, int64_t C,
+                                int64_t S, float scale, int skip);
 /* functional.meanvarnorm (functional/normalization.py:82-145); row_cap 0 = all rows */
 int wxx_meanvarnorm(const float* x, const float* gamma, const float* beta, float* y,
                     float* mean, float* inv_std, int64_t outer, int64_t reduce, int64_t inner,

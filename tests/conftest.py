@@ -29,7 +29,7 @@ if _EMU:
 
 # Cases too large for the CPU emulation (multi-GFLOP GEMMs, 100M-element rows);
 # they run unchanged on the GPU.
-_EMU_HEAVY = ("test_matmul_config2_sizes", "test_train_steps_do_not_grow_live_buffers", "test_matmul_every_tile_code", "test_softmax[shape2", "test_softmax[shape1-",
+_EMU_HEAVY = ("test_matmul_config2_sizes", "test_matmul_tri_modes[1024", "test_train_steps_do_not_grow_live_buffers", "test_matmul_every_tile_code", "test_softmax[shape2", "test_softmax[shape1-",
               "test_layernorm_fwd_bwd[shape1-", "test_rmsnorm_fwd_bwd[shape1-",
               "test_fft_full_size_properties", "test_hyena_shapes",
               "test_embed_bit_exact_and_embeddx[50304", "test_dropout_bit_exact[6291459",

@@ -130,7 +130,7 @@ def test_matmul_split_k_batched(device):
     assert_close(got, og.matmul_add(A, B, bias), **tol(2048))
 
 
-@pytest.mark.parametrize("code", [1, 2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("code", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
 @pytest.mark.parametrize("splits", [1, 3])
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
 def test_matmul_every_tile_code(device, code, splits, ta, tb):
@@ -152,3 +152,36 @@ def test_matmul_every_tile_code(device, code, splits, ta, tb):
         lib.call("wxx_matmul_add", P(tA.data_ptr()), P(tB.data_ptr()), P(tbias.data_ptr()),
                  P(out.data_ptr()), M, N, K, 1, 0, 0, 0, 1, int(ta), int(tb), code + 256 * splits)
         assert_close(out.numpy(), og.matmul_add(A, B, bias, ta, tb), **tol(K))
+
+
+@pytest.mark.parametrize("S,d", [(64, 64), (130, 64), (256, 32), (1024, 64)])
+def test_matmul_tri_modes(device, S, d):
+    # causal-attention products with their zero triangle skipped
+    b = 3
+    r = rng(S + d)
+    q = r.standard_normal((b, S, d)).astype(np.float32)
+    k = r.standard_normal((b, S, d)).astype(np.float32)
+    P = np.tril(r.standard_normal((b, S, S))).astype(np.float32)  # exact zeros above
+    on_or_below = np.tril(np.ones((S, S), bool))
+    # tri 1: scores, needed on / below the diagonal; above it 0 or the value
+    s1 = F().matmul_add(up(q), up(k), None, transpose_B=True, tri=1).numpy()
+    ref = og.matmul_add(q, k, None, False, True)
+    assert_close(s1[:, on_or_below], ref[:, on_or_below], **tol(d))
+    above = s1[:, ~on_or_below]
+    assert np.all((above == 0) | np.isclose(above, ref[:, ~on_or_below], rtol=1e-4, atol=1e-3))
+    # tri 2: P V with P lower triangular; tri 3: P^T V
+    s2 = F().matmul_add(up(P), up(k), None, tri=2).numpy()
+    assert_close(s2, og.matmul_add(P, k), **tol(S))
+    s3 = F().matmul_add(up(P), up(k), None, transpose_A=True, tri=3).numpy()
+    assert_close(s3, og.matmul_add(P, k, None, True, False), **tol(S))
+    # equal to the untriangular product bit for bit (only exact zeros skipped)
+    full2 = F().matmul_add(up(P), up(k), None).numpy()
+    assert np.array_equal(s2, full2)
+    # the zero triangle is never used: NaN there changes nothing
+    Pn = P.copy()
+    Pn[:, ~on_or_below] = np.nan
+    assert np.array_equal(F().matmul_add(up(Pn), up(k), None, tri=2).numpy(), s2)
+    assert np.array_equal(F().matmul_add(up(Pn), up(k), None, transpose_A=True, tri=3).numpy(),
+                          s3)
+    with pytest.raises(ValueError):
+        F().matmul_add(up(q), up(k), up(np.zeros(S)), transpose_B=True, tri=1)

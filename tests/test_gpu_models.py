@@ -250,3 +250,62 @@ def test_clip_grad_norm_device_path_matches_host_path(device):
     coef = 1.0 / (want + 1e-6)
     for (n, g0), (_, p) in zip(grads, m.named_parameters()):
         np.testing.assert_allclose(p.grad.numpy(), g0 * coef, rtol=1e-5, atol=1e-9, err_msg=n)
+
+
+@pytest.mark.parametrize("S", [16, 130])
+def test_causal_attention_skips_match_plain_masked_attention(device, S):
+    # GPT-2's marked causal mask lets attention skip the masked triangles;
+    # the same mask without the mark takes the full products: same numbers
+    wxx = W()
+    from wxx_amd.functional import from_numpy
+
+    D, H, B = 32, 4, 2
+    mha = wxx.nn.MultiHeadAttention(D, H)
+    X = rng(80).standard_normal((B, S, D)).astype(np.float32)
+    G = rng(81).standard_normal((B, S, D)).astype(np.float32)
+    i = np.arange(S)
+    data = np.where(i[None, :] <= i[:, None], 0.0, -1e9).astype(np.float32)
+    res = []
+    for marked in (True, False):
+        mask = from_numpy(data)
+        if marked:
+            mask._causal = True
+        x = up(X)
+        x.requires_grad = True
+        for _, p in mha.named_parameters():
+            p.grad = None
+        y = mha(x, mask)
+        (y * up(G)).sum().backward()
+        res.append([y.numpy(), x.grad.numpy()] + [p.grad.numpy() for _, p in mha.named_parameters()])
+    for a, b in zip(*res):
+        np.testing.assert_allclose(a, b, rtol=1e-6, atol=1e-7)
+
+
+def test_causal_attention_with_dropout_matches_plain(device):
+    # attention dropout > 0 takes the zero-writing causal path; same seeds,
+    # same numbers as the unmarked mask
+    import random
+
+    wxx = W()
+    from wxx_amd.functional import from_numpy
+
+    S, D, H, B = 40, 16, 2, 2
+    mha = wxx.nn.MultiHeadAttention(D, H, dropout=0.3)
+    X = rng(82).standard_normal((B, S, D)).astype(np.float32)
+    i = np.arange(S)
+    data = np.where(i[None, :] <= i[:, None], 0.0, -1e9).astype(np.float32)
+    res = []
+    for marked in (True, False):
+        mask = from_numpy(data)
+        if marked:
+            mask._causal = True
+        random.seed(5)
+        x = up(X)
+        x.requires_grad = True
+        for _, p in mha.named_parameters():
+            p.grad = None
+        y = mha(x, mask)
+        y.sum().backward()
+        res.append([y.numpy(), x.grad.numpy()] + [p.grad.numpy() for _, p in mha.named_parameters()])
+    for a, b in zip(*res):
+        np.testing.assert_allclose(a, b, rtol=1e-6, atol=1e-7)

@@ -158,3 +158,39 @@ def test_softmax_scale_mask_fused(device, rows, C, mask_rows, ld):
     g = r.standard_normal((rows, C)).astype(np.float32)
     dx = F().softmax_backward_scale(F().from_numpy(y), F().from_numpy(g), float(scale)).numpy()
     assert_close(dx, oa.softmax_backward(y, g, -1) * scale, rtol=1e-4, atol=1e-6)
+
+
+@pytest.mark.parametrize("BH,S", [(3, 7), (2, 64), (2, 130), (1, 1024)])
+def test_softmax_causal_equals_masked_softmax(device, BH, S):
+    # the causal path reads only j <= i and must give the masked fused
+    # softmax's numbers bit for bit: those entries equal, zeros above
+    from wxx_amd.functional._common import empty
+
+    r = rng(BH * S)
+    x = (r.standard_normal((BH, S, S)) * 3).astype(np.float32)
+    i = np.arange(S)
+    mask = np.where(i[None, :] <= i[:, None], 0.0, -1e9).astype(np.float32)
+    lower = np.broadcast_to(i[None, :] <= i[:, None], (BH, S, S))
+    scale = 0.125
+    want = F().softmax_scale_mask(F().from_numpy(x), scale, F().from_numpy(mask)).numpy()
+    y = F().softmax_causal(F().from_numpy(x), scale).numpy()
+    assert np.array_equal(y, want)
+    assert np.all(y[~lower] == 0)
+    # skip mode: the upper triangle keeps whatever the buffer held
+    from wxx_amd.backend import lib
+    import ctypes as C
+
+    out = F().from_numpy(np.full((BH, S, S), 7.0, np.float32))
+    tx = F().from_numpy(x)
+    lib.call("wxx_softmax_causal", C.c_void_p(tx.data_ptr()), C.c_void_p(out.data_ptr()), BH * S,
+             S, S, C.c_float(scale), 1)
+    got = out.numpy()
+    assert np.array_equal(got[lower], want[lower]) and np.all(got[~lower] == 7.0)
+    # backward: the masked gradient's numbers on and below the diagonal, 0 above
+    g = r.standard_normal((BH, S, S)).astype(np.float32)
+    wdx = F().softmax_backward_scale(F().from_numpy(want), F().from_numpy(g), scale).numpy()
+    dx = F().softmax_backward_causal(F().from_numpy(want), F().from_numpy(g), scale).numpy()
+    assert np.array_equal(dx[lower], wdx[lower]) and np.all(dx[~lower] == 0)
+    dxs = F().softmax_backward_causal(F().from_numpy(want), F().from_numpy(g), scale,
+                                      skip=True).numpy()
+    assert np.array_equal(dxs[lower], wdx[lower])

@@ -37,10 +37,16 @@ class scaled_masked_softmax(Function):
     multiply, add and softmax Functions of the reference's attention score
     path, nn/module.py:478-483); the mask receives no gradient."""
 
-    def forward(self, tensor1, scale, mask=None):
-        out = functional.softmax_scale_mask(tensor1, scale, mask)
+    def forward(self, tensor1, scale, mask=None, causal=0):
+        # causal: 0 general mask; 1 / 2 GPT-2's causal mask, the probabilities
+        # above the diagonal written as 0 / left unwritten (2 when every
+        # consumer reads only the lower triangle)
+        if causal:
+            out = functional.softmax_causal(tensor1, scale, skip=causal == 2)
+        else:
+            out = functional.softmax_scale_mask(tensor1, scale, mask)
         out.requires_grad = tensor1.requires_grad
-        self.scale = scale
+        self.scale, self.causal = scale, causal
         if out.requires_grad:
             self.hold_output(out)
         return self.attach(out)
@@ -49,6 +55,8 @@ class scaled_masked_softmax(Function):
         if not self.needs_input_grad[0]:
             return None
         y = self.held_output()
+        if self.causal:
+            return functional.softmax_backward_causal(y, g, self.scale, skip=self.causal == 2)
         return functional.softmax_backward_scale(y, g, self.scale)
 
 

@@ -57,28 +57,51 @@ def _weight_grad(a, g, trans_a, target_shape):
     return _sum_to_shape(functional.matmul_add(a, g, None, not trans_a, False), target_shape)
 
 
+# Triangular modes of the attention products under a causal mask (see
+# functional.matmul_add): forward mode, and the modes of the two gradient
+# products.  "scores" = Q K^T, whose entries above the diagonal the mask
+# sends to probability 0 (their gradient is 0); "probs" = P V with P lower
+# triangular.
+_CAUSAL = {
+    "scores": (1, 2, 3),  # C = Q K^T; dQ = dC K (dC lower); dK = dC^T Q
+    "probs": (2, 1, 3),   # C = P V; dP = dC V^T (only below the diagonal used); dV = P^T dC
+    # the same with the tiles above the diagonal left unwritten (every
+    # consumer reads only the lower triangle)
+    "scores_skip": (4, 2, 3),
+    "probs_skip": (2, 4, 3),
+}
+
+
 class matmul(Function):
-    def forward(self, tensor1, tensor2, transpose_a=False, transpose_b=False):
+    def forward(self, tensor1, tensor2, transpose_a=False, transpose_b=False, causal=None):
+        if causal is not None and (causal not in _CAUSAL or transpose_a
+                                   or transpose_b != causal.startswith("scores")):
+            raise ValueError(f"unsupported causal product {causal!r}")
+        modes = _CAUSAL.get(causal, (0, 0, 0))
         out = functional.matmul_add(tensor1, tensor2, None, transpose_A=transpose_a,
-                                    transpose_B=transpose_b)
+                                    transpose_B=transpose_b, tri=modes[0])
         out.requires_grad = tensor1.requires_grad or tensor2.requires_grad
         return self.attach(out, tensor1=tensor1, tensor2=tensor2, transpose_a=transpose_a,
-                           transpose_b=transpose_b)
+                           transpose_b=transpose_b, modes=modes)
 
     def backward(self, g):
         a, b = self.tensor1, self.tensor2
         ta, tb = self.transpose_a, self.transpose_b
+        _, tri_a, tri_b = self.modes
         self.tensor1 = self.tensor2 = None
         ga = gb = None
         if self.needs_input_grad[0]:
             if ta:
                 ga = functional.matmul_add(b, g, None, tb, True)
             else:
-                ga = functional.matmul_add(g, b, None, False, not tb)
+                ga = functional.matmul_add(g, b, None, False, not tb, tri=tri_a)
             ga = _sum_to_shape(ga, self.inputs[0].shape)
         if self.needs_input_grad[1]:
             target = tuple(self.inputs[1].shape)
-            if tb:
+            if tri_b:  # causal: both operands batched, no reduction
+                gb = functional.matmul_add(g if tb else a, a if tb else g, None, True, False,
+                                           tri=tri_b)
+            elif tb:
                 if not ta and len(a.shape) >= 3 and len(target) == 2:
                     gb = functional.matmul_add(_as_matrix(g), _as_matrix(a), None, True, False)
                 else:

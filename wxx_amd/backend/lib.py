@@ -45,6 +45,7 @@ SIGNATURES = {
         I32,
         [P, P, P, P, I64, I64, I64, I64, I64, I64, I64, I32, I32, I32, I32],
     ),
+    "wxx_matmul_tri": (I32, [P, P, P, I64, I64, I64, I64, I64, I64, I32, I32, I32]),
     # convolution / pooling
     "wxx_conv2d": (I32, [P, P, P, P] + [I64] * 13),
     "wxx_conv2ddx": (I32, [P, P, P] + [I64] * 13),
@@ -67,6 +68,8 @@ SIGNATURES = {
     "wxx_softmax_backward": (I32, [P, P, P, I64, I64, I64]),
     "wxx_softmax_scale_mask": (I32, [P, P, P, I64, I64, I64, I64, F32]),
     "wxx_softmax_backward_scale": (I32, [P, P, P, I64, I64, F32]),
+    "wxx_softmax_causal": (I32, [P, P, I64, I64, I64, F32, I32]),
+    "wxx_softmax_backward_causal": (I32, [P, P, P, I64, I64, I64, F32, I32]),
     # normalisation
     "wxx_meanvarnorm": (I32, [P, P, P, P, P, P, I64, I64, I64, F32, I64]),
     "wxx_meanvarnormdx": (I32, [P, P, P, P, P, P, I64, I64, I64, I64]),

@@ -47,9 +47,17 @@ struct GemmArgs {
   int64_t bias_rows;  // mode 2: rows of the bias matrix (row index taken modulo)
   int bias_mode;
   int tiles_m, tiles_n;
+  int64_t nbatch;  // batches in the launch (grid x = nbatch * tiles)
   int vec_ok;  // all leading dims, batch strides and base pointers allow float4
   int64_t kps;  // K elements per split (blockIdx.z); the whole K when not split
   int64_t sZ;   // element stride between split partial outputs (0 when not split)
+  // Causal attention structure (square in the triangular dimension, entries
+  // above the diagonal exactly zero or not needed): 0 none; 1 output tiles
+  // wholly above the diagonal are written as zeros without computing; 2 op(A)
+  // is lower triangular, so row tile m0 stops K at m0 + BM; 3 op(A) is upper
+  // triangular (a transposed lower-triangular matrix), so K starts at m0;
+  // 4 as 1 but the tiles above the diagonal are not written at all.
+  int tri;
 };
 
 constexpr int kGroupM = 8;
@@ -90,9 +98,16 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
   const int wn = wave % Cfg::kWavesN;
 
   // ---- tile id: XCD-contiguous remap, then GROUP_M swizzle -------------
+  // blockIdx.x runs over (batch, tile) pairs.  Workgroups are dealt to the 8
+  // XCDs round-robin by id, so id -> (id % 8) * (total / 8) + id / 8 gives
+  // each XCD a contiguous run of pairs: all tiles of a batch (which share
+  // that batch's operands) and neighbouring tiles of one GEMM hit one L2.
   const int ntiles = g.tiles_m * g.tiles_n;
-  int bid = blockIdx.x;
-  if ((ntiles & 7) == 0) bid = (bid & 7) * (ntiles >> 3) + (bid >> 3);
+  const int64_t total = (int64_t)ntiles * g.nbatch;
+  int64_t lin = blockIdx.x;
+  if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
+  const int64_t batch = lin / ntiles;
+  const int bid = (int)(lin - batch * ntiles);
   const int group_size = kGroupM * g.tiles_n;
   const int group = bid / group_size;
   const int first_m = group * kGroupM;
@@ -100,7 +115,6 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
   const int tile_m = first_m + (bid % group_size) % gm;
   const int tile_n = (bid % group_size) / gm;
 
-  const int64_t batch = blockIdx.y;
   const float* __restrict__ A = g.A + batch * g.sA;
   const float* __restrict__ B = g.B + batch * g.sB;
   float* __restrict__ C = g.C + batch * g.sC + (int64_t)blockIdx.z * g.sZ;
@@ -109,8 +123,13 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
   const int64_t n0 = (int64_t)tile_n * BN;
   const int64_t M = g.M, N = g.N;
   // this workgroup's K range [kbeg, K): the whole K, or one split of it
-  const int64_t kbeg = (int64_t)blockIdx.z * g.kps;
-  const int64_t K = min(g.K, kbeg + g.kps);
+  int64_t kbeg = (int64_t)blockIdx.z * g.kps;
+  int64_t K = min(g.K, kbeg + g.kps);
+  // The skipped products are those of exact zeros, so the sums are unchanged.
+  if (g.tri == 1 && n0 >= m0 + BM) K = kbeg;  // every (i, j) of the tile has j > i
+  if (g.tri == 4 && n0 >= m0 + BM) return;     // same tiles, left unwritten
+  if (g.tri == 2) K = min(K, m0 + BM);         // A[i][k] == 0 for k > i
+  if (g.tri == 3) kbeg = max(kbeg, (m0 / BK) * BK);  // op(A)[i][k] == 0 for k < i
   const bool interior = (m0 + BM <= M) && (n0 + BN <= N);
 
   float4 ra[PA], rb[PB];
@@ -274,10 +293,34 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
     constexpr int LM = decltype(mode_tag)::value;  // load mode of the full chunks
     const int64_t nfast = LM != 0 ? (K - kbeg) / BK : 0;  // chunks loadable without guards
     auto load = [&](int64_t kc) {
+      const int64_t k0 = kbeg + kc * BK;
       if (LM != 0 && kc < nfast)
-        load_chunk(kbeg + kc * BK, std::integral_constant<int, LM>{});
+        load_chunk(k0, std::integral_constant<int, LM>{});
       else
-        load_chunk(kbeg + kc * BK, std::integral_constant<int, 0>{});
+        load_chunk(k0, std::integral_constant<int, 0>{});
+      // Triangular op(A): in chunks that cross the diagonal band the entries
+      // on the zero side are set to 0 as loaded, so the product never depends
+      // on what that triangle holds (it may be left unwritten).
+      if ((g.tri == 2 && k0 + BK - 1 > m0) || (g.tri == 3 && k0 < m0 + BM - 1)) {
+#pragma unroll
+        for (int p = 0; p < PA; ++p) {
+          const int f = p * 256 + tid;  // the index mapping of load_chunk
+          float e[4] = {ra[p].x, ra[p].y, ra[p].z, ra[p].w};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            int64_t i, k;
+            if (!TA) {
+              i = m0 + f / (BK / 4);
+              k = k0 + (f % (BK / 4)) * 4 + c;
+            } else {
+              i = m0 + (f % (BM / 4)) * 4 + c;
+              k = k0 + f / (BM / 4);
+            }
+            if (g.tri == 2 ? k > i : k < i) e[c] = 0.f;
+          }
+          ra[p] = make_float4(e[0], e[1], e[2], e[3]);
+        }
+      }
     };
     load(0);
     store_chunk(0);
@@ -391,7 +434,8 @@ int launch_cfg(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits = 1) {
 
 template <int BM, int BN, int BK, int WM, int WN, int NBUF>
 int launch_tiles(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits) {
-  dim3 grid((unsigned)(g.tiles_m * g.tiles_n), (unsigned)batch, (unsigned)splits);
+  g.nbatch = batch;
+  dim3 grid((unsigned)((int64_t)g.tiles_m * g.tiles_n * batch), 1, (unsigned)splits);
   hipStream_t s = wxx::stream();
   if (!ta && !tb)
     hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, false, NBUF>), grid,
@@ -415,13 +459,48 @@ inline bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 // Replaces functional.matmul_add (reference src/wxx/functional/utils.py:378-499).
 // Strides are in elements; sA / sB == 0 marks an unbatched operand.
-// tile: 0 = choose automatically, 1 = 64x64, 2 = 128x128, 3 = 256x128; 4-8 select
+// tile: 0 = choose automatically, 1 = 64x64, 2 = 128x128, 3 = 256x128; 4-10 select
 // alternative tile / K-chunk / buffering shapes of the same kernel.  With an
 // explicit tile code, bits 8-15 give the number of K splits (0 or 1: none).
+namespace {
+int matmul_impl(const float* A, const float* B, const float* bias, float* C, int64_t M, int64_t N,
+                int64_t K, int64_t batch, int64_t sA, int64_t sB, int64_t sBias, int bias_mode,
+                int transpose_A, int transpose_B, int tile, int tri);
+}  // namespace
+
 WXX_API int wxx_matmul_add(const float* A, const float* B, const float* bias, float* C,
                            int64_t M, int64_t N, int64_t K, int64_t batch, int64_t sA,
                            int64_t sB, int64_t sBias, int bias_mode, int transpose_A,
                            int transpose_B, int tile) {
+  return matmul_impl(A, B, bias, C, M, N, K, batch, sA, sB, sBias, bias_mode, transpose_A,
+                     transpose_B, tile, 0);
+}
+
+// Causal-attention products (no counterpart in the reference: the same
+// C = op(A) op(B) as wxx_matmul_add without bias, for operands whose
+// entries above the diagonal are exactly zero, or outputs whose entries
+// above the diagonal are not needed).  tri 1: C is square (M == N) and its
+// tiles wholly above the diagonal are set to 0 instead of computed (the
+// scores Q K^T and dO V^T of masked attention); tri 2: op(A) is square lower
+// triangular (M == K), e.g. the probabilities P in P V; tri 3: op(A) is
+// square upper triangular, e.g. P^T in P^T dO; tri 4: as 1, but the tiles
+// wholly above the diagonal are left unwritten (for consumers that read only
+// the lower triangle).  The products skipped are those of exact zeros, so
+// the results equal wxx_matmul_add's.
+WXX_API int wxx_matmul_tri(const float* A, const float* B, float* C, int64_t M, int64_t N,
+                           int64_t K, int64_t batch, int64_t sA, int64_t sB, int transpose_A,
+                           int transpose_B, int tri) {
+  WXX_REQUIRE(tri >= 1 && tri <= 4, "bad tri mode %d", tri);
+  WXX_REQUIRE((tri == 1 || tri == 4) ? M == N : M == K,
+              "tri mode %d needs a square triangular operand", tri);
+  return matmul_impl(A, B, nullptr, C, M, N, K, batch, sA, sB, 0, 0, transpose_A, transpose_B, 0,
+                     tri);
+}
+
+namespace {
+int matmul_impl(const float* A, const float* B, const float* bias, float* C, int64_t M, int64_t N,
+                int64_t K, int64_t batch, int64_t sA, int64_t sB, int64_t sBias, int bias_mode,
+                int transpose_A, int transpose_B, int tile, int tri) {
   WXX_CHECK_INIT();
   WXX_REQUIRE(A && B && C, "null pointer");
   WXX_REQUIRE(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "negative GEMM dims");
@@ -447,10 +526,11 @@ WXX_API int wxx_matmul_add(const float* A, const float* B, const float* bias, fl
   g.sBias = sBias;
   g.bias_mode = bias_mode;
   g.bias_rows = M;
+  g.tri = tri;
   int64_t nb = batch;
   // Fold the batch into M when B is shared and A's rows are contiguous across
   // batches: one larger GEMM fills the GPU better than `batch` small ones.
-  if (batch > 1 && sB == 0 && !transpose_A && sA == M * K) {
+  if (batch > 1 && sB == 0 && !transpose_A && sA == M * K && tri == 0) {
     g.M = M * batch;
     g.sA = 0;
     g.sC = 0;
@@ -473,7 +553,8 @@ WXX_API int wxx_matmul_add(const float* A, const float* B, const float* bias, fl
   splits = std::max(splits, 1);
   if (tile == 0) {
     // Measured on MI355X (fp32 GEMM shapes of GPT-2 small and BASELINE
-    // config 2): 128x128 tiles are the fastest once they cover the CUs;
+    // config 2): 128x128 tiles are the fastest once they cover the CUs
+    // twice (128x64 below that when K is short);
     // the 32-deep single-buffered variant wins for long K; 64x64 tiles win
     // for thin operands (attention's N = 64 / K = 64 products) and when the
     // grid would otherwise leave CUs idle; K is split only when the output
@@ -483,13 +564,17 @@ WXX_API int wxx_matmul_add(const float* A, const float* B, const float* bias, fl
     const int64_t t64 = ((g.M + 63) / 64) * ((g.N + 63) / 64) * nb;
     const int64_t kmax = std::max<int64_t>(g.K / 1024, 1);
     if (g.M <= 64 || g.N <= 64 || g.K <= 128) {
-      tile = 1;
-      if (t64 < 2 * cus) splits = (int)std::min<int64_t>((8 * cus + t64 - 1) / t64, kmax);
+      // N = 64 over long M (attention's P V, dS K, P^T dO): 128 x 64 tiles
+      tile = (g.N <= 64 && g.M >= 128 && g.K > 128) ? (transpose_A ? 10 : 9) : 1;
+      if (tile == 1 && t64 < 2 * cus)
+        splits = (int)std::min<int64_t>((8 * cus + t64 - 1) / t64, kmax);
     } else if (t128 >= cus) {
       tile = g.K >= 4096 ? 4 : 2;
       if (t128 < 2 * cus && g.K >= 2048) {
         tile = 2;
         splits = 2;
+      } else if (t128 < 2 * cus) {
+        tile = 9;  // short K: 128 x 64 tiles give the grid twice the workgroups
       }
     } else if (2 * t128 >= cus && g.K >= 4096) {
       tile = 4;
@@ -500,6 +585,7 @@ WXX_API int wxx_matmul_add(const float* A, const float* B, const float* bias, fl
     }
     splits = std::max(1, std::min(splits, 32));
   }
+  if (tri) splits = 1;  // the triangular K ranges are per row tile
   switch (tile) {
     case 1: return launch_cfg<64, 64, 16, 32, 32>(g, nb, transpose_A, transpose_B, splits);
     case 2: return launch_cfg<128, 128, 16, 64, 64>(g, nb, transpose_A, transpose_B, splits);
@@ -510,6 +596,9 @@ WXX_API int wxx_matmul_add(const float* A, const float* B, const float* bias, fl
     case 6: return launch_cfg<128, 128, 32, 64, 64, 2>(g, nb, transpose_A, transpose_B, splits);
     case 7: return launch_cfg<256, 128, 32, 128, 64, 2>(g, nb, transpose_A, transpose_B, splits);
     case 8: return launch_cfg<128, 256, 16, 64, 128>(g, nb, transpose_A, transpose_B, splits);
+    case 9: return launch_cfg<128, 64, 16, 64, 32>(g, nb, transpose_A, transpose_B, splits);
+    case 10: return launch_cfg<128, 64, 32, 64, 32, 1>(g, nb, transpose_A, transpose_B, splits);
     default: return wxx::set_error(WXX_E_ARG, "bad tile %d", tile);
   }
 }
+}  // namespace

@@ -78,6 +78,50 @@ struct RowRegs {
   }
 
   __device__ __forceinline__ bool valid(int e, int t, int C) const { return col(e, t) < C; }
+
+  // The first lim columns of the row (lim <= C), pad beyond: the lower
+  // triangle of a causal attention row.
+  __device__ __forceinline__ void load_lim(const float* __restrict__ row, int lim, int t,
+                                           float pad) {
+    if (VEC) {
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        const int base = (c * TPR + t) * 4;
+        if (base + 4 <= lim) {
+          float4 q = *reinterpret_cast<const float4*>(row + base);
+          v[c * 4 + 0] = q.x;
+          v[c * 4 + 1] = q.y;
+          v[c * 4 + 2] = q.z;
+          v[c * 4 + 3] = q.w;
+        } else {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) v[c * 4 + k] = base + k < lim ? row[base + k] : pad;
+        }
+      }
+    } else {
+      load(row, lim, t, pad);
+    }
+  }
+
+  // Stores the first lim columns only.
+  __device__ __forceinline__ void store_lim(float* __restrict__ row, int lim, int t) const {
+    if (VEC) {
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        const int base = (c * TPR + t) * 4;
+        if (base + 4 <= lim) {
+          *reinterpret_cast<float4*>(row + base) =
+              make_float4(v[c * 4 + 0], v[c * 4 + 1], v[c * 4 + 2], v[c * 4 + 3]);
+        } else {
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+            if (base + k < lim) row[base + k] = v[c * 4 + k];
+        }
+      }
+    } else {
+      store(row, lim, t);
+    }
+  }
 };
 
 // Pick (TPR, NCH) for a row length: one wave per row up to 2048 columns,

@@ -19,7 +19,14 @@ namespace {
 // mask rows mask_ld floats apart (the
 // attention score scaling and additive mask), with the two roundings of the
 // separate multiply and add kept (no fused multiply-add).
-template <int TPR, int NCH, bool VEC, bool PRE = false>
+//
+// CAUSAL (with PRE; mask_rows = the diagonal's period S): the mask is GPT-2's
+// causal mask, 0 on and below the diagonal and -1e9 above it, so row
+// i = row % S reads only columns j <= i (x * scale + 0 there) and the others
+// are probability exactly 0 (exp(-1e9 - m) underflows), as in the masked
+// computation.  CAUSAL 1 writes those zeros; CAUSAL 2 leaves them unwritten
+// for consumers that read only the lower triangle.
+template <int TPR, int NCH, bool VEC, bool PRE = false, int CAUSAL = 0>
 __global__ __launch_bounds__(256) void softmax_rows_kernel(const float* __restrict__ x,
                                                             float* __restrict__ y, int64_t rows,
                                                             int C,
@@ -34,8 +41,16 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(const float* __restri
   if (TPR == 64 && row >= rows) return;
   const float* xr = x + row * C;
   wxx::RowRegs<TPR, NCH, VEC> r;
-  r.load(xr, C, t, -INFINITY);
-  if (PRE) {
+  const int lim = CAUSAL ? (int)min<int64_t>(C, row % mask_rows + 1) : C;
+  if (CAUSAL)
+    r.load_lim(xr, lim, t, -INFINITY);
+  else
+    r.load(xr, C, t, -INFINITY);
+  if (PRE && CAUSAL) {
+#pragma unroll
+    for (int e = 0; e < NCH * 4; ++e)
+      if (r.valid(e, t, lim)) r.v[e] = __fadd_rn(__fmul_rn(r.v[e], scale), 0.f);
+  } else if (PRE) {
     wxx::RowRegs<TPR, NCH, VEC> mk;
     if (mask) mk.load(mask + (row % mask_rows) * mask_ld, C, t, 0.f);
 #pragma unroll
@@ -58,7 +73,10 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(const float* __restri
   const float inv = 1.0f / s;
 #pragma unroll
   for (int e = 0; e < NCH * 4; ++e) r.v[e] *= inv;
-  r.store(y + row * C, C, t);
+  if (CAUSAL == 2)
+    r.store_lim(y + row * C, lim, t);
+  else
+    r.store(y + row * C, C, t);
 }
 
 // Rows longer than 16384: online max/sum in one pass, then a write pass.
@@ -121,20 +139,31 @@ __global__ __launch_bounds__(256) void softmax_cols_kernel(const float* __restri
 // dx = y * (g - sum(g * y)) per row: one read of y and g, one write.
 // SCALED: dx is further multiplied by `scale` (the gradient through the
 // score scaling), as a separate rounding.
-template <int TPR, int NCH, bool VEC, bool SCALED = false>
+// CAUSAL (rows of period diag): y is zero above the diagonal, so row
+// i = row % diag reads y and g for columns j <= i only (the dot product is
+// the same: the other terms are exact zeros); CAUSAL 1 writes dx = 0 above
+// the diagonal, CAUSAL 2 leaves it unwritten.
+template <int TPR, int NCH, bool VEC, bool SCALED = false, int CAUSAL = 0>
 __global__ __launch_bounds__(256) void softmax_bwd_rows_kernel(const float* __restrict__ y,
                                                                 const float* __restrict__ g,
                                                                 float* __restrict__ dx,
                                                                 int64_t rows, int C,
-                                                                float scale = 1.f) {
+                                                                float scale = 1.f,
+                                                                int64_t diag = 1) {
   __shared__ float red[4];
   constexpr int RPB = 256 / TPR;
   const int t = threadIdx.x % TPR;
   const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;
   if (TPR == 64 && row >= rows) return;
   wxx::RowRegs<TPR, NCH, VEC> vy, vg;
-  vy.load(y + row * C, C, t, 0.f);
-  vg.load(g + row * C, C, t, 0.f);
+  const int lim = CAUSAL ? (int)min<int64_t>(C, row % diag + 1) : C;
+  if (CAUSAL) {
+    vy.load_lim(y + row * C, lim, t, 0.f);
+    vg.load_lim(g + row * C, lim, t, 0.f);
+  } else {
+    vy.load(y + row * C, C, t, 0.f);
+    vg.load(g + row * C, C, t, 0.f);
+  }
   float dot = 0.f;
 #pragma unroll
   for (int e = 0; e < NCH * 4; ++e) dot += vg.v[e] * vy.v[e];
@@ -144,7 +173,10 @@ __global__ __launch_bounds__(256) void softmax_bwd_rows_kernel(const float* __re
     vy.v[e] = vy.v[e] * (vg.v[e] - dot);
     if (SCALED) vy.v[e] = __fmul_rn(vy.v[e], scale);
   }
-  vy.store(dx + row * C, C, t);
+  if (CAUSAL == 2)
+    vy.store_lim(dx + row * C, lim, t);
+  else
+    vy.store(dx + row * C, C, t);
 }
 
 __global__ __launch_bounds__(256) void softmax_bwd_cols_kernel(const float* __restrict__ y,
@@ -269,6 +301,71 @@ WXX_API int wxx_softmax_backward_scale(const float* y, const float* g, float* dx
                                                 decltype(v)::value, true>),
                        wxx::row_grid(decltype(tpr)::value, rows), dim3(256), 0, s, y, g, dx, rows,
                        (int)C, scale);
+    return 0;
+  });
+  if (rc) return rc;
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// Causal attention softmax (no counterpart in the reference: its masked
+// path with GPT-2's causal mask, -1e9 above the diagonal and 0 on and below
+// it, nn/gpt.py:75-96 + nn/module.py:478-483).  Rows of x are rows of
+// (S x C) score blocks; row i = row % S reads x[.. j <= i] only and gives
+// y = softmax(x * scale + 0) there and exactly 0 above the diagonal, the
+// same numbers as wxx_softmax_scale_mask with that mask.  skip = 1 leaves
+// the zeros above the diagonal unwritten (for consumers that read only the
+// lower triangle).
+WXX_API int wxx_softmax_causal(const float* x, float* y, int64_t rows, int64_t C, int64_t S,
+                               float scale, int skip) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(x && y, "null pointer");
+  WXX_REQUIRE(rows >= 0 && C >= 1 && S >= 1, "bad softmax dims");
+  if (wxx::row_plan(C) == 0)
+    return wxx::set_error(WXX_E_UNSUPPORTED, "fused softmax rows of %lld", (long long)C);
+  if (rows == 0) return WXX_OK;
+  hipStream_t s = wxx::stream();
+  const bool vec = (C % 4 == 0) && ((((uintptr_t)x) | ((uintptr_t)y)) % 16 == 0);
+  int rc = wxx::row_dispatch(C, vec, [&](auto tpr, auto nch, auto v) {
+    constexpr int TPR = decltype(tpr)::value, NCH = decltype(nch)::value;
+    constexpr bool V = decltype(v)::value;
+    if (skip)
+      hipLaunchKernelGGL((softmax_rows_kernel<TPR, NCH, V, true, 2>), wxx::row_grid(TPR, rows),
+                         dim3(256), 0, s, x, y, rows, (int)C, nullptr, S, 0, scale);
+    else
+      hipLaunchKernelGGL((softmax_rows_kernel<TPR, NCH, V, true, 1>), wxx::row_grid(TPR, rows),
+                         dim3(256), 0, s, x, y, rows, (int)C, nullptr, S, 0, scale);
+    return 0;
+  });
+  if (rc) return rc;
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// Gradient of wxx_softmax_causal: dx = scale * (y * (g - sum_j<=i g y)) on
+// and below the diagonal (row i = row % S), 0 above it (left unwritten when
+// skip = 1); y and g are read on and below the diagonal only.
+WXX_API int wxx_softmax_backward_causal(const float* y, const float* g, float* dx, int64_t rows,
+                                        int64_t C, int64_t S, float scale, int skip) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(y && g && dx, "null pointer");
+  WXX_REQUIRE(rows >= 0 && C >= 1 && S >= 1, "bad softmax dims");
+  if (wxx::row_plan(C) == 0)
+    return wxx::set_error(WXX_E_UNSUPPORTED, "fused softmax rows of %lld", (long long)C);
+  if (rows == 0) return WXX_OK;
+  hipStream_t s = wxx::stream();
+  const bool vec = (C % 4 == 0) && ((((uintptr_t)y) | ((uintptr_t)g) | ((uintptr_t)dx)) % 16 == 0);
+  int rc = wxx::row_dispatch(C, vec, [&](auto tpr, auto nch, auto v) {
+    constexpr int TPR = decltype(tpr)::value, NCH = decltype(nch)::value;
+    constexpr bool V = decltype(v)::value;
+    if (skip)
+      hipLaunchKernelGGL((softmax_bwd_rows_kernel<TPR, NCH, V, true, 2>),
+                         wxx::row_grid(TPR, rows), dim3(256), 0, s, y, g, dx, rows, (int)C, scale,
+                         S);
+    else
+      hipLaunchKernelGGL((softmax_bwd_rows_kernel<TPR, NCH, V, true, 1>),
+                         wxx::row_grid(TPR, rows), dim3(256), 0, s, y, g, dx, rows, (int)C, scale,
+                         S);
     return 0;
   });
   if (rc) return rc;

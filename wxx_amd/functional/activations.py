@@ -191,6 +191,43 @@ def softmax_scale_mask(tensor1, scale, mask=None):
     return out
 
 
+def softmax_causal(tensor1, scale, skip=False):
+    """``softmax(tensor1 * scale + causal_mask, dim=-1)`` for the (..., S, S)
+    scores of attention under GPT-2's causal mask (0 on and below the
+    diagonal, -1e9 above): each row reads its columns j <= i only and the
+    result is exactly 0 above the diagonal, the numbers of
+    :func:`softmax_scale_mask` with that mask.  ``skip`` leaves the zeros
+    above the diagonal unwritten (for consumers reading only the lower
+    triangle)."""
+    if not tensor1.is_contiguous():
+        tensor1 = tensor1.contiguous()
+    S, C = tensor1.shape[-2], tensor1.shape[-1]
+    if C > 16384 or S != C:
+        raise ValueError(f"causal softmax needs square score blocks of <= 16384, got {S}x{C}")
+    rows = validation.numel(tensor1.shape) // C
+    out = empty(tensor1.shape, requires_grad=tensor1.requires_grad)
+    if rows:
+        call("wxx_softmax_causal", ptr(tensor1), ptr(out), rows, C, S, float(scale),
+             1 if skip else 0)
+    return out
+
+
+def softmax_backward_causal(y, grad, scale, skip=False):
+    """Gradient of :func:`softmax_causal` (``grad`` read on and below the
+    diagonal only; 0 above it, left unwritten when ``skip``)."""
+    if not y.is_contiguous():
+        y = y.contiguous()
+    if not grad.is_contiguous():
+        grad = grad.contiguous()
+    S, C = y.shape[-2], y.shape[-1]
+    rows = validation.numel(y.shape) // C
+    out = empty(y.shape)
+    if rows:
+        call("wxx_softmax_backward_causal", ptr(y), ptr(grad), ptr(out), rows, C, S,
+             float(scale), 1 if skip else 0)
+    return out
+
+
 def softmax_backward_scale(y, grad, scale):
     """Gradient of :func:`softmax_scale_mask`: ``scale * y * (grad - sum(grad * y))``."""
     if not y.is_contiguous():

@@ -212,8 +212,14 @@ def contiguous(tensor1):
     return out
 
 
-def matmul_add(tensor1, tensor2, tensor3, transpose_A=False, transpose_B=False):
-    """Batched ``op(A) @ op(B) (+ bias)`` over the last two dimensions."""
+def matmul_add(tensor1, tensor2, tensor3, transpose_A=False, transpose_B=False, tri=0):
+    """Batched ``op(A) @ op(B) (+ bias)`` over the last two dimensions.
+
+    ``tri`` (no bias) marks causal-attention structure whose zero triangle
+    the kernel skips, with the same result: 1 the square output is only
+    needed on and below the diagonal (zeros above), 2 ``op(A)`` is square
+    lower triangular, 3 ``op(A)`` is square upper triangular.
+    """
     validation.check_rank(tensor1.shape, min_rank=2, name="matmul left operand")
     validation.check_rank(tensor2.shape, min_rank=2, name="matmul right operand")
     if not tensor1.is_contiguous():
@@ -267,6 +273,12 @@ def matmul_add(tensor1, tensor2, tensor3, transpose_A=False, transpose_B=False):
             or (tensor3 is not None and tensor3.requires_grad)
         ),
     )
+    if tri:
+        if bias_ptr is not None:
+            raise ValueError("a triangular product takes no bias")
+        call("wxx_matmul_tri", ptr(tensor1), ptr(tensor2), ptr(out), M, N, K, batch, s_a, s_b,
+             1 if transpose_A else 0, 1 if transpose_B else 0, int(tri))
+        return out
     call(
         "wxx_matmul_add",
         ptr(tensor1),

@@ -69,10 +69,15 @@ class GPT2(Module):
             i = np.arange(self.max_len)
             data = np.where(i[None, :] <= i[:, None], 0.0, -1e9).astype(np.float32)
             mask = from_numpy(np.ascontiguousarray(data))
+            mask._causal = True
             self._causal_mask_cache = mask
         if seq == self.max_len:
             return mask
-        return mask.narrow(0, 0, seq).narrow(1, 0, seq)
+        view = mask.narrow(0, 0, seq).narrow(1, 0, seq)
+        # marks the -1e9-above-the-diagonal mask: attention may then skip the
+        # products whose results the mask zeroes (nn.MultiHeadAttention)
+        view._causal = True
+        return view
 
     def forward(self, x, mask=None):
         b, seq = x.shape

@@ -375,9 +375,23 @@ class MultiHeadAttention(Module):
         q = self._heads(self.q(x), b, seq)
         k = self._heads(self.k(x), b, seq)
         v = self._heads(self.v(x), b, seq)
-        score = autograd.matmul(q, k).forward(q, k, transpose_b=True)
+        # Under GPT-2's causal mask (-1e9 above the diagonal) the scores above
+        # the diagonal get probability exactly 0 and their gradients are
+        # exactly 0, so the products skip those triangles with unchanged results.
+        causal = (mask is not None and getattr(mask, "_causal", False)
+                  and tuple(mask.shape) == (seq, seq) and seq <= 16384)
+        # Without attention dropout every consumer of the scores, the
+        # probabilities and their gradients reads only the lower triangle, so
+        # the upper one is not even written.
+        skip = causal and self.drop.p == 0
+        suffix = "_skip" if skip else ""
+        score = autograd.matmul(q, k).forward(q, k, transpose_b=True,
+                                              causal="scores" + suffix if causal else None)
         scale = 1.0 / math.sqrt(self.head_dim)
-        if mask is None or (len(mask.shape) == 2 and not mask.requires_grad):
+        if causal:
+            attn = autograd.scaled_masked_softmax(score).forward(score, scale, mask,
+                                                                 causal=2 if skip else 1)
+        elif mask is None or (len(mask.shape) == 2 and not mask.requires_grad):
             # scale, mask add and softmax as one pass over the scores (same
             # roundings as the three separate ops)
             attn = autograd.scaled_masked_softmax(score).forward(score, scale, mask)
@@ -385,7 +399,8 @@ class MultiHeadAttention(Module):
             score = score * scale
             attn = (score + mask).softmax(dim=-1)
         attn = self.drop(attn)
-        out = autograd.matmul(attn, v).forward(attn, v)
+        out = autograd.matmul(attn, v).forward(attn, v,
+                                               causal="probs" + suffix if causal else None)
         out = (out.reshape((b, self.n_heads, seq, self.head_dim)).permute(0, 2, 1, 3)
                .reshape((b, seq, self.d_model)))
         return self.out(out)
