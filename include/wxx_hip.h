@@ -274,6 +274,13 @@ int wxx_complex_pad(const void* src, void* dst, int64_t batch, int64_t in_len, i
  *      target is >= K; the caller zeroes and reads it. ---- */
 int wxx_cceloss(const float* z, const uint32_t* targets, float* loss, float* dz, int64_t B,
                 int64_t K, int* bad);
+/* No single reference counterpart: cceloss with dlogits deferred to the
+ * backward (autograd/layers.py:6-20), already scaled by the upstream gradient
+ * g[row * g_stride].  stats holds (max, exp-sum) per row; K <= 65536. */
+int wxx_cceloss_stats(const float* z, const uint32_t* targets, float* loss, float* stats,
+                      int64_t B, int64_t K, int* bad);
+int wxx_cceloss_backward(const float* z, const uint32_t* targets, const float* stats,
+                         const float* g, int64_t g_stride, float* dz, int64_t B, int64_t K);
 
 /* ---- E8 / D8: optimizer and gradient norm ---------------------------------- */
 /* functional.adamw (functional/layers.py:21-68) */

@@ -43,6 +43,28 @@ def test_cceloss(device, B, K, scale):
     assert_close(dz.numpy(), edz, rtol=1e-4, atol=1e-6, msg="dlogits")
 
 
+@pytest.mark.parametrize("B,K", [(5, 10), (64, 1000), (8, 50304), (3, 70001)])
+def test_cceloss_autograd_deferred_gradient(device, B, K):
+    # the autograd path defers dlogits to the backward (rows <= 65536); the
+    # loss and the gradient equal cceloss's, times the mean's 1/B, bit for bit
+    import wxx_amd as wxx
+
+    z = (rng(B + K).standard_normal((B, K)) * 3).astype(np.float32)
+    t = rng(K).integers(0, K, B).astype(np.uint32)
+    t[-1] = K - 1
+    loss_e, dz_e = F().cceloss(up(z), up_u32(t))
+    want = (dz_e * F().from_numpy(np.full((B, 1), 1.0 / B, np.float32))).numpy()
+    x = up(z)
+    x.requires_grad = True
+    rows = wxx.autograd.CrossEntropyLoss(x).forward(x, up_u32(t))  # per-row losses
+    assert np.array_equal(rows.numpy(), loss_e.numpy())
+    loss = rows.mean()
+    loss.backward()
+    assert np.array_equal(x.grad.numpy(), want)
+    with pytest.raises(ValueError):  # out-of-range target, autograd path
+        wxx.nn.CCELoss()(x, up_u32(np.full(B, K, np.uint32)))
+
+
 def test_cceloss_rejects_out_of_range_target(device):
     z = np.zeros((3, 5), np.float32)
     with pytest.raises(ValueError):

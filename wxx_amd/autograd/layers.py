@@ -5,16 +5,29 @@ from .function import Function
 
 
 class CrossEntropyLoss(Function):
-    """Per-row softmax cross-entropy; backward scales the fused dlogits by ``g``."""
+    """Per-row softmax cross-entropy; the logits gradient is the fused
+    dlogits scaled by ``g``.  Rows up to 65536 defer dlogits to the backward
+    (one pass writing the scaled gradient; the forward keeps each row's max
+    and exp-sum), longer rows keep cceloss's eager dlogits."""
 
     def forward(self, tensor1, tensor2):
+        deferred = functional.cceloss_stats(tensor1, tensor2) if any(self.needs_input_grad) \
+            else None
+        if deferred is not None:
+            loss, stats, logits, targets = deferred
+            loss.requires_grad = True
+            return self.attach(loss, stats=stats, logits=logits, targets=targets, grad=None)
         loss, grad = functional.cceloss(tensor1, tensor2)
         loss.requires_grad = any(self.needs_input_grad)
-        return self.attach(loss, grad=grad)
+        return self.attach(loss, grad=grad, stats=None)
 
     def backward(self, g):
         # one gradient: the Function is built with the logits only
         # (CrossEntropyLoss(prediction), reference nn/loss.py:28)
+        if self.stats is not None:
+            out = functional.cceloss_grad(self.logits, self.targets, self.stats, g)
+            self.stats = self.logits = self.targets = None
+            return out
         grad, self.grad = self.grad, None
         return functional.pointwise(grad, g, 2)
 

@@ -102,6 +102,8 @@ SIGNATURES = {
     "wxx_complex_pad": (I32, [P, P, I64, I64, I64]),
     # loss
     "wxx_cceloss": (I32, [P, P, P, P, I64, I64, P]),
+    "wxx_cceloss_stats": (I32, [P, P, P, P, I64, I64, P]),
+    "wxx_cceloss_backward": (I32, [P, P, P, P, I64, P, I64, I64]),
     # optimizer / grad norm
     "wxx_adamw": (I32, [P, P, P, P, I64, F32, F32, F32, F32, F32, F32, F32]),
     "wxx_adamw_multi": (I32, [P, P, P, P, P, I32, F32, F32, F32, F32, F32, F32, F32]),

@@ -56,3 +56,49 @@ def cceloss(tensor1, tensor2):
         tmax = int(tensor2.numpy().max())
         raise ValueError(f"cceloss targets must be in [0, {K}), got max target {tmax}")
     return loss, grad
+
+
+def _check_targets(tensor1, tensor2, flag, K):
+    bad = np.zeros(1, np.int32)
+    _lib.call("wxx_d2h", bad.ctypes.data_as(C.c_void_p), C.c_void_p(flag.ptr), 4)
+    if bad[0]:
+        tmax = int(tensor2.numpy().max())
+        raise ValueError(f"cceloss targets must be in [0, {K}), got max target {tmax}")
+
+
+def cceloss_stats(tensor1, tensor2):
+    """Forward half of :func:`cceloss` for the autograd path: ``(loss (B, 1),
+    stats (B, 2))`` with each row's max and exp-sum; the logits gradient is
+    produced later by :func:`cceloss_grad` (same values as cceloss's dlogits
+    times the upstream gradient).  None when the rows are too long for it."""
+    if (len(tensor1.shape) != 2 or len(tensor2.shape) != 1 or tensor1.type != "f32"
+            or tensor2.type != "u32" or min(tensor1.shape) < 1 or tensor1.shape[1] > 65536):
+        return None  # cceloss itself validates (and raises) or handles the long rows
+    B, K = tensor1.shape
+    if not tensor1.is_contiguous():
+        tensor1 = tensor1.contiguous()
+    if not tensor2.is_contiguous():
+        tensor2 = tensor2.contiguous()
+    if tensor2.shape[0] != B:
+        raise ValueError(
+            f"cceloss expects one target per row, got {tensor2.shape[0]} targets for {B} rows"
+        )
+    flag = _flag()
+    call("wxx_fill_u32", C.c_void_p(flag.ptr), 1, 0)
+    loss = empty((B, 1), requires_grad=tensor1.requires_grad)
+    stats = empty((B, 2))
+    call("wxx_cceloss_stats", ptr(tensor1), ptr(tensor2), ptr(loss), ptr(stats), B, K,
+         C.c_void_p(flag.ptr))
+    _check_targets(tensor1, tensor2, flag, K)
+    return loss, stats, tensor1, tensor2
+
+
+def cceloss_grad(logits, targets, stats, grad):
+    """``(softmax(logits) - onehot(targets)) * grad[row]`` from :func:`cceloss_stats`."""
+    B, K = logits.shape
+    if len(grad.shape) == 0 or grad.shape[0] != B or validation.numel(grad.shape) != B:
+        raise ValueError(f"cceloss gradient of shape {grad.shape} for {B} rows")
+    out = empty(logits.shape)
+    call("wxx_cceloss_backward", ptr(logits), ptr(targets), ptr(stats), ptr(grad),
+         grad.stride[0], ptr(out), B, K)
+    return out
