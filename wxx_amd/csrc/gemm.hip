@@ -81,7 +81,9 @@ struct GemmCfg {
 
 // NBUF = 2: double-buffered LDS tiles, one barrier per K chunk; NBUF = 1: one
 // LDS tile (half the LDS, so more workgroups per CU), two barriers per chunk.
-template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, int NBUF>
+// TRI: the triangular (causal attention) modes are compiled in; the plain
+// instantiations carry none of their code.
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, int NBUF, bool TRI = false>
 __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
   using Cfg = GemmCfg<BM, BN, BK, WM, WN, TA, TB>;
   constexpr int TM = Cfg::TM, TN = Cfg::TN;
@@ -126,10 +128,12 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
   int64_t kbeg = (int64_t)blockIdx.z * g.kps;
   int64_t K = min(g.K, kbeg + g.kps);
   // The skipped products are those of exact zeros, so the sums are unchanged.
-  if (g.tri == 1 && n0 >= m0 + BM) K = kbeg;  // every (i, j) of the tile has j > i
-  if (g.tri == 4 && n0 >= m0 + BM) return;     // same tiles, left unwritten
-  if (g.tri == 2) K = min(K, m0 + BM);         // A[i][k] == 0 for k > i
-  if (g.tri == 3) kbeg = max(kbeg, (m0 / BK) * BK);  // op(A)[i][k] == 0 for k < i
+  if constexpr (TRI) {
+    if (g.tri == 1 && n0 >= m0 + BM) K = kbeg;  // every (i, j) of the tile has j > i
+    if (g.tri == 4 && n0 >= m0 + BM) return;     // same tiles, left unwritten
+    if (g.tri == 2) K = min(K, m0 + BM);         // A[i][k] == 0 for k > i
+    if (g.tri == 3) kbeg = max(kbeg, (m0 / BK) * BK);  // op(A)[i][k] == 0 for k < i
+  }
   const bool interior = (m0 + BM <= M) && (n0 + BN <= N);
 
   float4 ra[PA], rb[PB];
@@ -301,7 +305,7 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
       // Triangular op(A): in chunks that cross the diagonal band the entries
       // on the zero side are set to 0 as loaded, so the product never depends
       // on what that triangle holds (it may be left unwritten).
-      if ((g.tri == 2 && k0 + BK - 1 > m0) || (g.tri == 3 && k0 < m0 + BM - 1)) {
+      if (TRI && ((g.tri == 2 && k0 + BK - 1 > m0) || (g.tri == 3 && k0 < m0 + BM - 1))) {
 #pragma unroll
         for (int p = 0; p < PA; ++p) {
           const int f = p * 256 + tid;  // the index mapping of load_chunk
@@ -372,7 +376,7 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
   }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int NBUF>
+template <int BM, int BN, int BK, int WM, int WN, int NBUF, bool TRI = false>
 int launch_tiles(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits);
 
 // Adds the split-K partials part[z][b][M][N] in split order (deterministic)
@@ -397,14 +401,14 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmArgs g,
   }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int NBUF = 2>
+template <int BM, int BN, int BK, int WM, int WN, int NBUF = 2, bool TRI = false>
 int launch_cfg(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits = 1) {
   g.tiles_m = (int)((g.M + BM - 1) / BM);
   g.tiles_n = (int)((g.N + BN - 1) / BN);
   if (splits <= 1) {
     g.kps = g.K > 0 ? g.K : 1;
     g.sZ = 0;
-    return launch_tiles<BM, BN, BK, WM, WN, NBUF>(g, batch, ta, tb, 1);
+    return launch_tiles<BM, BN, BK, WM, WN, NBUF, TRI>(g, batch, ta, tb, 1);
   }
   // Split K: partial products go to a scratch buffer (bias off), then one
   // pass adds them in split order and applies the bias.
@@ -421,7 +425,7 @@ int launch_cfg(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits = 1) {
   p.sZ = n;
   p.kps = kps;
   p.bias_mode = 0;
-  int rc = launch_tiles<BM, BN, BK, WM, WN, NBUF>(p, batch, ta, tb, splits);
+  int rc = launch_tiles<BM, BN, BK, WM, WN, NBUF, TRI>(p, batch, ta, tb, splits);
   if (rc == WXX_OK) {
     hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3(wxx::grid_1d(n, 256, 8192)), dim3(256), 0,
                        wxx::stream(), g, (const float*)part, splits, batch);
@@ -432,22 +436,22 @@ int launch_cfg(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits = 1) {
   return rc;
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int NBUF>
+template <int BM, int BN, int BK, int WM, int WN, int NBUF, bool TRI>
 int launch_tiles(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits) {
   g.nbatch = batch;
   dim3 grid((unsigned)((int64_t)g.tiles_m * g.tiles_n * batch), 1, (unsigned)splits);
   hipStream_t s = wxx::stream();
   if (!ta && !tb)
-    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, false, NBUF>), grid,
+    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, false, NBUF, TRI>), grid,
                        dim3(256), 0, s, g);
   else if (!ta && tb)
-    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, true, NBUF>), grid,
+    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, true, NBUF, TRI>), grid,
                        dim3(256), 0, s, g);
   else if (ta && !tb)
-    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, false, NBUF>), grid,
+    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, false, NBUF, TRI>), grid,
                        dim3(256), 0, s, g);
   else
-    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, true, NBUF>), grid,
+    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, true, NBUF, TRI>), grid,
                        dim3(256), 0, s, g);
   WXX_LAUNCHED();
   return WXX_OK;
@@ -585,7 +589,14 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
     }
     splits = std::max(1, std::min(splits, 32));
   }
-  if (tri) splits = 1;  // the triangular K ranges are per row tile
+  if (tri) {
+    // triangular modes: one K range per row tile (no split), on the tile
+    // shapes that carry the triangular code
+    const int t = (g.N <= 64 && g.M >= 128) ? (transpose_A ? 10 : 9) : 1;
+    if (t == 1) return launch_cfg<64, 64, 16, 32, 32, 2, true>(g, nb, transpose_A, transpose_B, 1);
+    if (t == 9) return launch_cfg<128, 64, 16, 64, 32, 2, true>(g, nb, transpose_A, transpose_B, 1);
+    return launch_cfg<128, 64, 32, 64, 32, 1, true>(g, nb, transpose_A, transpose_B, 1);
+  }
   switch (tile) {
     case 1: return launch_cfg<64, 64, 16, 32, 32>(g, nb, transpose_A, transpose_B, splits);
     case 2: return launch_cfg<128, 128, 16, 64, 64>(g, nb, transpose_A, transpose_B, splits);
