@@ -90,6 +90,25 @@ class Tensor:
         self.creator = None
         self.grad = None
 
+    @classmethod
+    def _wrap(cls, shape, buffer, dtype="f32", requires_grad=False):
+        """A contiguous tensor over ``buffer`` for an op's output, skipping the
+        argument validation of ``__init__`` (``shape`` is a list of ints the
+        op has already checked); the same attributes as ``__init__``."""
+        t = cls.__new__(cls)
+        t.shape = shape
+        t.offset = 0
+        t._base = None
+        t.type = dtype
+        t.stride = validation.contiguous_strides(shape)
+        t.nbytes = validation.numel(shape) * (8 if dtype == "c64" else 4)
+        t.data = None
+        t.buffer = buffer
+        t.requires_grad = requires_grad
+        t.creator = None
+        t.grad = None
+        return t
+
     # ------------------------------------------------------------------
     # Layout
     # ------------------------------------------------------------------

@@ -16,10 +16,12 @@ call = _lib.call
 
 def empty(shape, dtype="f32", requires_grad=False, label=None):
     """A new uninitialised tensor of ``shape`` (device memory from the cache)."""
-    shape = list(shape)
+    shape = [int(s) for s in shape]
+    if dtype not in ("f32", "u32", "c64") or any(s < 0 for s in shape):
+        return Tensor(shape, None, requires_grad=requires_grad, dtype=dtype)  # raises
     item = 8 if dtype == "c64" else 4
     buf = buffer_pool.create_buffer(validation.numel(shape) * item, label=label or "op output")
-    return Tensor(shape, buf, requires_grad=requires_grad, dtype=dtype)
+    return Tensor._wrap(shape, buf, dtype, requires_grad)
 
 
 def ptr(t):
