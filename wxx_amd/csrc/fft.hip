@@ -347,12 +347,19 @@ __global__ __launch_bounds__(Geo<LOGM>::NT) void irfft_kernel(const float2* __re
 // pass twiddle are loaded once per workgroup and the other powers are formed
 // by at most four complex products.  The rfft untangling step handles bins
 // k and M - k together (one LDS pair read per two output bins).
+// Points per thread of the persistent kernels for a row of 2^logm complex
+// points: 16 up to 2^13 points (128 VGPRs, so a CU holds as many rows as its
+// LDS does, with 4 waves per SIMD to overlap HBM and VALU work), 32 above
+// (radix up to 32; 16 points would spill at 2^14).
+constexpr int big_ept(int logm) { return logm <= 13 ? 16 : 32; }
+
 template <int LOGM>
 struct Big {
   static constexpr int M = 1 << LOGM;
-  static constexpr int E = 32;
+  static constexpr int E = big_ept(LOGM);
+  static constexpr int LE = E == 16 ? 4 : 5;  // log2(E): the largest pass radix
   static constexpr int T = M / E;
-  static constexpr int NP = (LOGM + 4) / 5;
+  static constexpr int NP = (LOGM + LE - 1) / LE;
   static constexpr int PM = M + (M >> 5);  // one pad slot per 32 points
   __host__ __device__ static constexpr int bits(int p) {
     return LOGM / NP + (p < LOGM % NP ? 1 : 0);
@@ -377,6 +384,9 @@ struct Big {
   }
   static constexpr int NTB = tbo(NP) > 0 ? tbo(NP) : 1;
   static constexpr int MIN_BLOCKS = (160 * 1024) / (PM * 8) < 1 ? 1 : (160 * 1024) / (PM * 8);
+  // __launch_bounds__'s second argument is waves per SIMD: MIN_BLOCKS
+  // resident workgroups of T / 64 waves over the CU's 4 SIMDs
+  static constexpr int MIN_WAVES = MIN_BLOCKS * (T / 64) / 4 < 1 ? 1 : MIN_BLOCKS * (T / 64) / 4;
 };
 
 __device__ __forceinline__ int bpad(int i) { return i + (i >> 5); }
@@ -549,7 +559,7 @@ __device__ __forceinline__ void rfft_big_load(float2* v, const float* __restrict
 }
 
 template <int LOGM, bool VEC>
-__global__ __launch_bounds__(Big<LOGM>::T, Big<LOGM>::MIN_BLOCKS) void rfft_big_kernel(
+__global__ __launch_bounds__(Big<LOGM>::T, Big<LOGM>::MIN_WAVES) void rfft_big_kernel(
     const float* __restrict__ x, float2* __restrict__ X, const float2* __restrict__ tw,
     int64_t rows, int64_t in_len) {
   using G = Big<LOGM>;
@@ -613,7 +623,7 @@ __device__ __forceinline__ void irfft_big_load(float2* a, const float2* __restri
 }
 
 template <int LOGM, int CROP>
-__global__ __launch_bounds__(Big<LOGM>::T, Big<LOGM>::MIN_BLOCKS) void irfft_big_kernel(
+__global__ __launch_bounds__(Big<LOGM>::T, Big<LOGM>::MIN_WAVES) void irfft_big_kernel(
     const float2* __restrict__ X, float* __restrict__ x, const float2* __restrict__ tw,
     int64_t rows, int64_t in_len, RowOut ro) {
   using G = Big<LOGM>;
