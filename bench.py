@@ -351,7 +351,7 @@ def main():
                       "launches on the library stream) / R",
         },
         "roofline": {
-            "kernel": "gemm_f32_mfma_kernel<128,128,32,64,64,false,false,1,false> (4096x4096x4096)",
+            "kernel": "gemm_f32_dtl_kernel<false,false> (4096x4096x4096)",
             "bound": "mfma",
             "achieved": dom["tflops"],
             "peak": PEAK_FP32_TFLOPS,

@@ -66,7 +66,9 @@ int wxx_timer_elapsed(int start, int stop, float* ms);
 /* ---- A: GEMM — functional.matmul_add (functional/utils.py:378-499) +
  *      shaders/matmul.wgsl.  sA/sB = batch strides (0 = unbatched);
  *      bias_mode 0 none, 1 (N,), 2 (M,N), 3 (batch,M,N); tile 0 = auto, else a
- *      tile code (1-10) plus 256 x the number of K splits. ---- */
+ *      tile code (1-11) plus 256 x the number of K splits; tile 11 (operand
+ *      tiles loaded straight into LDS) needs M, N multiples of 128, K a
+ *      multiple of 32 and 16-byte aligned operands, else the call fails. ---- */
 int wxx_matmul_add(const float* A, const float* B, const float* bias, float* C, int64_t M,
                    int64_t N, int64_t K, int64_t batch, int64_t sA, int64_t sB, int64_t sBias,
                    int bias_mode, int transpose_A, int transpose_B, int tile);

@@ -114,6 +114,15 @@ inline T __shfl_xor(T v, int off, int width = 64) {
 // Wave-uniform value: every lane of the emulated wave already holds it.
 inline int __builtin_amdgcn_readfirstlane(int v) { return v; }
 
+// global_load_lds: lane L's `size` bytes from src land at lds + offset +
+// size * L (lds is wave-uniform).  The copy is done at once, so the wait
+// for it is a no-op.
+inline void __builtin_amdgcn_global_load_lds(const void* src, void* lds, unsigned size, int offset,
+                                             int) {
+  std::memcpy(static_cast<char*>(lds) + offset + (size_t)size * wxx_emu::lane(), src, size);
+}
+inline void __builtin_amdgcn_s_waitcnt(int) {}
+
 inline float __int_as_float(int v) { float f; std::memcpy(&f, &v, 4); return f; }
 inline float __uint_as_float(uint32_t v) { float f; std::memcpy(&f, &v, 4); return f; }
 inline int __float_as_int(float f) { int v; std::memcpy(&v, &f, 4); return v; }

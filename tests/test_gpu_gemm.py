@@ -154,6 +154,46 @@ def test_matmul_every_tile_code(device, code, splits, ta, tb):
         assert_close(out.numpy(), og.matmul_add(A, B, bias, ta, tb), **tol(K))
 
 
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("batch,M,N,K,splits,bias_mode", [
+    (1, 128, 256, 96, 1, 1),
+    (2, 256, 128, 160, 3, 3),  # batched operands; K splits of 64, 64 and 32; per-batch bias
+    (3, 128, 128, 64, 1, 2),   # one (M, N) bias for every batch
+])
+def test_matmul_direct_to_lds(device, ta, tb, batch, M, N, K, splits, bias_mode):
+    # tile 11: operand tiles loaded straight into LDS in swizzled layouts;
+    # only for M, N multiples of 128 and whole 32-deep K chunks
+    import ctypes as C
+
+    from wxx_amd.backend import lib
+    from wxx_amd.functional._common import empty
+
+    r = rng(M + N + K + batch)
+    A = r.standard_normal((batch, K, M) if ta else (batch, M, K)).astype(np.float32)
+    B = r.standard_normal((batch, N, K) if tb else (batch, K, N)).astype(np.float32)
+    bias = r.standard_normal({1: (N,), 2: (M, N), 3: (batch, M, N)}[bias_mode]).astype(np.float32)
+    tA, tB, tbias = up(A), up(B), up(bias)
+    out = empty([batch, M, N])
+    P = C.c_void_p
+    lib.call("wxx_matmul_add", P(tA.data_ptr()), P(tB.data_ptr()), P(tbias.data_ptr()),
+             P(out.data_ptr()), M, N, K, batch, M * K, K * N, M * N if bias_mode == 3 else 0,
+             bias_mode, int(ta), int(tb), 11 + 256 * splits)
+    assert_close(out.numpy(), og.matmul_add(A, B, bias, ta, tb), **tol(K))
+
+
+def test_matmul_direct_to_lds_rejects_edge_tiles(device):
+    import ctypes as C
+
+    from wxx_amd.backend import lib
+    from wxx_amd.functional._common import empty
+
+    A, B, out = up(np.ones((130, 64), np.float32)), up(np.ones((64, 128), np.float32)), empty([130, 128])
+    P = C.c_void_p
+    with pytest.raises(lib.HIPError, match="tile 11"):
+        lib.call("wxx_matmul_add", P(A.data_ptr()), P(B.data_ptr()), None, P(out.data_ptr()),
+                 130, 128, 64, 1, 0, 0, 0, 0, 0, 0, 11)
+
+
 @pytest.mark.parametrize("S,d", [(64, 64), (130, 64), (256, 32), (1024, 64)])
 def test_matmul_tri_modes(device, S, d):
     # causal-attention products with their zero triangle skipped

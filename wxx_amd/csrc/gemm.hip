@@ -79,6 +79,67 @@ struct GemmCfg {
   static_assert(PA >= 1 && PB >= 1, "tile too small for 256 threads");
 };
 
+// Output tile of this workgroup.  blockIdx.x runs over (batch, tile) pairs.
+// Workgroups are dealt to the 8 XCDs round-robin by id, so id -> (id % 8) *
+// (total / 8) + id / 8 gives each XCD a contiguous run of pairs: all tiles of
+// a batch (which share that batch's operands) and neighbouring tiles of one
+// GEMM hit one L2.  Within a batch, tiles are walked in GROUP_M row groups.
+struct TileId {
+  int64_t batch;
+  int tile_m, tile_n;
+};
+__device__ __forceinline__ TileId tile_id(const GemmArgs& g) {
+  const int ntiles = g.tiles_m * g.tiles_n;
+  const int64_t total = (int64_t)ntiles * g.nbatch;
+  int64_t lin = blockIdx.x;
+  if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
+  TileId t;
+  t.batch = lin / ntiles;
+  const int bid = (int)(lin - t.batch * ntiles);
+  const int group_size = kGroupM * g.tiles_n;
+  const int group = bid / group_size;
+  const int first_m = group * kGroupM;
+  const int gm = min(g.tiles_m - first_m, kGroupM);
+  t.tile_m = first_m + (bid % group_size) % gm;
+  t.tile_n = (bid % group_size) / gm;
+  return t;
+}
+
+// Writes a wave's TM x TN 32x32 MFMA accumulators (rows from row0, columns
+// from col0) with the bias; rows and columns outside M x N are skipped.
+// D[i][j] of a 32x32 tile sits in lane j + 32*((i/4)%2), register
+// (i%4) + 4*(i/8).
+template <int TM, int TN>
+__device__ __forceinline__ void store_acc(const GemmArgs& g, float* __restrict__ C,
+                                          const floatx16 (&acc)[TM][TN], int64_t row0,
+                                          int64_t col0, int l32, int half, int64_t batch) {
+  const float* __restrict__ bias = g.bias;
+#pragma unroll
+  for (int a = 0; a < TM; ++a) {
+#pragma unroll
+    for (int b = 0; b < TN; ++b) {
+      const int64_t col = col0 + 32 * b + l32;
+      if (col >= g.N) continue;
+      float bias1 = 0.f;
+      if (g.bias_mode == 1) bias1 = bias[col];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = row0 + 32 * a + 8 * (r >> 2) + 4 * half + (r & 3);
+        if (row < g.M) {
+          float v = acc[a][b][r];
+          if (g.bias_mode == 1)
+            v += bias1;
+          else if (g.bias_mode == 2)
+            v += bias[(row % g.bias_rows) * g.N + col];
+          else if (g.bias_mode == 3)
+            v += bias[batch * g.sBias + row * g.N + col];
+          C[row * g.ldc + col] = v;
+        }
+      }
+    }
+  }
+}
+
 // NBUF = 2: double-buffered LDS tiles, one barrier per K chunk; NBUF = 1: one
 // LDS tile (half the LDS, so more workgroups per CU), two barriers per chunk.
 // TRI: the triangular (causal attention) modes are compiled in; the plain
@@ -99,23 +160,9 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
   const int wm = wave / Cfg::kWavesN;
   const int wn = wave % Cfg::kWavesN;
 
-  // ---- tile id: XCD-contiguous remap, then GROUP_M swizzle -------------
-  // blockIdx.x runs over (batch, tile) pairs.  Workgroups are dealt to the 8
-  // XCDs round-robin by id, so id -> (id % 8) * (total / 8) + id / 8 gives
-  // each XCD a contiguous run of pairs: all tiles of a batch (which share
-  // that batch's operands) and neighbouring tiles of one GEMM hit one L2.
-  const int ntiles = g.tiles_m * g.tiles_n;
-  const int64_t total = (int64_t)ntiles * g.nbatch;
-  int64_t lin = blockIdx.x;
-  if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
-  const int64_t batch = lin / ntiles;
-  const int bid = (int)(lin - batch * ntiles);
-  const int group_size = kGroupM * g.tiles_n;
-  const int group = bid / group_size;
-  const int first_m = group * kGroupM;
-  const int gm = min(g.tiles_m - first_m, kGroupM);
-  const int tile_m = first_m + (bid % group_size) % gm;
-  const int tile_n = (bid % group_size) / gm;
+  const TileId tid_ = tile_id(g);
+  const int64_t batch = tid_.batch;
+  const int tile_m = tid_.tile_m, tile_n = tid_.tile_n;
 
   const float* __restrict__ A = g.A + batch * g.sA;
   const float* __restrict__ B = g.B + batch * g.sB;
@@ -347,36 +394,158 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
   else
     main_loop(std::integral_constant<int, 0>{});
 
-  // ---- epilogue: D[i][j] of a 32x32 tile sits in lane j + 32*((i/4)%2),
-  //      register (i%4) + 4*(i/8) --------------------------------------------
-  const float* __restrict__ bias = g.bias;
+  store_acc<TM, TN>(g, C, acc, m0 + wm * WM, n0 + wn * WN, l32, half, batch);
+}
+
+// ---- direct-to-LDS variant: 128 x 128 tiles, 32-deep K chunks ------------
+// For launches whose tiles are all interior (M and N multiples of 128, every
+// K range a multiple of 32, operands float4-aligned).  Each chunk's operand
+// tiles go from global memory straight into LDS (global_load_lds_dwordx4:
+// one wave instruction fills 1 KiB, lane L's 16 bytes at byte 16 L), so no
+// registers stage them and no ds_write runs; two LDS buffers (separate
+// objects, so the compiler can tell the loads into one from the reads of the
+// other), one barrier per chunk.  Which global quad a lane fetches sets the
+// LDS layout:
+//  * k-contiguous operand (A when !TA, B when TB): row x of the tile holds
+//    its 32 k as 8 quads, quad q in slot q ^ ((x >> 1) & 7), so the 16 lanes
+//    of a ds_read_b128 phase (16 rows, one quad each) hit distinct banks;
+//  * m/n-contiguous operand (A when TA, B when !TB): row k holds the tile's
+//    128 m (n) in order.
+// Step s = 4t + r of a chunk feeds the MFMA's K lanes k = 8t + r (lanes
+// 0-31) and k = 8t + 4 + r (lanes 32-63), so a k-contiguous fragment is one
+// ds_read_b128 per 4 steps.
+template <bool TA, bool TB>
+__global__ __launch_bounds__(256, 2) void gemm_f32_dtl_kernel(GemmArgs g) {
+  constexpr int BM = 128, BN = 128, BK = 32, WM = 64, WN = 64, TM = 2, TN = 2;
+  constexpr int TILE = BM * BK;  // floats per operand tile (BM == BN)
+  __shared__ __attribute__((aligned(16))) float As0[TILE];
+  __shared__ __attribute__((aligned(16))) float As1[TILE];
+  __shared__ __attribute__((aligned(16))) float Bs0[TILE];
+  __shared__ __attribute__((aligned(16))) float Bs1[TILE];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;  // 2 x 2 waves of 64 x 64
+  const int half = lane >> 5, l32 = lane & 31;
+
+  const TileId tid_ = tile_id(g);
+  const int64_t batch = tid_.batch;
+  const int64_t m0 = (int64_t)tid_.tile_m * BM, n0 = (int64_t)tid_.tile_n * BN;
+  const float* __restrict__ A = g.A + batch * g.sA;
+  const float* __restrict__ B = g.B + batch * g.sB;
+  float* __restrict__ C = g.C + batch * g.sC + (int64_t)blockIdx.z * g.sZ;
+  const int64_t kbeg = (int64_t)blockIdx.z * g.kps;
+  const int64_t nk = (min(g.K, kbeg + g.kps) - kbeg) / BK;
+
+  // The lane's global source for each of the wave's 4 instructions per
+  // operand tile (instruction j fills the tile's 1 KiB region R = 4 wave + j)
+  // at the first chunk, and the advance per chunk.
+  const float* pa[4];
+  const float* pb[4];
 #pragma unroll
-  for (int a = 0; a < TM; ++a) {
+  for (int j = 0; j < 4; ++j) {
+    const int R = 4 * wave + j;
+    const int r = 8 * R + (lane >> 3);                // k-contiguous: tile row
+    const int q = (lane & 7) ^ ((r >> 1) & 7);        // logical quad of slot lane & 7
+    const int kr = 2 * R + (lane >> 5);               // m/n-contiguous: k row
+    pa[j] = TA ? A + (kbeg + kr) * g.lda + m0 + 4 * (lane & 31)
+               : A + (m0 + r) * g.lda + kbeg + 4 * q;
+    pb[j] = TB ? B + (n0 + r) * g.ldb + kbeg + 4 * q
+               : B + (kbeg + kr) * g.ldb + n0 + 4 * (lane & 31);
+  }
+  const int64_t a_step = TA ? BK * g.lda : BK;
+  const int64_t b_step = TB ? BK : BK * g.ldb;
+
+  auto issue = [&](int64_t kc, auto buf_tag) {
+    float* as = decltype(buf_tag)::value ? As1 : As0;
+    float* bs = decltype(buf_tag)::value ? Bs1 : Bs0;
 #pragma unroll
-    for (int b = 0; b < TN; ++b) {
-      const int64_t col = n0 + wn * WN + 32 * b + l32;
-      if (col >= N) continue;
-      float bias1 = 0.f;
-      if (g.bias_mode == 1) bias1 = bias[col];
+    for (int j = 0; j < 4; ++j) {
+      __builtin_amdgcn_global_load_lds(pa[j] + kc * a_step, as + (4 * wave + j) * 256, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(pb[j] + kc * b_step, bs + (4 * wave + j) * 256, 16, 0, 0);
+    }
+  };
+
+  // fragment addresses (floats): k-contiguous row x = w * 64 + l32 (+ 32 a)
+  // reads logical quad 2t + half, i.e. slot (2t + half) ^ ((l32 >> 1) & 7);
+  // m/n-contiguous reads (k, y) at k * 128 + y with k = 8t + 4 half + r.
+  const int sw = (l32 >> 1) & 7;
+  int qoff[4];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * WM + 32 * a + 8 * (r >> 2) + 4 * half + (r & 3);
-        if (row < M) {
-          float v = acc[a][b][r];
-          if (g.bias_mode == 1)
-            v += bias1;
-          else if (g.bias_mode == 2)
-            v += bias[(row % g.bias_rows) * N + col];
-          else if (g.bias_mode == 3)
-            v += bias[batch * g.sBias + row * N + col];
-          C[row * g.ldc + col] = v;
+  for (int t = 0; t < 4; ++t) qoff[t] = 4 * (((2 * t) ^ (sw & 6)) | ((half ^ sw) & 1));
+  const int xa = (wm * WM + l32) * BK, xb = (wn * WN + l32) * BK;
+  const int ya = 4 * half * BM + wm * WM + l32, yb = 4 * half * BN + wn * WN + l32;
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int b = 0; b < TN; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+
+  auto compute = [&](auto buf_tag) {
+    const float* as = decltype(buf_tag)::value ? As1 : As0;
+    const float* bs = decltype(buf_tag)::value ? Bs1 : Bs0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      float av[TM][4], bv[TN][4];
+#pragma unroll
+      for (int a = 0; a < TM; ++a) {
+        if (!TA) {
+          const float4 v = *reinterpret_cast<const float4*>(&as[xa + 32 * BK * a + qoff[t]]);
+          av[a][0] = v.x, av[a][1] = v.y, av[a][2] = v.z, av[a][3] = v.w;
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) av[a][r] = as[(8 * t + r) * BM + ya + 32 * a];
         }
+      }
+#pragma unroll
+      for (int b = 0; b < TN; ++b) {
+        if (TB) {
+          const float4 v = *reinterpret_cast<const float4*>(&bs[xb + 32 * BK * b + qoff[t]]);
+          bv[b][0] = v.x, bv[b][1] = v.y, bv[b][2] = v.z, bv[b][3] = v.w;
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) bv[b][r] = bs[(8 * t + r) * BN + yb + 32 * b];
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+#pragma unroll
+          for (int b = 0; b < TN; ++b)
+            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a][r], bv[b][r], acc[a][b], 0, 0, 0);
+    }
+  };
+  // every wave's loads of a chunk have landed before the barrier that
+  // publishes it (0x0F70: s_waitcnt vmcnt(0), the other counters left alone)
+  auto landed = [&]() {
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+  };
+
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  if (nk > 0) {
+    issue(0, B0{});
+    landed();
+    for (int64_t kc = 0; kc < nk; kc += 2) {
+      if (kc + 1 < nk) issue(kc + 1, B1{});
+      compute(B0{});
+      landed();  // chunk kc + 1 is in buffer 1; every wave is done with buffer 0
+      if (kc + 1 < nk) {
+        if (kc + 2 < nk) issue(kc + 2, B0{});
+        compute(B1{});
+        landed();
       }
     }
   }
+  store_acc<TM, TN>(g, C, acc, m0 + wm * WM, n0 + wn * WN, l32, half, batch);
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int NBUF, bool TRI = false>
+template <int BM, int BN, int BK, int WM, int WN, int NBUF, bool TRI = false, bool DTL = false>
 int launch_tiles(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits);
 
 // Adds the split-K partials part[z][b][M][N] in split order (deterministic)
@@ -401,14 +570,15 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmArgs g,
   }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int NBUF = 2, bool TRI = false>
+template <int BM, int BN, int BK, int WM, int WN, int NBUF = 2, bool TRI = false,
+          bool DTL = false>
 int launch_cfg(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits = 1) {
   g.tiles_m = (int)((g.M + BM - 1) / BM);
   g.tiles_n = (int)((g.N + BN - 1) / BN);
   if (splits <= 1) {
     g.kps = g.K > 0 ? g.K : 1;
     g.sZ = 0;
-    return launch_tiles<BM, BN, BK, WM, WN, NBUF, TRI>(g, batch, ta, tb, 1);
+    return launch_tiles<BM, BN, BK, WM, WN, NBUF, TRI, DTL>(g, batch, ta, tb, 1);
   }
   // Split K: partial products go to a scratch buffer (bias off), then one
   // pass adds them in split order and applies the bias.
@@ -425,7 +595,7 @@ int launch_cfg(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits = 1) {
   p.sZ = n;
   p.kps = kps;
   p.bias_mode = 0;
-  int rc = launch_tiles<BM, BN, BK, WM, WN, NBUF, TRI>(p, batch, ta, tb, splits);
+  int rc = launch_tiles<BM, BN, BK, WM, WN, NBUF, TRI, DTL>(p, batch, ta, tb, splits);
   if (rc == WXX_OK) {
     hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3(wxx::grid_1d(n, 256, 8192)), dim3(256), 0,
                        wxx::stream(), g, (const float*)part, splits, batch);
@@ -436,11 +606,24 @@ int launch_cfg(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits = 1) {
   return rc;
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int NBUF, bool TRI>
+template <int BM, int BN, int BK, int WM, int WN, int NBUF, bool TRI, bool DTL>
 int launch_tiles(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits) {
   g.nbatch = batch;
   dim3 grid((unsigned)((int64_t)g.tiles_m * g.tiles_n * batch), 1, (unsigned)splits);
   hipStream_t s = wxx::stream();
+  if constexpr (DTL) {
+    static_assert(BM == 128 && BN == 128 && BK == 32, "direct-to-LDS tiles are 128 x 128 x 32");
+    if (!ta && !tb)
+      hipLaunchKernelGGL((gemm_f32_dtl_kernel<false, false>), grid, dim3(256), 0, s, g);
+    else if (!ta && tb)
+      hipLaunchKernelGGL((gemm_f32_dtl_kernel<false, true>), grid, dim3(256), 0, s, g);
+    else if (ta && !tb)
+      hipLaunchKernelGGL((gemm_f32_dtl_kernel<true, false>), grid, dim3(256), 0, s, g);
+    else
+      hipLaunchKernelGGL((gemm_f32_dtl_kernel<true, true>), grid, dim3(256), 0, s, g);
+    WXX_LAUNCHED();
+    return WXX_OK;
+  }
   if (!ta && !tb)
     hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, false, NBUF, TRI>), grid,
                        dim3(256), 0, s, g);
@@ -546,6 +729,9 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
   }
   g.vec_ok = (g.lda % 4 == 0) && (g.ldb % 4 == 0) && (g.sA % 4 == 0) && (g.sB % 4 == 0) &&
              al16(A) && al16(B);
+  // every tile interior and every K range whole chunks: the direct-to-LDS kernel applies
+  const bool dtl_ok = g.vec_ok && g.M % 128 == 0 && g.N % 128 == 0 && K > 0 && K % 32 == 0 &&
+                      tri == 0;
 
   if (K == 0) {
     // Empty contraction: C = bias (or 0).  Reuse the kernel with K = 0: the
@@ -557,7 +743,8 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
   splits = std::max(splits, 1);
   if (tile == 0) {
     // Measured on MI355X (fp32 GEMM shapes of GPT-2 small and BASELINE
-    // config 2): 128x128 tiles are the fastest once they cover the CUs
+    // config 2): the direct-to-LDS 128x128 tiles are the fastest wherever
+    // they apply and balance; otherwise 128x128 tiles once they cover the CUs
     // twice (128x64 below that when K is short);
     // the 32-deep single-buffered variant wins for long K; 64x64 tiles win
     // for thin operands (attention's N = 64 / K = 64 products) and when the
@@ -567,7 +754,28 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
     const int64_t t128 = ((g.M + 127) / 128) * ((g.N + 127) / 128) * nb;
     const int64_t t64 = ((g.M + 63) / 64) * ((g.N + 63) / 64) * nb;
     const int64_t kmax = std::max<int64_t>(g.K / 1024, 1);
-    if (g.M <= 64 || g.N <= 64 || g.K <= 128) {
+    // Direct-to-LDS 128 x 128 tiles when every tile is interior and the
+    // tiles, times at most 4 K splits of >= 512, keep the CUs evenly busy:
+    // s splits of t tiles give t*s units, of which a CU runs
+    // ceil(t*s / cus), so the balance is t*s / (ceil(t*s / cus) * cus); each
+    // split beyond the first costs about 3 % (the partials' extra pass).
+    // Below a balance of 0.8 the smaller tiles below do better.
+    const int64_t smax = dtl_ok ? std::min<int64_t>(4, std::max<int64_t>(g.K / 512, 1)) : 0;
+    double best = 0.0;
+    int best_splits = 1;
+    for (int64_t sp = 1; sp <= smax; ++sp) {
+      const int64_t units = t128 * sp;
+      const double bal = (double)units / (double)(((units + cus - 1) / cus) * cus) *
+                         (sp > 1 ? 0.97 : 1.0);
+      if (bal > best + 1e-9) {
+        best = bal;
+        best_splits = (int)sp;
+      }
+    }
+    if (dtl_ok && t128 * smax >= cus && best >= 0.8) {
+      tile = 11;
+      splits = best_splits;
+    } else if (g.M <= 64 || g.N <= 64 || g.K <= 128) {
       // N = 64 over long M (attention's P V, dS K, P^T dO): 128 x 64 tiles
       tile = (g.N <= 64 && g.M >= 128 && g.K > 128) ? (transpose_A ? 10 : 9) : 1;
       if (tile == 1 && t64 < 2 * cus)
@@ -609,6 +817,11 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
     case 8: return launch_cfg<128, 256, 16, 64, 128>(g, nb, transpose_A, transpose_B, splits);
     case 9: return launch_cfg<128, 64, 16, 64, 32>(g, nb, transpose_A, transpose_B, splits);
     case 10: return launch_cfg<128, 64, 32, 64, 32, 1>(g, nb, transpose_A, transpose_B, splits);
+    case 11:
+      WXX_REQUIRE(dtl_ok, "tile 11 needs M, N multiples of 128, K a multiple of 32 and "
+                  "16-byte aligned operands");
+      return launch_cfg<128, 128, 32, 64, 64, 2, false, true>(g, nb, transpose_A, transpose_B,
+                                                              splits);
     default: return wxx::set_error(WXX_E_ARG, "bad tile %d", tile);
   }
 }
