@@ -755,18 +755,20 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
     const int64_t t64 = ((g.M + 63) / 64) * ((g.N + 63) / 64) * nb;
     const int64_t kmax = std::max<int64_t>(g.K / 1024, 1);
     // Direct-to-LDS 128 x 128 tiles when every tile is interior and the
-    // tiles, times at most 4 K splits of >= 512, keep the CUs evenly busy:
+    // tiles, times at most 16 K splits of >= 512, keep the CUs evenly busy:
     // s splits of t tiles give t*s units, of which a CU runs
-    // ceil(t*s / cus), so the balance is t*s / (ceil(t*s / cus) * cus); each
-    // split beyond the first costs about 3 % (the partials' extra pass).
-    // Below a balance of 0.8 the smaller tiles below do better.
-    const int64_t smax = dtl_ok ? std::min<int64_t>(4, std::max<int64_t>(g.K / 512, 1)) : 0;
+    // ceil(t*s / cus), so the balance is t*s / (ceil(t*s / cus) * cus).  With
+    // s > 1 the partials' extra pass moves (s + 1) * M * N * 4 bytes at
+    // ~5 TB/s next to 2 * M * N * K flops at ~130 TFLOP/s, a relative cost of
+    // (s + 1) * 52 / K.  Below an efficiency of 0.8 the smaller tiles below
+    // do better.
+    const int64_t smax = dtl_ok ? std::min<int64_t>(16, std::max<int64_t>(g.K / 512, 1)) : 0;
     double best = 0.0;
     int best_splits = 1;
     for (int64_t sp = 1; sp <= smax; ++sp) {
       const int64_t units = t128 * sp;
-      const double bal = (double)units / (double)(((units + cus - 1) / cus) * cus) *
-                         (sp > 1 ? 0.97 : 1.0);
+      const double bal = (double)units / (double)(((units + cus - 1) / cus) * cus) /
+                         (sp > 1 ? 1.0 + (double)(sp + 1) * 52.0 / (double)g.K : 1.0);
       if (bal > best + 1e-9) {
         best = bal;
         best_splits = (int)sp;
