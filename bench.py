@@ -279,7 +279,7 @@ def main():
         if args.reps:
             return args.reps
         amount, kind = ks.work[name]
-        est_ms = amount / (80e9 if kind == "flop" else 4e6)  # rough 80 TF/s, 4 TB/s
+        est_ms = amount / (80e9 if kind == "flop" else 4e9)  # rough 80 TF/s, 4 TB/s, per ms
         return int(min(200, max(3, round(2.0 / max(est_ms, 1e-3)))))
 
     reps = {n: reps_for(n) for n in names}

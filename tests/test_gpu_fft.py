@@ -137,7 +137,8 @@ def test_fft_full_size_properties(device):
     assert_fft_close(two, 2 * Xh.astype(np.complex128))
 
 
-@pytest.mark.parametrize("rows,n", [(300, 4096), (3000, 4096), (1100, 8192), (600, 32768)])
+@pytest.mark.parametrize("rows,n", [(300, 4096), (3000, 4096), (1100, 8192), (1300, 16384),
+                                    (600, 32768)])
 def test_fft_many_rows_every_row(device, rows, n):
     # More rows than one pass of the resident workgroups holds, so every
     # workgroup walks several rows; every row is checked.
@@ -147,6 +148,20 @@ def test_fft_many_rows_every_row(device, rows, n):
     Xc = (rng(n).standard_normal((rows, n // 2 + 1))
           + 1j * rng(n + 1).standard_normal((rows, n // 2 + 1))).astype(np.complex64)
     assert_fft_close(F().irfft(upc(Xc), n).numpy(), of.irfft(Xc, n), f"irfft rows={rows} n={n}")
+
+
+@pytest.mark.parametrize("length", [8192, 8191])
+def test_irfft_crop_many_rows(device, length):
+    # 1300 rows leave every persistent n = 16384 workgroup 2 or 3 rows; each
+    # cropped row must equal the full transform's first `length` samples
+    n, rows = 16384, 1300
+    r = rng(length)
+    X = (r.standard_normal((rows, n // 2 + 1))
+         + 1j * r.standard_normal((rows, n // 2 + 1))).astype(np.complex64)
+    full = F().irfft(upc(X), n).numpy()
+    got = F().irfft(upc(X), n, length=length, scale=2.0).numpy()
+    np.testing.assert_allclose(got, 2.0 * full[:, :length], rtol=0,
+                               atol=2e-6 * np.abs(full).max())
 
 
 def test_hyena_shapes(device):

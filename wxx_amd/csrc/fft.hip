@@ -444,6 +444,22 @@ __device__ __forceinline__ float2 rot32(float2 v, int m) {
   return make_float2(v.x * c - v.y * s, v.x * s + v.y * c);
 }
 
+// W_{2M}^k of the untangling table at a lane-independent offset k (a multiple
+// of T, constant after unrolling).  With 16 points per thread T = M / 16, so
+// W_{2M}^k = exp(-i pi (k / T) / 16) comes from the rotation constants instead
+// of a global load: the persistent kernels keep a row prefetch in flight
+// across the untangle, and an in-order vmcnt wait for a table load would wait
+// for that prefetch too.
+template <int E, int T>
+__device__ __forceinline__ float2 untangle_tw(const float2* __restrict__ wu, int k) {
+  if constexpr (E == 16) {
+    const int m = k / T;
+    return make_float2(kCosPi16[m & 31], -kCosPi16[(m + 24) & 31]);
+  } else {
+    return wu[k];
+  }
+}
+
 // In-register radix-2 decimation-in-frequency DFT of R <= 32 points; output
 // in bit-reversed order.
 template <int R, bool INV>
@@ -570,18 +586,36 @@ __global__ __launch_bounds__(Big<LOGM>::T, Big<LOGM>::MIN_WAVES) void rfft_big_k
   const float2 wt = wu[threadIdx.x];  // W_{2M}^t
 
   float2 v[G::E];
+  const bool full = in_len >= 2 * G::M;
+  if ((int64_t)blockIdx.x < rows) {
+    if (full)
+      rfft_big_load<LOGM, VEC, true>(v, x + blockIdx.x * in_len, threadIdx.x, in_len);
+    else
+      rfft_big_load<LOGM, VEC, false>(v, x + blockIdx.x * in_len, threadIdx.x, in_len);
+  }
   for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
     // Hide the lane index from loop-invariant code motion: every LDS address
     // below is a function of t, and hoisting them all out of the row loop
     // would hold ~200 VGPRs; recomputed per row they fold into base + offset.
     int t = threadIdx.x;
     WXX_OPAQUE(t);
-    if (in_len >= 2 * G::M)
-      rfft_big_load<LOGM, VEC, true>(v, x + row * in_len, t, in_len);
-    else
-      rfft_big_load<LOGM, VEC, false>(v, x + row * in_len, t, in_len);
     big_passes<LOGM, 0, false, false, true>(v, buf, t, twb, RowOut{}, nullptr);
-    // untangle: bins k and M - k from Z[k], Z[M - k]
+    // The transform is in LDS and v is free: start loading this workgroup's
+    // next row now, so its HBM latency overlaps the untangle and the stores
+    // below instead of following them.
+    const int64_t next = row + gridDim.x;
+    if (next < rows) {
+      if (full)
+        rfft_big_load<LOGM, VEC, true>(v, x + next * in_len, t, in_len);
+      else
+        rfft_big_load<LOGM, VEC, false>(v, x + next * in_len, t, in_len);
+    }
+    // untangle: bins k and M - k from Z[k], Z[M - k].  wt is hidden per row
+    // like t: its products with the constant twiddles are loop invariant, and
+    // hoisted they would hold 2 E VGPRs across the row loop.
+    float2 wtr = wt;
+    WXX_OPAQUE(wtr.x);
+    WXX_OPAQUE(wtr.y);
     float2* Xr = X + row * (G::M + 1);
     const int tb = bpad(t), nb = -t + ((-t) >> 5);  // bpad(t), and bpad(a - t) - bpad_c(a)
 #pragma unroll
@@ -592,7 +626,7 @@ __global__ __launch_bounds__(Big<LOGM>::T, Big<LOGM>::MIN_WAVES) void rfft_big_k
       const float2 b = buf[k == 0 ? 0 : nb + bpad_c(G::M - i * G::T)];  // bin (M - k) mod M
       const float2 e = make_float2(0.5f * (a.x + b.x), 0.5f * (a.y - b.y));
       const float2 o = make_float2(0.5f * (a.y + b.y), 0.5f * (b.x - a.x));
-      const float2 w = cmul(wt, wu[i * G::T]);
+      const float2 w = cmul(wtr, untangle_tw<G::E, G::T>(wu, i * G::T));
       const float2 wo = cmul(w, o);
       Xr[k] = make_float2(e.x + wo.x, e.y + wo.y);
       if (k != G::M / 2) Xr[G::M - k] = make_float2(e.x - wo.x, wo.y - e.y);
