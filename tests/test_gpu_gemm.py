@@ -72,7 +72,7 @@ def test_matmul_attention_shapes(device):
 
 
 @pytest.mark.parametrize("M,N,K", [(1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096),
-                                   (8192, 3072, 768), (8192, 768, 3072)])
+                                   (8192, 3072, 768), (8192, 768, 3072), (8192, 768, 768)])
 def test_matmul_config2_sizes(device, M, N, K):
     r = rng(10 + M % 7)
     A = r.standard_normal((M, K)).astype(np.float32)
@@ -154,20 +154,24 @@ def test_matmul_every_tile_code(device, code, splits, ta, tb):
         assert_close(out.numpy(), og.matmul_add(A, B, bias, ta, tb), **tol(K))
 
 
+@pytest.mark.parametrize("code", [11, 12])
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
 @pytest.mark.parametrize("batch,M,N,K,splits,bias_mode", [
     (1, 128, 256, 96, 1, 1),
     (2, 256, 128, 160, 3, 3),  # batched operands; K splits of 64, 64 and 32; per-batch bias
     (3, 128, 128, 64, 1, 2),   # one (M, N) bias for every batch
 ])
-def test_matmul_direct_to_lds(device, ta, tb, batch, M, N, K, splits, bias_mode):
-    # tile 11: operand tiles loaded straight into LDS in swizzled layouts;
-    # only for M, N multiples of 128 and whole 32-deep K chunks
+def test_matmul_direct_to_lds(device, code, ta, tb, batch, M, N, K, splits, bias_mode):
+    # tiles 11 / 12: 128 x 128 / 128 x 192 operand tiles loaded straight into
+    # LDS in swizzled layouts; only for M a multiple of 128, N of the tile
+    # width, and whole 32-deep K chunks (N scaled to 192 / 384 for tile 12)
     import ctypes as C
 
     from wxx_amd.backend import lib
     from wxx_amd.functional._common import empty
 
+    if code == 12:
+        N = N * 3 // 2
     r = rng(M + N + K + batch)
     A = r.standard_normal((batch, K, M) if ta else (batch, M, K)).astype(np.float32)
     B = r.standard_normal((batch, N, K) if tb else (batch, K, N)).astype(np.float32)
@@ -177,8 +181,30 @@ def test_matmul_direct_to_lds(device, ta, tb, batch, M, N, K, splits, bias_mode)
     P = C.c_void_p
     lib.call("wxx_matmul_add", P(tA.data_ptr()), P(tB.data_ptr()), P(tbias.data_ptr()),
              P(out.data_ptr()), M, N, K, batch, M * K, K * N, M * N if bias_mode == 3 else 0,
-             bias_mode, int(ta), int(tb), 11 + 256 * splits)
+             bias_mode, int(ta), int(tb), code + 256 * splits)
     assert_close(out.numpy(), og.matmul_add(A, B, bias, ta, tb), **tol(K))
+
+
+@pytest.mark.parametrize("K", [768, 3072])
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+def test_matmul_n768_every_transpose(device, ta, tb, K):
+    # GPT-2 small's 8192 x 768 outputs under the automatic tile choice: the
+    # q/k/v/out projections (K = 768) and the MLP's down projection and
+    # up-projection input gradient (K = 3072; 128 x 192 tiles when B is
+    # k-contiguous)
+    M, N = 8192, 768
+    r = rng(K + 2 * ta + tb)
+    A = r.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    B = r.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    bias = r.standard_normal(N).astype(np.float32)
+    got = F().matmul_add(up(A), up(B), up(bias), transpose_A=ta, transpose_B=tb).numpy()
+    Ad = (A.T if ta else A).astype(np.float64)
+    Bd = (B.T if tb else B).astype(np.float64)
+    rows = np.r_[0:8, 4092:4100, M - 8:M]
+    assert_close(got[rows], Ad[rows] @ Bd + bias, **tol(K))
+    ones = np.ones(N)
+    assert_close(got.astype(np.float64) @ ones, Ad @ (Bd @ ones) + bias.sum(),
+                 rtol=1e-4, atol=1e-3 * np.sqrt(K * N))
 
 
 def test_matmul_direct_to_lds_rejects_edge_tiles(device):
@@ -192,6 +218,10 @@ def test_matmul_direct_to_lds_rejects_edge_tiles(device):
     with pytest.raises(lib.HIPError, match="tile 11"):
         lib.call("wxx_matmul_add", P(A.data_ptr()), P(B.data_ptr()), None, P(out.data_ptr()),
                  130, 128, 64, 1, 0, 0, 0, 0, 0, 0, 11)
+    # tile 12 needs N a multiple of 192
+    with pytest.raises(lib.HIPError, match="tile 12"):
+        lib.call("wxx_matmul_add", P(A.data_ptr()), P(B.data_ptr()), None, P(out.data_ptr()),
+                 128, 128, 64, 1, 0, 0, 0, 0, 0, 0, 12)
 
 
 @pytest.mark.parametrize("S,d", [(64, 64), (130, 64), (256, 32), (1024, 64)])

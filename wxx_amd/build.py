@@ -60,7 +60,11 @@ def build(jobs=None, verbose=True):
     with _cf.ThreadPoolExecutor(max_workers=jobs) as pool:
         objs = list(pool.map(_compile, srcs))
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    # --no-undefined: a symbol the objects reference but none defines (e.g. a
+    # kernel launch stub the host pass did not emit) fails the build here
+    # rather than the library's load on a GPU host
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", "-o", tmp,
+           *objs]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")

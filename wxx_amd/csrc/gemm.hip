@@ -397,9 +397,9 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
   store_acc<TM, TN>(g, C, acc, m0 + wm * WM, n0 + wn * WN, l32, half, batch);
 }
 
-// ---- direct-to-LDS variant: 128 x 128 tiles, 32-deep K chunks ------------
-// For launches whose tiles are all interior (M and N multiples of 128, every
-// K range a multiple of 32, operands float4-aligned).  Each chunk's operand
+// ---- direct-to-LDS variant: 128 x BN tiles (BN 128 or 192), 32-deep K chunks
+// For launches whose tiles are all interior (M a multiple of 128, N of BN,
+// every K range a multiple of 32, operands float4-aligned).  Each chunk's operand
 // tiles go from global memory straight into LDS (global_load_lds_dwordx4:
 // one wave instruction fills 1 KiB, lane L's 16 bytes at byte 16 L), so no
 // registers stage them and no ds_write runs; two LDS buffers (separate
@@ -410,22 +410,28 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
 //    its 32 k as 8 quads, quad q in slot q ^ ((x >> 1) & 7), so the 16 lanes
 //    of a ds_read_b128 phase (16 rows, one quad each) hit distinct banks;
 //  * m/n-contiguous operand (A when TA, B when !TB): row k holds the tile's
-//    128 m (n) in order.
+//    128 m (BN n) in order; a region's 256 floats are the next 256 of that
+//    row-major k x BN tile, whichever rows they fall in.
+// BN = 192 serves outputs of N = 768 (GPT-2's d_model): 8192 x 768 is 256
+// tiles, one per CU, where 128 x 128 tiles would leave half the CUs a second
+// tile.  Its 80 KiB of LDS would let two workgroups share a CU, so it is
+// launched with 4 KiB of dynamic LDS more, which keeps one per CU.
 // Step s = 4t + r of a chunk feeds the MFMA's K lanes k = 8t + r (lanes
 // 0-31) and k = 8t + 4 + r (lanes 32-63), so a k-contiguous fragment is one
 // ds_read_b128 per 4 steps.
-template <bool TA, bool TB>
+template <bool TA, bool TB, int BN>
 __global__ __launch_bounds__(256, 2) void gemm_f32_dtl_kernel(GemmArgs g) {
-  constexpr int BM = 128, BN = 128, BK = 32, WM = 64, WN = 64, TM = 2, TN = 2;
-  constexpr int TILE = BM * BK;  // floats per operand tile (BM == BN)
-  __shared__ __attribute__((aligned(16))) float As0[TILE];
-  __shared__ __attribute__((aligned(16))) float As1[TILE];
-  __shared__ __attribute__((aligned(16))) float Bs0[TILE];
-  __shared__ __attribute__((aligned(16))) float Bs1[TILE];
+  static_assert(BN == 128 || BN == 192, "direct-to-LDS tiles are 128 x 128 or 128 x 192");
+  constexpr int BM = 128, BK = 32, WM = 64, WN = BN / 2, TM = 2, TN = WN / 32;
+  constexpr int RB = BN * BK / 256 / 4;  // 1 KiB regions of the B tile per wave
+  __shared__ __attribute__((aligned(16))) float As0[BM * BK];
+  __shared__ __attribute__((aligned(16))) float As1[BM * BK];
+  __shared__ __attribute__((aligned(16))) float Bs0[BN * BK];
+  __shared__ __attribute__((aligned(16))) float Bs1[BN * BK];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave >> 1, wn = wave & 1;  // 2 x 2 waves of 64 x 64
+  const int wm = wave >> 1, wn = wave & 1;  // 2 x 2 waves of 64 x WN
   const int half = lane >> 5, l32 = lane & 31;
 
   const TileId tid_ = tile_id(g);
@@ -437,21 +443,32 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_dtl_kernel(GemmArgs g) {
   const int64_t kbeg = (int64_t)blockIdx.z * g.kps;
   const int64_t nk = (min(g.K, kbeg + g.kps) - kbeg) / BK;
 
-  // The lane's global source for each of the wave's 4 instructions per
-  // operand tile (instruction j fills the tile's 1 KiB region R = 4 wave + j)
-  // at the first chunk, and the advance per chunk.
+  // The lane's global source for each of the wave's instructions per
+  // operand tile (instruction j fills the tile's 1 KiB region R = 4 wave + j
+  // of A, R = RB wave + j of B) at the first chunk, and the advance per chunk.
+  // pb has a fixed size (RB <= 6 entries used): with the template-dependent
+  // size RB, the host pass of this compiler silently emits no launch stub for
+  // the kernel, whose lambdas capture the array.
   const float* pa[4];
-  const float* pb[4];
+  const float* pb[6];
+  static_assert(RB <= 6, "B regions per wave");
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int R = 4 * wave + j;
     const int r = 8 * R + (lane >> 3);                // k-contiguous: tile row
     const int q = (lane & 7) ^ ((r >> 1) & 7);        // logical quad of slot lane & 7
-    const int kr = 2 * R + (lane >> 5);               // m/n-contiguous: k row
+    const int kr = 2 * R + (lane >> 5);               // m-contiguous: k row
     pa[j] = TA ? A + (kbeg + kr) * g.lda + m0 + 4 * (lane & 31)
                : A + (m0 + r) * g.lda + kbeg + 4 * q;
+  }
+#pragma unroll
+  for (int j = 0; j < RB; ++j) {
+    const int R = RB * wave + j;
+    const int r = 8 * R + (lane >> 3);
+    const int q = (lane & 7) ^ ((r >> 1) & 7);
+    const int f = 256 * R + 4 * lane;                 // n-contiguous: float f of the tile
     pb[j] = TB ? B + (n0 + r) * g.ldb + kbeg + 4 * q
-               : B + (kbeg + kr) * g.ldb + n0 + 4 * (lane & 31);
+               : B + (kbeg + f / BN) * g.ldb + n0 + f % BN;
   }
   const int64_t a_step = TA ? BK * g.lda : BK;
   const int64_t b_step = TB ? BK : BK * g.ldb;
@@ -460,10 +477,11 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_dtl_kernel(GemmArgs g) {
     float* as = decltype(buf_tag)::value ? As1 : As0;
     float* bs = decltype(buf_tag)::value ? Bs1 : Bs0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 4; ++j)
       __builtin_amdgcn_global_load_lds(pa[j] + kc * a_step, as + (4 * wave + j) * 256, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(pb[j] + kc * b_step, bs + (4 * wave + j) * 256, 16, 0, 0);
-    }
+#pragma unroll
+    for (int j = 0; j < RB; ++j)
+      __builtin_amdgcn_global_load_lds(pb[j] + kc * b_step, bs + (RB * wave + j) * 256, 16, 0, 0);
   };
 
   // fragment addresses (floats): k-contiguous row x = w * 64 + l32 (+ 32 a)
@@ -612,30 +630,33 @@ int launch_tiles(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits) {
   dim3 grid((unsigned)((int64_t)g.tiles_m * g.tiles_n * batch), 1, (unsigned)splits);
   hipStream_t s = wxx::stream();
   if constexpr (DTL) {
-    static_assert(BM == 128 && BN == 128 && BK == 32, "direct-to-LDS tiles are 128 x 128 x 32");
+    static_assert(BM == 128 && (BN == 128 || BN == 192) && BK == 32,
+                  "direct-to-LDS tiles are 128 x 128 x 32 or 128 x 192 x 32");
+    // 128 x 192: 4 KiB of dynamic LDS on top of the tiles' 80 KiB, so that
+    // one workgroup occupies a CU (the grids it is chosen for are <= 1 per CU)
+    const unsigned dyn = BN == 192 ? 4096u : 0u;
     if (!ta && !tb)
-      hipLaunchKernelGGL((gemm_f32_dtl_kernel<false, false>), grid, dim3(256), 0, s, g);
+      hipLaunchKernelGGL((gemm_f32_dtl_kernel<false, false, BN>), grid, dim3(256), dyn, s, g);
     else if (!ta && tb)
-      hipLaunchKernelGGL((gemm_f32_dtl_kernel<false, true>), grid, dim3(256), 0, s, g);
+      hipLaunchKernelGGL((gemm_f32_dtl_kernel<false, true, BN>), grid, dim3(256), dyn, s, g);
     else if (ta && !tb)
-      hipLaunchKernelGGL((gemm_f32_dtl_kernel<true, false>), grid, dim3(256), 0, s, g);
+      hipLaunchKernelGGL((gemm_f32_dtl_kernel<true, false, BN>), grid, dim3(256), dyn, s, g);
     else
-      hipLaunchKernelGGL((gemm_f32_dtl_kernel<true, true>), grid, dim3(256), 0, s, g);
-    WXX_LAUNCHED();
-    return WXX_OK;
+      hipLaunchKernelGGL((gemm_f32_dtl_kernel<true, true, BN>), grid, dim3(256), dyn, s, g);
+  } else {
+    if (!ta && !tb)
+      hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, false, NBUF, TRI>),
+                         grid, dim3(256), 0, s, g);
+    else if (!ta && tb)
+      hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, true, NBUF, TRI>),
+                         grid, dim3(256), 0, s, g);
+    else if (ta && !tb)
+      hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, false, NBUF, TRI>),
+                         grid, dim3(256), 0, s, g);
+    else
+      hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, true, NBUF, TRI>),
+                         grid, dim3(256), 0, s, g);
   }
-  if (!ta && !tb)
-    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, false, NBUF, TRI>), grid,
-                       dim3(256), 0, s, g);
-  else if (!ta && tb)
-    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, true, NBUF, TRI>), grid,
-                       dim3(256), 0, s, g);
-  else if (ta && !tb)
-    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, false, NBUF, TRI>), grid,
-                       dim3(256), 0, s, g);
-  else
-    hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, true, NBUF, TRI>), grid,
-                       dim3(256), 0, s, g);
   WXX_LAUNCHED();
   return WXX_OK;
 }
@@ -647,7 +668,8 @@ inline bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 // Replaces functional.matmul_add (reference src/wxx/functional/utils.py:378-499).
 // Strides are in elements; sA / sB == 0 marks an unbatched operand.
 // tile: 0 = choose automatically, 1 = 64x64, 2 = 128x128, 3 = 256x128; 4-10 select
-// alternative tile / K-chunk / buffering shapes of the same kernel.  With an
+// alternative tile / K-chunk / buffering shapes of the same kernel; 11 / 12 the
+// direct-to-LDS 128x128 / 128x192 kernel.  With an
 // explicit tile code, bits 8-15 give the number of K splits (0 or 1: none).
 namespace {
 int matmul_impl(const float* A, const float* B, const float* bias, float* C, int64_t M, int64_t N,
@@ -732,6 +754,8 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
   // every tile interior and every K range whole chunks: the direct-to-LDS kernel applies
   const bool dtl_ok = g.vec_ok && g.M % 128 == 0 && g.N % 128 == 0 && K > 0 && K % 32 == 0 &&
                       tri == 0;
+  const bool dtl192_ok = g.vec_ok && g.M % 128 == 0 && g.N % 192 == 0 && K > 0 && K % 32 == 0 &&
+                         tri == 0;
 
   if (K == 0) {
     // Empty contraction: C = bias (or 0).  Reuse the kernel with K = 0: the
@@ -774,7 +798,25 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
         best_splits = (int)sp;
       }
     }
-    if (dtl_ok && t128 * smax >= cus && best >= 0.8) {
+    // 128 x 192 direct-to-LDS tiles, unsplit, when they make one round of at
+    // most one tile per CU that balances better (8192 x 768: 256 tiles, where
+    // 128 x 128 makes 384, or needs split-K partials to balance), and only for
+    // the shapes where they measured faster on MI355X (GPT-2 small): a
+    // k-contiguous B (one ds_read_b128 per 4 MFMA steps; an n-contiguous B
+    // reads 4x as many LDS words singly) with K >= 2048 (8192x768x3072:
+    // 321 us against 388 us on two K splits), or K >= 16384, where the
+    // 128 x 128 alternative adds 16 splits' partials (8192x768x50304: 4.99
+    // against 5.19 ms).  At K = 768 the 128 x 64 tiles stay faster
+    // (100-101 us against 107-108 us), as do the split 128 x 128 tiles for
+    // an n-contiguous B at K = 3072 (318 us against 340 us).
+    const int64_t t192 = dtl192_ok && ((transpose_B && g.K >= 2048) || g.K >= 16384)
+                             ? (g.M / 128) * (g.N / 192) * nb
+                             : 0;
+    const double bal192 = (double)t192 / (double)cus;
+    if (t192 > 0 && t192 <= cus && bal192 >= 0.9 && bal192 > best) {
+      tile = 12;
+      splits = 1;
+    } else if (dtl_ok && t128 * smax >= cus && best >= 0.8) {
       tile = 11;
       splits = best_splits;
     } else if (g.M <= 64 || g.N <= 64 || g.K <= 128) {
@@ -823,6 +865,11 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
       WXX_REQUIRE(dtl_ok, "tile 11 needs M, N multiples of 128, K a multiple of 32 and "
                   "16-byte aligned operands");
       return launch_cfg<128, 128, 32, 64, 64, 2, false, true>(g, nb, transpose_A, transpose_B,
+                                                              splits);
+    case 12:
+      WXX_REQUIRE(dtl192_ok, "tile 12 needs M a multiple of 128, N of 192, K of 32 and "
+                  "16-byte aligned operands");
+      return launch_cfg<128, 192, 32, 64, 96, 2, false, true>(g, nb, transpose_A, transpose_B,
                                                               splits);
     default: return wxx::set_error(WXX_E_ARG, "bad tile %d", tile);
   }
