@@ -224,9 +224,12 @@ def test_matmul_direct_to_lds_rejects_edge_tiles(device):
                  128, 128, 64, 1, 0, 0, 0, 0, 0, 0, 12)
 
 
-@pytest.mark.parametrize("S,d", [(64, 64), (130, 64), (256, 32), (1024, 64)])
+@pytest.mark.parametrize("S,d", [(64, 64), (130, 64), (256, 32), (300, 64), (640, 64),
+                                 (1024, 64)])
 def test_matmul_tri_modes(device, S, d):
-    # causal-attention products with their zero triangle skipped
+    # causal-attention products with their zero triangle skipped; in modes 2
+    # and 3 a workgroup runs row tiles p and T - 1 - p of the T row tiles
+    # (S = 300 and 640: an odd T, whose middle tile runs alone)
     b = 3
     r = rng(S + d)
     q = r.standard_normal((b, S, d)).astype(np.float32)

@@ -58,6 +58,11 @@ struct GemmArgs {
   // triangular (a transposed lower-triangular matrix), so K starts at m0;
   // 4 as 1 but the tiles above the diagonal are not written at all.
   int tri;
+  // Modes 2 and 3 give row tile m a K range of m + 1 (mode 2) or T - m (mode
+  // 3) of the T row tiles' chunks, so when pair_m = T > 0 the grid covers
+  // pairs of row tiles and the workgroup of pair p runs tiles p and T - 1 - p:
+  // every workgroup then has the same T + 1 chunks of work.
+  int pair_m;
 };
 
 constexpr int kGroupM = 8;
@@ -144,8 +149,10 @@ __device__ __forceinline__ void store_acc(const GemmArgs& g, float* __restrict__
 // LDS tile (half the LDS, so more workgroups per CU), two barriers per chunk.
 // TRI: the triangular (causal attention) modes are compiled in; the plain
 // instantiations carry none of their code.
-template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, int NBUF, bool TRI = false>
-__global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
+// One output tile of gemm_f32_mfma_kernel (the workgroup's, or each of its
+// pair of row tiles in the paired triangular modes).
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, int NBUF, bool TRI>
+__device__ __forceinline__ void gemm_mfma_tile(const GemmArgs& g, const TileId tid_) {
   using Cfg = GemmCfg<BM, BN, BK, WM, WN, TA, TB>;
   constexpr int TM = Cfg::TM, TN = Cfg::TN;
   constexpr int LDA_S = Cfg::LDA_S, LDB_S = Cfg::LDB_S;
@@ -160,7 +167,6 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
   const int wm = wave / Cfg::kWavesN;
   const int wn = wave % Cfg::kWavesN;
 
-  const TileId tid_ = tile_id(g);
   const int64_t batch = tid_.batch;
   const int tile_m = tid_.tile_m, tile_n = tid_.tile_n;
 
@@ -397,6 +403,25 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
   store_acc<TM, TN>(g, C, acc, m0 + wm * WM, n0 + wn * WN, l32, half, batch);
 }
 
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, int NBUF, bool TRI = false>
+__global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
+  TileId t = tile_id(g);
+  if constexpr (TRI) {
+    if (g.pair_m > 0) {
+      // tile_id ran over pairs: row tiles t.tile_m and pair_m - 1 - t.tile_m
+      const int partner = g.pair_m - 1 - t.tile_m;
+      gemm_mfma_tile<BM, BN, BK, WM, WN, TA, TB, NBUF, TRI>(g, t);
+      if (partner != t.tile_m) {
+        __syncthreads();  // every wave is done with the LDS tiles
+        t.tile_m = partner;
+        gemm_mfma_tile<BM, BN, BK, WM, WN, TA, TB, NBUF, TRI>(g, t);
+      }
+      return;
+    }
+  }
+  gemm_mfma_tile<BM, BN, BK, WM, WN, TA, TB, NBUF, TRI>(g, t);
+}
+
 // ---- direct-to-LDS variant: 128 x BN tiles (BN 128 or 192), 32-deep K chunks
 // For launches whose tiles are all interior (M a multiple of 128, N of BN,
 // every K range a multiple of 32, operands float4-aligned).  Each chunk's operand
@@ -593,6 +618,11 @@ template <int BM, int BN, int BK, int WM, int WN, int NBUF = 2, bool TRI = false
 int launch_cfg(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits = 1) {
   g.tiles_m = (int)((g.M + BM - 1) / BM);
   g.tiles_n = (int)((g.N + BN - 1) / BN);
+  g.pair_m = 0;
+  if (TRI && (g.tri == 2 || g.tri == 3) && splits <= 1 && g.tiles_m > 1) {
+    g.pair_m = g.tiles_m;
+    g.tiles_m = (g.tiles_m + 1) / 2;
+  }
   if (splits <= 1) {
     g.kps = g.K > 0 ? g.K : 1;
     g.sZ = 0;
@@ -843,8 +873,20 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
   }
   if (tri) {
     // triangular modes: one K range per row tile (no split), on the tile
-    // shapes that carry the triangular code
-    const int t = (g.N <= 64 && g.M >= 128) ? (transpose_A ? 10 : 9) : 1;
+    // shapes that carry the triangular code.  Modes 2 and 3 run paired row
+    // tiles on 64 x 64 tiles: at GPT-2 small's attention (96 x 1024 x 64,
+    // K = 1024) that is 768 workgroups of equal work, 3 per CU, and measured
+    // 96 / 110 us (modes 2 / 3) against 130 / 125 us for paired 128 x 64
+    // tiles (384 workgroups) and 142 / 131 us for unpaired ones, which take
+    // as long as the full-K product: the CUs given the long-K row tiles set
+    // the time.
+    const int t = (g.N <= 64 && g.M >= 128 && tri != 2 && tri != 3) ? (transpose_A ? 10 : 9) : 1;
+    // The K chunk depth sets which k pairs each MFMA adds, so mode 3 keeps the
+    // 32-deep chunks of tile 10, which the untriangular product of that shape
+    // runs on: the skipped chunks are exact zeros, and the sums stay equal bit
+    // for bit to the plain masked computation's.
+    if (tri == 3 && g.N <= 64 && g.M >= 128 && g.K > 128 && transpose_A)
+      return launch_cfg<64, 64, 32, 32, 32, 2, true>(g, nb, transpose_A, transpose_B, 1);
     if (t == 1) return launch_cfg<64, 64, 16, 32, 32, 2, true>(g, nb, transpose_A, transpose_B, 1);
     if (t == 9) return launch_cfg<128, 64, 16, 64, 32, 2, true>(g, nb, transpose_A, transpose_B, 1);
     return launch_cfg<128, 64, 32, 64, 32, 1, true>(g, nb, transpose_A, transpose_B, 1);
