@@ -154,7 +154,7 @@ def test_matmul_every_tile_code(device, code, splits, ta, tb):
         assert_close(out.numpy(), og.matmul_add(A, B, bias, ta, tb), **tol(K))
 
 
-@pytest.mark.parametrize("code", [11, 12])
+@pytest.mark.parametrize("code", [11, 12, 13])
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
 @pytest.mark.parametrize("batch,M,N,K,splits,bias_mode", [
     (1, 128, 256, 96, 1, 1),
@@ -162,9 +162,10 @@ def test_matmul_every_tile_code(device, code, splits, ta, tb):
     (3, 128, 128, 64, 1, 2),   # one (M, N) bias for every batch
 ])
 def test_matmul_direct_to_lds(device, code, ta, tb, batch, M, N, K, splits, bias_mode):
-    # tiles 11 / 12: 128 x 128 / 128 x 192 operand tiles loaded straight into
-    # LDS in swizzled layouts; only for M a multiple of 128, N of the tile
-    # width, and whole 32-deep K chunks (N scaled to 192 / 384 for tile 12)
+    # tiles 11 / 12 / 13: 128 x 128 / 128 x 192 / 128 x 64 operand tiles
+    # loaded straight into LDS in swizzled layouts; only for M a multiple of
+    # 128, N of the tile width, and whole 32-deep K chunks (N scaled to 192 /
+    # 384 for tile 12)
     import ctypes as C
 
     from wxx_amd.backend import lib
@@ -218,10 +219,13 @@ def test_matmul_direct_to_lds_rejects_edge_tiles(device):
     with pytest.raises(lib.HIPError, match="tile 11"):
         lib.call("wxx_matmul_add", P(A.data_ptr()), P(B.data_ptr()), None, P(out.data_ptr()),
                  130, 128, 64, 1, 0, 0, 0, 0, 0, 0, 11)
-    # tile 12 needs N a multiple of 192
+    # tile 12 needs N a multiple of 192, tile 13 M a multiple of 128
     with pytest.raises(lib.HIPError, match="tile 12"):
         lib.call("wxx_matmul_add", P(A.data_ptr()), P(B.data_ptr()), None, P(out.data_ptr()),
                  128, 128, 64, 1, 0, 0, 0, 0, 0, 0, 12)
+    with pytest.raises(lib.HIPError, match="tile 13"):
+        lib.call("wxx_matmul_add", P(A.data_ptr()), P(B.data_ptr()), None, P(out.data_ptr()),
+                 130, 128, 64, 1, 0, 0, 0, 0, 0, 0, 13)
 
 
 @pytest.mark.parametrize("S,d", [(64, 64), (130, 64), (256, 32), (300, 64), (640, 64),

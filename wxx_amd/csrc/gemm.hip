@@ -446,7 +446,7 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
 // ds_read_b128 per 4 steps.
 template <bool TA, bool TB, int BN>
 __global__ __launch_bounds__(256, 2) void gemm_f32_dtl_kernel(GemmArgs g) {
-  static_assert(BN == 128 || BN == 192, "direct-to-LDS tiles are 128 x 128 or 128 x 192");
+  static_assert(BN == 64 || BN == 128 || BN == 192, "direct-to-LDS tiles are 128 x 64/128/192");
   constexpr int BM = 128, BK = 32, WM = 64, WN = BN / 2, TM = 2, TN = WN / 32;
   constexpr int RB = BN * BK / 256 / 4;  // 1 KiB regions of the B tile per wave
   __shared__ __attribute__((aligned(16))) float As0[BM * BK];
@@ -660,8 +660,8 @@ int launch_tiles(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits) {
   dim3 grid((unsigned)((int64_t)g.tiles_m * g.tiles_n * batch), 1, (unsigned)splits);
   hipStream_t s = wxx::stream();
   if constexpr (DTL) {
-    static_assert(BM == 128 && (BN == 128 || BN == 192) && BK == 32,
-                  "direct-to-LDS tiles are 128 x 128 x 32 or 128 x 192 x 32");
+    static_assert(BM == 128 && (BN == 64 || BN == 128 || BN == 192) && BK == 32,
+                  "direct-to-LDS tiles are 128 x 64/128/192 x 32");
     // 128 x 192: 4 KiB of dynamic LDS on top of the tiles' 80 KiB, so that
     // one workgroup occupies a CU (the grids it is chosen for are <= 1 per CU)
     const unsigned dyn = BN == 192 ? 4096u : 0u;
@@ -698,8 +698,8 @@ inline bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 // Replaces functional.matmul_add (reference src/wxx/functional/utils.py:378-499).
 // Strides are in elements; sA / sB == 0 marks an unbatched operand.
 // tile: 0 = choose automatically, 1 = 64x64, 2 = 128x128, 3 = 256x128; 4-10 select
-// alternative tile / K-chunk / buffering shapes of the same kernel; 11 / 12 the
-// direct-to-LDS 128x128 / 128x192 kernel.  With an
+// alternative tile / K-chunk / buffering shapes of the same kernel; 11 / 12 / 13 the
+// direct-to-LDS 128x128 / 128x192 / 128x64 kernel.  With an
 // explicit tile code, bits 8-15 give the number of K splits (0 or 1: none).
 namespace {
 int matmul_impl(const float* A, const float* B, const float* bias, float* C, int64_t M, int64_t N,
@@ -786,6 +786,8 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
                       tri == 0;
   const bool dtl192_ok = g.vec_ok && g.M % 128 == 0 && g.N % 192 == 0 && K > 0 && K % 32 == 0 &&
                          tri == 0;
+  const bool dtl64_ok = g.vec_ok && g.M % 128 == 0 && g.N % 64 == 0 && K > 0 && K % 32 == 0 &&
+                        tri == 0;
 
   if (K == 0) {
     // Empty contraction: C = bias (or 0).  Reuse the kernel with K = 0: the
@@ -843,8 +845,21 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
                              ? (g.M / 128) * (g.N / 192) * nb
                              : 0;
     const double bal192 = (double)t192 / (double)cus;
+    // 128 x 64 direct-to-LDS tiles, unsplit, for grids of 1-4 rounds over the
+    // CUs that they balance better than the 128 x 128 ones (measured on
+    // MI355X: 8192x768x768 93 / 90 us against 106 / 107 us on the 128 x 64
+    // register-staged tiles, B n- / k-contiguous; 8192x768x3072 310 us
+    // against 317 us on two K splits of 128 x 128).  Not for N <= 64: the
+    // attention products there keep the tiles their causal variants
+    // reproduce bit for bit.
+    const int64_t t64d = dtl64_ok && g.N > 64 ? (g.M / 128) * (g.N / 64) * nb : 0;
+    const double bal64 =
+        t64d > 0 ? (double)t64d / (double)(((t64d + cus - 1) / cus) * cus) : 0.0;
     if (t192 > 0 && t192 <= cus && bal192 >= 0.9 && bal192 > best) {
       tile = 12;
+      splits = 1;
+    } else if (t64d >= cus && t64d <= 4 * cus && bal64 >= 0.95 && bal64 > best) {
+      tile = 13;
       splits = 1;
     } else if (dtl_ok && t128 * smax >= cus && best >= 0.8) {
       tile = 11;
@@ -913,6 +928,11 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
                   "16-byte aligned operands");
       return launch_cfg<128, 192, 32, 64, 96, 2, false, true>(g, nb, transpose_A, transpose_B,
                                                               splits);
+    case 13:
+      WXX_REQUIRE(dtl64_ok, "tile 13 needs M a multiple of 128, N of 64, K of 32 and "
+                  "16-byte aligned operands");
+      return launch_cfg<128, 64, 32, 64, 32, 2, false, true>(g, nb, transpose_A, transpose_B,
+                                                             splits);
     default: return wxx::set_error(WXX_E_ARG, "bad tile %d", tile);
   }
 }
