@@ -818,7 +818,12 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
     // ~5 TB/s next to 2 * M * N * K flops at ~130 TFLOP/s, a relative cost of
     // (s + 1) * 52 / K.  Below an efficiency of 0.8 the smaller tiles below
     // do better.
-    const int64_t smax = dtl_ok ? std::min<int64_t>(16, std::max<int64_t>(g.K / 512, 1)) : 0;
+    // (Not for K <= 128 or thin M / N: the register-staged 64 x 64 / 128 x 64
+    // tiles below are faster there, e.g. attention's 96 x 1024 x 1024 x 64
+    // scores at 191 us against 237 us on 128 x 128 direct-to-LDS tiles.)
+    const bool thin = g.M <= 64 || g.N <= 64 || g.K <= 128;
+    const int64_t smax =
+        dtl_ok && !thin ? std::min<int64_t>(16, std::max<int64_t>(g.K / 512, 1)) : 0;
     double best = 0.0;
     int best_splits = 1;
     for (int64_t sp = 1; sp <= smax; ++sp) {
@@ -841,7 +846,7 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
     // against 5.19 ms).  At K = 768 the 128 x 64 tiles stay faster
     // (100-101 us against 107-108 us), as do the split 128 x 128 tiles for
     // an n-contiguous B at K = 3072 (318 us against 340 us).
-    const int64_t t192 = dtl192_ok && ((transpose_B && g.K >= 2048) || g.K >= 16384)
+    const int64_t t192 = dtl192_ok && !thin && ((transpose_B && g.K >= 2048) || g.K >= 16384)
                              ? (g.M / 128) * (g.N / 192) * nb
                              : 0;
     const double bal192 = (double)t192 / (double)cus;
@@ -849,10 +854,10 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
     // CUs that they balance better than the 128 x 128 ones (measured on
     // MI355X: 8192x768x768 93 / 90 us against 106 / 107 us on the 128 x 64
     // register-staged tiles, B n- / k-contiguous; 8192x768x3072 310 us
-    // against 317 us on two K splits of 128 x 128).  Not for N <= 64: the
-    // attention products there keep the tiles their causal variants
+    // against 317 us on two K splits of 128 x 128).  Not for thin operands:
+    // attention's N = 64 products keep the tiles their causal variants
     // reproduce bit for bit.
-    const int64_t t64d = dtl64_ok && g.N > 64 ? (g.M / 128) * (g.N / 64) * nb : 0;
+    const int64_t t64d = dtl64_ok && !thin ? (g.M / 128) * (g.N / 64) * nb : 0;
     const double bal64 =
         t64d > 0 ? (double)t64d / (double)(((t64d + cus - 1) / cus) * cus) : 0.0;
     if (t192 > 0 && t192 <= cus && bal192 >= 0.9 && bal192 > best) {
