@@ -127,6 +127,19 @@ def test_contiguous_bit_exact(device, shape, perm):
     assert np.array_equal(got, np.ascontiguousarray(np.transpose(x, perm)))
 
 
+@pytest.mark.parametrize("start", [0, 1, 4])
+@pytest.mark.parametrize("inner", [8, 6])
+def test_contiguous_quads_and_fallbacks(device, start, inner):
+    # copies whose innermost dim is unit stride in both views move 16-byte
+    # quads when that length, the outer strides and both bases allow it;
+    # a length of 6 or a base 1 float off 16 bytes takes the element path
+    x = rng(20 + start + inner).standard_normal((2, 5, 3, 12)).astype(np.float32)
+    v = F().permute(up(x).narrow(3, start, inner), 0, 2, 1, 3)
+    got = F().contiguous(v).numpy()
+    assert np.array_equal(got, np.ascontiguousarray(
+        np.transpose(x[..., start:start + inner], (0, 2, 1, 3))))
+
+
 def test_assign_and_scatter_and_unfold(device):
     x = np.zeros((5, 6), np.float32)
     t = up(x)

@@ -301,6 +301,11 @@ __global__ __launch_bounds__(kBlock) void copy_strided_kernel(T* __restrict__ ds
   }
 }
 
+// 16 bytes moved as one element by copy_strided_kernel (dwordx4 accesses).
+struct alignas(16) Quad {
+  uint32_t x, y, z, w;
+};
+
 template <typename T>
 __global__ __launch_bounds__(kBlock) void fill_strided_kernel(T* __restrict__ dst, ND nd,
                                                               int64_t n, T v) {
@@ -612,6 +617,34 @@ WXX_API int wxx_copy_strided(void* dst, const void* src, int itemsize, int rank,
         hipLaunchKernelGGL(transpose_tile_kernel<uint64_t>, grid, dim3(kBlock), 0, s,
                            (uint64_t*)dst, (const uint64_t*)src, batch, rows, cols, sb,
                            nd.stride[1][nd.rank - 2], nd.stride[1][nd.rank - 1], db, dr);
+      WXX_LAUNCHED();
+      return WXX_OK;
+    }
+  }
+  // Both views unit stride along the innermost dim, whose length and every
+  // outer stride are multiples of 4, on 16-byte aligned bases (e.g. the
+  // attention head split / merge permutes, 64 contiguous floats per head):
+  // copy 16-byte quads, a quarter of the index arithmetic per byte.
+  if (itemsize == 4 && nd.stride[0][nd.rank - 1] == 1 && nd.stride[1][nd.rank - 1] == 1 &&
+      nd.shape[nd.rank - 1] % 4 == 0 && ((uintptr_t)dst & 15) == 0 &&
+      ((uintptr_t)src & 15) == 0) {
+    bool quads = true;
+    for (int d = 0; d + 1 < nd.rank; ++d)
+      quads = quads && nd.stride[0][d] % 4 == 0 && nd.stride[1][d] % 4 == 0;
+    if (quads) {
+      ND q = nd;
+      q.shape[q.rank - 1] /= 4;
+      for (int d = 0; d + 1 < q.rank; ++d) {
+        q.stride[0][d] /= 4;
+        q.stride[1][d] /= 4;
+      }
+      const int64_t nq = n / 4;
+      if (!fits32(q, nq))
+        hipLaunchKernelGGL((copy_strided_kernel<Quad, true>), dim3(grid_for(nq)), dim3(kBlock), 0,
+                           s, (Quad*)dst, (const Quad*)src, q, nq);
+      else
+        hipLaunchKernelGGL((copy_strided_kernel<Quad, false>), dim3(grid_for(nq)), dim3(kBlock),
+                           0, s, (Quad*)dst, (const Quad*)src, q, nq);
       WXX_LAUNCHED();
       return WXX_OK;
     }
