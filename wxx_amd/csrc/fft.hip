@@ -669,8 +669,11 @@ __global__ __launch_bounds__(Big<LOGM>::T, Big<LOGM>::MIN_WAVES) void irfft_big_
 
   float2 v[G::E];
   for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
-    int t = threadIdx.x;  // opaque per row, as in rfft_big_kernel
+    int t = threadIdx.x;  // t and wt opaque per row, as in rfft_big_kernel
     WXX_OPAQUE(t);
+    float2 wtr = wt;
+    WXX_OPAQUE(wtr.x);
+    WXX_OPAQUE(wtr.y);
     const float2* Xr = X + row * in_len;
     if (in_len >= G::M)
       irfft_big_load<LOGM, true>(v, Xr, t, in_len);
@@ -696,7 +699,10 @@ __global__ __launch_bounds__(Big<LOGM>::T, Big<LOGM>::MIN_WAVES) void irfft_big_
       }
       const float2 ee = make_float2(0.5f * (a.x + b.x), 0.5f * (a.y - b.y));
       const float2 d = make_float2(0.5f * (a.x - b.x), 0.5f * (a.y + b.y));
-      const float2 w = cmul(wt, wu[big_pos0<LOGM>(e)]);  // o = d * conj(w)
+      // o = d * conj(w); the constant twiddles only at n = 16384, where they
+      // fit the VGPR budget (the shorter rows' kernels would spill)
+      const float2 w = LOGM == 13 ? cmul(wtr, untangle_tw<G::E, G::T>(wu, big_pos0<LOGM>(e)))
+                                  : cmul(wt, wu[big_pos0<LOGM>(e)]);
       const float2 o = make_float2(d.x * w.x + d.y * w.y, d.y * w.x - d.x * w.y);
       v[e] = make_float2(ee.x - o.y, ee.y + o.x);
     }
