@@ -105,6 +105,8 @@ def test_matmul_errors(device):
     (False, False, 100, 70, 5000, "mat"),      # 64x64 tiles, split K
     (False, True, 256, 200, 4097, "vec"),      # ragged K tail in the last split
     (True, True, 130, 129, 2048, "none"),
+    (True, False, 256, 682, 65536, "vec"),     # Hyena SwiGLU dW: 128x128 tiles, 64 splits
+    (True, False, 130, 300, 40000, "none"),    # 38 splits of 1056, the last one shorter
 ])
 def test_matmul_split_k(device, ta, tb, M, N, K, bias_kind):
     # few output tiles over a long K: the K range is split across workgroups

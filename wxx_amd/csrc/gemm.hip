@@ -885,11 +885,18 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
     } else if (2 * t128 >= cus && g.K >= 4096) {
       tile = 4;
       splits = (int)std::min<int64_t>((4 * cus + t128 - 1) / t128, kmax);
+    } else if (!dtl_ok && t128 * 64 <= 4 * cus && g.K >= 32768) {
+      // a few output tiles over a very long K that the direct-to-LDS tiles
+      // cannot take (Hyena's SwiGLU weight gradients, 256 x 682 and 682 x
+      // 256 over K = 65536): 128 x 128 tiles, about 3 units per CU, measured
+      // 262 us against 286 us on 64 x 64 tiles with 32 splits
+      tile = 4;
+      splits = (int)std::min<int64_t>(std::min<int64_t>(64, (3 * cus + t128 - 1) / t128), kmax);
     } else {
       tile = 1;
       if (t64 < 2 * cus) splits = (int)std::min<int64_t>((8 * cus + t64 - 1) / t64, kmax);
     }
-    splits = std::max(1, std::min(splits, 32));
+    splits = std::max(1, std::min(splits, tile == 4 ? 64 : 32));
   }
   if (tri) {
     // triangular modes: one K range per row tile (no split), on the tile
