@@ -31,6 +31,22 @@ def test_pointwise_broadcast(device, op, sa, sb):
     assert_close(got, oe.pointwise(a, b, op), rtol=1e-6, atol=1e-6)
 
 
+@pytest.mark.parametrize("op", [0, 1, 2, 3])
+def test_pointwise_inplace_broadcast_and_misaligned(device, op):
+    # in place (out aliases a), broadcast over the middle dim, and a view
+    # whose base is 1 float off 16 bytes, all bit-exact against float32
+    a = rng(30 + op).standard_normal((4, 6, 16)).astype(np.float32)
+    b = rng(40 + op).standard_normal((4, 1, 16)).astype(np.float32) + (3.0 if op == 3 else 0.0)
+    want = oe.pointwise(a, b, op)
+    ta = up(a)
+    F()._pointwise(ta, up(b), op)
+    assert np.array_equal(ta.numpy(), want)
+    assert np.array_equal(F().pointwise(up(a), up(b), op).numpy(), want)
+    x = rng(50 + op).standard_normal((4, 6, 17)).astype(np.float32)
+    got = F().pointwise(up(x).narrow(2, 1, 16), up(b), op).numpy()
+    assert np.array_equal(got, oe.pointwise(x[:, :, 1:], b, op))
+
+
 def test_pointwise_strided_views(device):
     # reference tests/test_pointwise.py:90-112
     x = rng(4).standard_normal((4, 6, 8)).astype(np.float32)
