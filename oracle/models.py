@@ -65,6 +65,12 @@ def _softmax(x):
     return e / e.sum(axis=-1, keepdims=True)
 
 
+def _outer_sum(a, b):
+    """sum over (batch, seq) of a[..., i] b[..., o]: one BLAS product
+    (config-5 sizes are far too slow through einsum's loops)."""
+    return a.reshape(-1, a.shape[-1]).T @ b.reshape(-1, b.shape[-1])
+
+
 def gpt2_loss_and_grads(params, x, y, n_heads, n_layers):
     """Loss and gradients (keyed by the tensors' first names: ``weightg`` /
     ``weightb`` for LayerNorm) of one GPT-2 forward + backward."""
@@ -113,7 +119,7 @@ def gpt2_loss_and_grads(params, x, y, n_heads, n_layers):
     dz[rows, y] -= 1.0
     dz /= z.shape[0]
     dlog = dz.reshape(B, S, V)
-    G["tok_emb.weight"] += np.einsum("bsv,bsd->vd", dlog, hf)
+    G["tok_emb.weight"] += _outer_sum(dlog, hf)
     dhf = dlog @ tok
     dh, dg, db = _ln_back(dhf, P["ln_f.weightg"], cf)
     G["ln_f.weightg"] += dg
@@ -123,17 +129,17 @@ def gpt2_loss_and_grads(params, x, y, n_heads, n_layers):
         a, c1, q, k, v, att, o, h1, a2, c2, z1, g1 = caches[i]
         # MLP
         G[p + "mlp.2.bias"] += dh.sum(axis=(0, 1))
-        G[p + "mlp.2.weight"] += np.einsum("bsi,bso->io", g1, dh)
+        G[p + "mlp.2.weight"] += _outer_sum(g1, dh)
         dz1 = (dh @ P[p + "mlp.2.weight"].T) * _gelu_grad(z1)
         G[p + "mlp.0.bias"] += dz1.sum(axis=(0, 1))
-        G[p + "mlp.0.weight"] += np.einsum("bsi,bso->io", a2, dz1)
+        G[p + "mlp.0.weight"] += _outer_sum(a2, dz1)
         da2 = dz1 @ P[p + "mlp.0.weight"].T
         dx2, dg2, db2 = _ln_back(da2, P[p + "ln2.weightg"], c2)
         G[p + "ln2.weightg"] += dg2
         G[p + "ln2.weightb"] += db2
         dh1 = dh + dx2
         # attention
-        G[p + "attn.out.weight"] += np.einsum("bsi,bso->io", o, dh1)
+        G[p + "attn.out.weight"] += _outer_sum(o, dh1)
         do = heads(dh1 @ P[p + "attn.out.weight"].T)
         datt = do @ v.transpose(0, 1, 3, 2)
         dv = att.transpose(0, 1, 3, 2) @ do
@@ -143,7 +149,7 @@ def gpt2_loss_and_grads(params, x, y, n_heads, n_layers):
         da = np.zeros_like(a)
         for n, dt in (("q", dq), ("k", dk), ("v", dv)):
             dt = merge(dt)
-            G[p + f"attn.{n}.weight"] += np.einsum("bsi,bso->io", a, dt)
+            G[p + f"attn.{n}.weight"] += _outer_sum(a, dt)
             da += dt @ P[p + f"attn.{n}.weight"].T
         dx1, dg1, db1 = _ln_back(da, P[p + "ln1.weightg"], c1)
         G[p + "ln1.weightg"] += dg1

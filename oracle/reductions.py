@@ -4,6 +4,9 @@
   viewed as (outer, reduce, inner) — reference src/wxx/backend/dispatch.py:173-214
   (axis mapping) and src/wxx/shaders/helpers/reduce.wgsl:31-66 (mean divides
   by f32(reduce), mode 2 squares before summing).  Accumulated in float64.
+* ``var`` / ``std``: population (ddof=0) variance as the reference composes
+  it — mean, subtract, square, mean (src/wxx/functional/reductions.py:315-336);
+  std = sqrt(var).  Accumulated in float64.
 * ``minmax``: value and u32 index with the reference's exact tie rule —
   src/wxx/shaders/helpers/reduce_minmax.wgsl:41-71: 256 lanes scan
   r = t, t+256, ... keeping the first strictly better value (init -1e38 /
@@ -49,6 +52,20 @@ def reduce(x, axis=None, keepdims=False, mode=0):
             axes = {a + x.ndim if a < 0 else a for a in axes}
             out_shape = tuple(1 if d in axes else n for d, n in enumerate(x.shape))
     return s.astype(np.float32).reshape(out_shape)
+
+
+def var(x, axis=None, keepdims=False):
+    """mean((x - mean(x, keepdims))^2) over ``axis``; float32 result."""
+    x = np.asarray(x, dtype=np.float32).astype(np.float64)
+    ax = None if axis is None else (axis if isinstance(axis, int) else tuple(axis))
+    m = x.mean(axis=ax, keepdims=True)
+    d = x - m
+    v = (d * d).mean(axis=ax, keepdims=keepdims)
+    return np.asarray(v, np.float32).reshape(np.shape(v) or (1,))
+
+
+def std(x, axis=None, keepdims=False):
+    return np.sqrt(var(x, axis, keepdims).astype(np.float64)).astype(np.float32)
 
 
 def minmax(x, axis=None, op=0):

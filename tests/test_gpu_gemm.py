@@ -264,3 +264,46 @@ def test_matmul_tri_modes(device, S, d):
                           s3)
     with pytest.raises(ValueError):
         F().matmul_add(up(q), up(k), up(np.zeros(S)), transpose_B=True, tri=1)
+
+
+def test_matmul_explicit_splits_empty_k(device):
+    # K == 0 with an explicit split count: nothing to split, C = bias
+    import ctypes as C
+
+    from wxx_amd.backend import lib
+    from wxx_amd.functional._common import empty
+
+    M, N = 5, 3
+    bias = rng(5).standard_normal(N).astype(np.float32)
+    A, B, tbias = up(np.ones((M, 1))), up(np.ones((1, N))), up(bias)
+    P = C.c_void_p
+    for code in (1, 2, 4, 9):
+        out = empty([M, N])
+        lib.call("wxx_matmul_add", P(A.data_ptr()), P(B.data_ptr()), P(tbias.data_ptr()),
+                 P(out.data_ptr()), M, N, 0, 1, 0, 0, 0, 1, 0, 0, code | (3 << 8))
+        assert np.array_equal(out.numpy(), np.broadcast_to(bias, (M, N)))
+
+
+@pytest.mark.parametrize("sbias_kind", ["shared", "padded"])
+def test_matmul_per_batch_bias_strides(device, sbias_kind):
+    # bias_mode 3 with a batch stride other than M * N over a shared B (the
+    # batch must not be folded into M then): stride 0 = one (M, N) bias for
+    # every batch; a padded stride leaves a gap between the batches' biases
+    import ctypes as C
+
+    from wxx_amd.backend import lib
+    from wxx_amd.functional._common import empty
+
+    b, M, K, N = 3, 40, 24, 36
+    r = rng(77)
+    A = r.standard_normal((b, M, K)).astype(np.float32)
+    B = r.standard_normal((K, N)).astype(np.float32)
+    sb = 0 if sbias_kind == "shared" else M * N + 17
+    store = r.standard_normal(sb * (b - 1) + M * N).astype(np.float32)
+    bias = np.stack([store[i * sb:i * sb + M * N].reshape(M, N) for i in range(b)])
+    tA, tB, tbias = up(A), up(B), up(store)
+    out = empty([b, M, N])
+    P = C.c_void_p
+    lib.call("wxx_matmul_add", P(tA.data_ptr()), P(tB.data_ptr()), P(tbias.data_ptr()),
+             P(out.data_ptr()), M, N, K, b, M * K, 0, sb, 3, 0, 0, 0)
+    assert_close(out.numpy(), og.matmul_add(A, B, bias), **tol(K))

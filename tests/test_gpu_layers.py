@@ -174,6 +174,28 @@ def test_dropout_bit_exact(device, n, p):
     assert np.array_equal(dx, ol.dropout(g, seed, p))
 
 
+def test_dropout_p0_fresh_buffer_and_module_sharing(device):
+    # functional.dropout / dropoutdx at p == 0 return a fresh buffer (as the
+    # reference does): writing into the result leaves the input unchanged.
+    # The nn/autograd layer shares the input's storage at p == 0 on purpose
+    # (no copy of attention's probabilities): there the write shows through.
+    from wxx_amd import nn
+
+    x = rng(3).standard_normal((4, 6)).astype(np.float32)
+    tx = up(x)
+    y, _ = F().dropout(tx, 0.0)
+    F().assign(y, 5.0)
+    assert np.array_equal(tx.numpy(), x)
+    assert np.all(y.numpy() == 5.0)
+    d = F().dropoutdx(tx, 0.0, 123)
+    F().assign(d, 7.0)
+    assert np.array_equal(tx.numpy(), x)
+    ym = nn.Dropout(0.0)(tx)
+    assert np.array_equal(ym.numpy(), x)
+    F().assign(ym, 9.0)
+    assert np.all(tx.numpy() == 9.0), "the autograd layer's p == 0 result shares storage"
+
+
 # ------------------------------------------------------------- decay window
 
 

@@ -139,6 +139,61 @@ def test_gpt2_shape_error_and_state_dict_roundtrip(device, tmp_path):
         assert np.array_equal(restored[k], v), k
 
 
+def test_checkpoint_resume_equals_continuous_training(device, tmp_path):
+    # weights + AdamW moments/step count + WarmupCosineLR position in one
+    # archive: 2 steps, save, 2 more steps == a fresh model restored from the
+    # archive running the same 2 steps, bit for bit (the reference loses the
+    # moments, nn/optimizer.py:50-57)
+    wxx = W()
+    nn = wxx.nn
+
+    def make():
+        m = nn.GPT2(48, d_model=32, n_heads=4, n_layers=2, max_len=16, dropout=0.0)
+        m.load_state_dict(_gpt2_state(m, seed=7))
+        opt = nn.AdamW(m.named_parameters(), lr=3e-3)  # names checked on load
+        sched = nn.WarmupCosineLR(opt, warmup_steps=2, total_steps=10, min_lr=1e-4)
+        return m, opt, sched
+
+    r = rng(21)
+    batches = [(r.integers(0, 48, (2, 12)), r.integers(0, 48, (2, 12))) for _ in range(4)]
+
+    def step(m, opt, sched, xy):
+        x, y = xy
+        loss = nn.CCELoss()(m(up_u32(x)).reshape(-1, 48), up_u32(y.reshape(-1)))
+        opt.zero_grad()
+        loss.backward()
+        nn.clip_grad_norm_(m.parameters(), 1.0)
+        opt.step()
+        sched.step()
+        return float(loss.numpy().reshape(-1)[0])
+
+    m, opt, sched = make()
+    for xy in batches[:2]:
+        step(m, opt, sched, xy)
+    path = wxx.serialization.save_checkpoint(tmp_path / "ck", m, opt, sched)
+    cont = [step(m, opt, sched, xy) for xy in batches[2:]]
+    m2, opt2, sched2 = make()
+    wxx.serialization.load_checkpoint(path, m2, opt2, sched2)
+    assert opt2.step_count == 2 and sched2.last_epoch == sched.last_epoch - 2
+    resumed = [step(m2, opt2, sched2, xy) for xy in batches[2:]]
+    assert cont == resumed
+    a, b = m.state_dict(), m2.state_dict()
+    for k in a:
+        assert np.array_equal(a[k], b[k]), k
+    for s1, s2 in zip(opt.state, opt2.state):
+        assert np.array_equal(s1["exp_avg_sq"].numpy(), s2["exp_avg_sq"].numpy())
+    # without the moments (weights only) the next step differs
+    m3, opt3, sched3 = make()
+    wxx.serialization.load_checkpoint(path, m3, None, sched3)
+    step(m3, opt3, sched3, batches[2])
+    assert any(not np.array_equal(m3.state_dict()[k], m2.state_dict()[k]) for k in a)
+    with pytest.raises(ValueError):
+        other = nn.AdamW(nn.GPT2(48, d_model=32, n_heads=4, n_layers=1, max_len=16)
+                         .named_parameters())
+        other.load_state_dict({k[6:]: v for k, v in wxx.load(path).items()
+                               if k.startswith("optim.")})
+
+
 def test_gpt2_is_causal_and_mask(device):
     wxx = W()
     from wxx_amd.backend.context import inferenceMode

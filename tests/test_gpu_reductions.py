@@ -194,3 +194,35 @@ def test_softmax_causal_equals_masked_softmax(device, BH, S):
     dxs = F().softmax_backward_causal(F().from_numpy(want), F().from_numpy(g), scale,
                                       skip=True).numpy()
     assert np.array_equal(dxs[lower], wdx[lower])
+
+
+@pytest.mark.parametrize("shape,axis,keepdims", [
+    ((6, 7), None, False), ((6, 7), 1, True), ((3, 4, 5), (1, 2), False), ((9,), 0, False),
+    ((64, 4096), -1, False), ((8, 1024, 768), 2, True), ((5, 1, 3), 1, False),
+])
+def test_var_std(device, shape, axis, keepdims):
+    # the reference's composite (functional/reductions.py:315-336): mean,
+    # subtract, square, mean; std = sqrt(var); population variance
+    x = (rng(sum(shape)).standard_normal(shape) * 2 + 0.5).astype(np.float32)
+    v = F().var(up(x), axis=axis, keepdims=keepdims).numpy()
+    s = F().std(up(x), axis=axis, keepdims=keepdims).numpy()
+    assert_close(v, orr.var(x, axis, keepdims), rtol=1e-4, atol=1e-5)
+    assert_close(s, orr.std(x, axis, keepdims), rtol=1e-4, atol=1e-5)
+    # the Tensor methods take the same path, and var backward is 2 (x - mean) / n
+    from wxx_amd.Tensor import Tensor
+
+    t = Tensor(list(x.shape), data=x, requires_grad=True)
+    tv = t.var(axis=axis, keepdims=keepdims)
+    assert_close(tv.numpy(), v, rtol=0, atol=0)
+    tv.sum().backward()
+    ax = None if axis is None else axis
+    n = x.size if axis is None else int(np.prod([x.shape[a] for a in np.atleast_1d(axis)]))
+    xd = x.astype(np.float64)
+    want = 2 * (xd - xd.mean(axis=ax, keepdims=True)) / n
+    assert_close(t.grad.numpy(), want, rtol=1e-4, atol=1e-5)
+
+
+def test_var_rejects_non_contiguous_axes(device):
+    # as the reference's reduction mapping (backend/dispatch.py:173-214)
+    with pytest.raises(ValueError):
+        F().var(up(np.ones((3, 4, 5))), axis=(0, 2))

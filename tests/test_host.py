@@ -44,3 +44,23 @@ def test_validation_errors():
 def test_keepdims_shape():
     assert dispatch.keepdims_shape((4, 5), 1) == (4, 1)
     assert dispatch.keepdims_shape((4, 5), None) == (1, 1)
+
+
+def test_reference_import_name_resolves_to_this_package():
+    # code written against the reference imports ``wxx`` and its submodules
+    # (e.g. nn/module.py:5 ``from wxx.functional.utils import from_numpy``);
+    # both names must give the very same module objects (one device, one
+    # set of classes), and importing opens no device
+    import wxx
+    import wxx_amd
+    from wxx.functional.utils import from_numpy
+    from wxx.nn.gpt import GPT2
+    import wxx.autograd.function as waf
+    import wxx_amd.autograd.function as aaf
+
+    assert wxx is wxx_amd
+    assert from_numpy is wxx_amd.functional.utils.from_numpy
+    assert GPT2 is wxx_amd.nn.GPT2
+    assert waf is aaf
+    with pytest.raises(ModuleNotFoundError):
+        __import__("wxx.no_such_module")

@@ -467,3 +467,107 @@ def test_reference_float32_arithmetic_error_is_small(n):
     assert (np.abs(got - want) / scale).max() < 2e-6
     back = of.irfft_radix2_f32(want.astype(np.complex64), n)
     np.testing.assert_allclose(back, x, atol=2e-6 * np.abs(x).max())
+
+
+# ------------------------------------------- softmax backward, selu, complex
+
+
+@pytest.mark.parametrize("shape,dim", [((5, 9), -1), ((3, 7, 4), 1), ((2, 3, 6), 0)])
+def test_softmax_backward_against_torch_autograd_and_differences(shape, dim):
+    # the chain of reference autograd/reductions.py:25-35: y * (g - sum(g y))
+    # pinned by torch's float64 autograd of softmax (independent code) and by
+    # central differences of oa.softmax; a dropped y factor, a flipped sign or
+    # a sum over the wrong axis fails both
+    import torch
+
+    r = rng(sum(shape) + dim)
+    x = r.standard_normal(shape)
+    g = r.standard_normal(shape)
+    y = oa.softmax(x, dim)
+    got = oa.softmax_backward(y, g, dim)
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    torch.softmax(xt, dim).backward(torch.tensor(g, dtype=torch.float64))
+    assert_close(got, xt.grad.numpy(), rtol=1e-5, atol=1e-6)
+    # directional derivative: <dL/dx, v> = d/dt <g, softmax(x + t v)> at t = 0
+    v = r.standard_normal(shape)
+    h = 1e-3
+    num = ((g * oa.softmax(x + h * v, dim)).sum() - (g * oa.softmax(x - h * v, dim)).sum()) / (2 * h)
+    assert abs(float((got.astype(np.float64) * v).sum()) - num) < 1e-3 * (1 + abs(num))
+
+
+def test_selu_against_torch():
+    # selu.wgsl's constants and branch (x > 0 -> SCALE x, else SCALE ALPHA (e^x - 1))
+    import torch
+
+    x = np.concatenate([np.linspace(-6, 6, 241), [0.0, -0.0, 1e-8, -1e-8, 30.0, -30.0]])
+    ref = torch.nn.functional.selu(torch.tensor(x, dtype=torch.float64)).numpy()
+    assert_close(oa.selu(x), ref, rtol=1e-6, atol=1e-7)
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    torch.nn.functional.selu(xt).sum().backward()
+    d = xt.grad.numpy()
+    # torch takes the left branch's derivative at exactly 0 as well
+    nz = x != 0
+    assert_close(oa.selubackwards(x)[nz], d[nz], rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("conj_a", [False, True])
+@pytest.mark.parametrize("conj_b", [False, True])
+def test_complex_mul_against_real_expansion(conj_a, conj_b):
+    # complex_mul.wgsl: conjugation negates the operand's imaginary part before
+    # (ac - bd, ad + bc); checked against that expansion written on real
+    # pairs and against Python's own complex product on scalars
+    r = rng(int(conj_a) * 2 + int(conj_b))
+    a = (r.standard_normal((4, 9)) + 1j * r.standard_normal((4, 9))).astype(np.complex64)
+    b = (r.standard_normal((4, 9)) + 1j * r.standard_normal((4, 9))).astype(np.complex64)
+    ar, ai = a.real.astype(np.float64), a.imag.astype(np.float64) * (-1 if conj_a else 1)
+    br, bi = b.real.astype(np.float64), b.imag.astype(np.float64) * (-1 if conj_b else 1)
+    got = of.complex_mul(a, b, conj_a, conj_b)
+    assert_close(got.real, ar * br - ai * bi, rtol=1e-6, atol=1e-6)
+    assert_close(got.imag, ar * bi + ai * br, rtol=1e-6, atol=1e-6)
+    for i, j in [(0, 0), (3, 8), (2, 5)]:
+        za, zb = complex(a[i, j]), complex(b[i, j])
+        za = za.conjugate() if conj_a else za
+        zb = zb.conjugate() if conj_b else zb
+        assert abs(complex(got[i, j]) - za * zb) < 1e-5 * (1 + abs(za * zb))
+    # broadcast over leading dims
+    bb = b[0]
+    assert np.array_equal(of.complex_mul(a, bb, conj_a, conj_b),
+                          np.stack([of.complex_mul(a[k], bb, conj_a, conj_b) for k in range(4)]))
+    # a * conj(a) = |a|^2, real
+    s = of.complex_mul(a, a, False, True)
+    assert_close(s.real, np.abs(a.astype(np.complex128)) ** 2, rtol=1e-6, atol=1e-6)
+    assert np.all(np.abs(s.imag) <= 1e-6 * (1 + s.real))
+
+
+@pytest.mark.parametrize("in_len,out_len", [(5, 9), (9, 5), (7, 7), (1, 4), (6, 1)])
+def test_complex_pad_against_reference_index_rule(in_len, out_len):
+    # complex_pad.wgsl: Y[b, j] = X[b, j] for j < in_len else 0, over a
+    # contiguous (batch, in_len) source; restated here as a literal loop
+    r = rng(in_len * 10 + out_len)
+    x = (r.standard_normal((3, 2, in_len)) + 1j * r.standard_normal((3, 2, in_len))).astype(
+        np.complex64)
+    flat = x.reshape(-1)
+    batch = 6
+    want = np.empty(batch * out_len, np.complex64)
+    for idx in range(batch * out_len):
+        bi, j = divmod(idx, out_len)
+        want[idx] = flat[bi * in_len + j] if j < in_len else 0
+    got = of.complex_pad(x, out_len)
+    assert got.shape == (3, 2, out_len)
+    assert np.array_equal(got.reshape(-1), want)
+
+
+@pytest.mark.parametrize("shape,axis,keepdims", [((6, 7), None, False), ((6, 7), 1, True),
+                                                 ((3, 4, 5), (0, 2), False), ((9,), 0, False)])
+def test_var_std_against_numpy(shape, axis, keepdims):
+    # population variance (ddof = 0) of reference functional/reductions.py:315-336;
+    # numpy's var / std are independent code, and a ddof = 1 slip or a mean over
+    # the wrong axis fails
+    x = rng(len(shape)).standard_normal(shape) * 3 + 1
+    want = np.var(x.astype(np.float32).astype(np.float64), axis=axis, keepdims=keepdims)
+    assert_close(orr.var(x, axis, keepdims), np.asarray(want).reshape(np.shape(want) or (1,)),
+                 rtol=1e-6, atol=1e-7)
+    wstd = np.std(x.astype(np.float32).astype(np.float64), axis=axis, keepdims=keepdims)
+    assert_close(orr.std(x, axis, keepdims), np.asarray(wstd).reshape(np.shape(wstd) or (1,)),
+                 rtol=1e-6, atol=1e-7)
+    assert np.all(orr.var(np.full(shape, 2.5), axis, keepdims) == 0)

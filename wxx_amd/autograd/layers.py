@@ -34,14 +34,16 @@ class CrossEntropyLoss(Function):
 
 class Dropout(Function):
     def forward(self, tensor1, p=0.2):
-        out, seed = functional.dropout(tensor1, p)
+        # at p == 0 the output shares the input's storage (no copy); the
+        # engine never writes into activations or gradients in place
+        out, seed = functional.dropout(tensor1, p, share_at_zero=True)
         out.requires_grad = tensor1.requires_grad
         return self.attach(out, p=p, seed=seed)
 
     def backward(self, g):
         if not any(self.needs_input_grad):
             return None
-        return functional.dropoutdx(g, self.p, self.seed)
+        return functional.dropoutdx(g, self.p, self.seed, share_at_zero=True)
 
 
 class Embedding(Function):

@@ -623,7 +623,8 @@ int launch_cfg(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits = 1) {
     g.pair_m = g.tiles_m;
     g.tiles_m = (g.tiles_m + 1) / 2;
   }
-  if (splits <= 1) {
+  // K == 0 has nothing to split (and no K range to size splits from)
+  if (splits <= 1 || g.K == 0) {
     g.kps = g.K > 0 ? g.K : 1;
     g.sZ = 0;
     return launch_tiles<BM, BN, BK, WM, WN, NBUF, TRI, DTL>(g, batch, ta, tb, 1);
@@ -769,7 +770,10 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
   int64_t nb = batch;
   // Fold the batch into M when B is shared and A's rows are contiguous across
   // batches: one larger GEMM fills the GPU better than `batch` small ones.
-  if (batch > 1 && sB == 0 && !transpose_A && sA == M * K && tri == 0) {
+  // (A per-batch bias folds into an (M*batch, N) bias only when its batches
+  // are packed back to back.)
+  if (batch > 1 && sB == 0 && !transpose_A && sA == M * K && tri == 0 &&
+      (bias_mode != 3 || sBias == M * N)) {
     g.M = M * batch;
     g.sA = 0;
     g.sC = 0;
@@ -797,6 +801,7 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
   tile &= 0xff;
   WXX_REQUIRE(splits <= 64, "bad split count %d", splits);
   splits = std::max(splits, 1);
+  if (K == 0) splits = 1;
   if (tile == 0) {
     // Measured on MI355X (fp32 GEMM shapes of GPT-2 small and BASELINE
     // config 2): the direct-to-LDS 128x128 tiles are the fastest wherever

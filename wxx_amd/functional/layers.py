@@ -84,12 +84,23 @@ def _same_values(t):
     return out
 
 
-def dropout(tensor1, p):
+def _copy_of(t):
+    """A fresh buffer holding ``t``'s (contiguous) values."""
+    out = empty(t.shape)
+    call("wxx_d2d", ptr(out), ptr(t), 4 * math.prod(t.shape))
+    return out
+
+
+def dropout(tensor1, p, share_at_zero=False):
     """Inverted dropout; returns ``(y, seed)`` with a fresh 32-bit seed per call.
 
-    At ``p == 0`` every element is kept with scale exactly 1, so the result is
-    the input's values: the seed is still drawn (the host RNG advances exactly
-    as in the reference) and a view of the input is returned without a launch.
+    At ``p == 0`` every element is kept with scale exactly 1, so the result
+    holds the input's values and the seed is still drawn (the host RNG
+    advances exactly as in the reference).  The result is a fresh buffer, as
+    in the reference, unless ``share_at_zero`` asks for a tensor over the
+    input's storage instead (the autograd layer's choice: it saves a copy of
+    attention's probabilities; an in-place write into such a result also
+    changes the input).
     """
     if not tensor1.is_contiguous():
         tensor1 = tensor1.contiguous()
@@ -97,19 +108,20 @@ def dropout(tensor1, p):
     scale = 1 / (1 - p)
     r = random.randint(0, 2**32 - 1)
     if p == 0:
-        return _same_values(tensor1), r
+        return (_same_values(tensor1) if share_at_zero else _copy_of(tensor1)), r
     out = empty(tensor1.shape)
     call("wxx_dropout", ptr(tensor1), ptr(out), n, r, float(p), float(scale))
     return out, r
 
 
-def dropoutdx(tensor1, p, seed):
+def dropoutdx(tensor1, p, seed, share_at_zero=False):
     """Gradient of :func:`dropout` with the forward call's ``seed`` (the
-    gradient's own values at ``p == 0``)."""
+    gradient's own values at ``p == 0``, in a fresh buffer unless
+    ``share_at_zero``)."""
     if not tensor1.is_contiguous():
         tensor1 = tensor1.contiguous()
     if p == 0:
-        return _same_values(tensor1)
+        return _same_values(tensor1) if share_at_zero else _copy_of(tensor1)
     n = math.prod(tensor1.shape)
     out = empty(tensor1.shape)
     call("wxx_dropout", ptr(tensor1), ptr(out), n, int(seed) & 0xFFFFFFFF, float(p),

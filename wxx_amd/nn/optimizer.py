@@ -9,6 +9,8 @@ as the reference's sequential loop does: the list is split into rounds in
 which every storage appears once, and the rounds run in order.
 """
 
+import numpy as np
+
 from .. import functional
 from ..backend.device import get_cmd_buffer
 from ..Tensor import Tensor
@@ -22,6 +24,14 @@ class Optimizer:
 
     def step(self):
         pass
+
+    def state_dict(self):
+        """Hyper-parameters only (a stateless optimizer)."""
+        return {"lr": np.float64(self.lr)} if hasattr(self, "lr") else {}
+
+    def load_state_dict(self, state):
+        if "lr" in state:
+            self.lr = float(state["lr"])
 
     def zero_grad(self, wait=False):
         for _, w in self.parameters:
@@ -64,6 +74,46 @@ class AdamW(Optimizer):
         self.step_count = 0
         self.state = [{"exp_avg": Tensor(p.shape, value=0), "exp_avg_sq": Tensor(p.shape, value=0)}
                       for _, p in self.params]
+
+    # The reference keeps the moments only in memory (nn/optimizer.py:50-57);
+    # these two make them part of a checkpoint.  Entries are keyed by the
+    # position in the parameter list (a parameter listed twice has two
+    # moment pairs); the names are stored to check the list on load.
+    def state_dict(self):
+        """The step count, hyper-parameters and both moments of every entry,
+        as numpy arrays (an ``.npz``-ready dict)."""
+        sd = {
+            "step_count": np.int64(self.step_count),
+            "lr": np.float64(self.lr),
+            "betas": np.array([self.beta1, self.beta2], np.float64),
+            "eps": np.float64(self.eps),
+            "weight_decay": np.float64(self.weight_decay),
+            "param_names": np.array([str(n) for n, _ in self.params]),
+        }
+        for i, st in enumerate(self.state):
+            sd[f"exp_avg.{i}"] = st["exp_avg"].numpy()
+            sd[f"exp_avg_sq.{i}"] = st["exp_avg_sq"].numpy()
+        return sd
+
+    def load_state_dict(self, state):
+        """Restore what :meth:`state_dict` saved into this optimizer's moment
+        buffers; the parameter list must have the same names and shapes."""
+        names = [str(n) for n in np.asarray(state["param_names"]).tolist()]
+        mine = [str(n) for n, _ in self.params]
+        if names != mine:
+            raise ValueError(f"optimizer state is for parameters {names[:4]}..., "
+                             f"this optimizer holds {mine[:4]}...")
+        for i, st in enumerate(self.state):
+            for key in ("exp_avg", "exp_avg_sq"):
+                arr = np.asarray(state[f"{key}.{i}"], np.float32)
+                if list(arr.shape) != list(st[key].shape):
+                    raise ValueError(f"{key}.{i}: shape {arr.shape} != {tuple(st[key].shape)}")
+                functional.assign(st[key], functional.from_numpy(arr))
+        self.step_count = int(state["step_count"])
+        self.lr = float(state["lr"])
+        self.beta1, self.beta2 = (float(b) for b in np.asarray(state["betas"]))
+        self.eps = float(state["eps"])
+        self.weight_decay = float(state["weight_decay"])
 
     def step(self):
         self.step_count += 1

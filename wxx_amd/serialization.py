@@ -1,43 +1,95 @@
-"""``.npz`` save / load of models, state_dicts and tensors (reference
-src/wxx/serialization.py:1-54): one array per dotted parameter name."""
+"""On-disk format: numpy ``.npz`` archives (reference src/wxx/serialization.py:1-54).
+
+``save`` / ``load`` keep the reference's contract: a model (or any
+``state_dict``) is stored as one array per dotted parameter name, a lone
+tensor under the key ``"tensor"``, and ``load(path, model)`` fills the model
+and returns it.  Archives are read with ``allow_pickle=False``: they hold
+plain arrays only.
+
+``save_checkpoint`` / ``load_checkpoint`` add what the reference cannot
+persist: the AdamW moments and step count and the LR scheduler position, in
+the same archive as the weights, under the prefixes ``model.``, ``optim.``
+and ``sched.``, so that a resumed run continues bit for bit.
+"""
 
 import os
 
 import numpy as np
 
-from .nn.module import Module
+_PREFIXES = ("model.", "optim.", "sched.")
 
 
-def _to_arrays(obj):
-    if isinstance(obj, Module):
+def _npz_path(path, reading=False):
+    path = str(path)
+    if path.endswith(".npz") or (reading and os.path.exists(path)):
+        return path
+    return path + ".npz"
+
+
+def _as_array(v):
+    if isinstance(v, np.ndarray):
+        return v
+    if hasattr(v, "numpy"):  # a device Tensor
+        return np.asarray(v.numpy())
+    return np.asarray(v)
+
+
+def _flatten(obj):
+    """Name -> array for a model / optimizer / scheduler, dict or tensor."""
+    if hasattr(obj, "state_dict") and callable(obj.state_dict):
         obj = obj.state_dict()
     if isinstance(obj, dict):
-        return {str(k): np.asarray(v.numpy() if hasattr(v, "numpy") and
-                                   not isinstance(v, np.ndarray) else v)
-                for k, v in obj.items()}
-    if hasattr(obj, "numpy") and not isinstance(obj, np.ndarray):
-        obj = obj.numpy()
-    return {"tensor": np.asarray(obj)}
+        return {str(k): _as_array(v) for k, v in obj.items()}
+    return {"tensor": _as_array(obj)}
+
+
+def _read(path):
+    with np.load(_npz_path(path, reading=True), allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
 
 
 def save(obj, path):
-    """Save a model, state_dict or tensor to ``path`` (``.npz`` appended if missing)."""
-    path = str(path)
-    if not path.endswith(".npz"):
-        path += ".npz"
-    np.savez(path, **_to_arrays(obj))
-    return path
+    """Write a model, optimizer, scheduler, state_dict or tensor to ``path``
+    (``.npz`` appended when missing); returns the path written."""
+    out = _npz_path(path)
+    np.savez(out, **_flatten(obj))
+    return out
 
 
 def load(path, model=None):
-    """Load an ``.npz`` archive (numpy arrays only, no pickles); with ``model``
-    fill its parameters and return it, else return the dict of arrays."""
-    path = str(path)
-    if not path.endswith(".npz") and not os.path.exists(path):
-        path += ".npz"
-    with np.load(path, allow_pickle=False) as data:
-        state = {k: data[k] for k in data.files}
-    if model is not None:
-        model.load_state_dict(state)
-        return model
-    return state
+    """Read an archive.  With ``model`` (anything with ``load_state_dict``)
+    the arrays are loaded into it and it is returned; otherwise the dict of
+    arrays is returned."""
+    arrays = _read(path)
+    if model is None:
+        return arrays
+    model.load_state_dict(arrays)
+    return model
+
+
+def save_checkpoint(path, model, optimizer=None, scheduler=None):
+    """Weights, optimizer state and scheduler position in one archive."""
+    arrays = {}
+    for prefix, part in zip(_PREFIXES, (model, optimizer, scheduler)):
+        if part is not None:
+            arrays.update({prefix + k: v for k, v in _flatten(part).items()})
+    out = _npz_path(path)
+    np.savez(out, **arrays)
+    return out
+
+
+def load_checkpoint(path, model, optimizer=None, scheduler=None):
+    """Restore what :func:`save_checkpoint` wrote into the given objects; a
+    part requested but absent from the archive raises ``KeyError``."""
+    arrays = _read(path)
+    for prefix, part in zip(_PREFIXES, (model, optimizer, scheduler)):
+        if part is None:
+            continue
+        sub = {k[len(prefix):]: v for k, v in arrays.items() if k.startswith(prefix)}
+        if not sub:
+            raise KeyError(f"{path}: no '{prefix[:-1]}' entries in the checkpoint")
+        part.load_state_dict(sub)
+    return model
+
+
+__all__ = ["save", "load", "save_checkpoint", "load_checkpoint"]
