@@ -73,6 +73,17 @@ int wxx_timer_elapsed(int start, int stop, float* ms);
 int wxx_matmul_add(const float* A, const float* B, const float* bias, float* C, int64_t M,
                    int64_t N, int64_t K, int64_t batch, int64_t sA, int64_t sB, int64_t sBias,
                    int bias_mode, int transpose_A, int transpose_B, int tile);
+/* No counterpart in the reference: wxx_matmul_add for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, kernels and results (bit
+ * for bit); the split-K partials go to a fixed 64 MiB (16 Mi floats) device
+ * array instead of the allocator, and a call needing more fails with
+ * WXX_E_RANGE before enqueuing anything.  Calls share that array per GPU:
+ * calls that overlap on one GPU race. */
+int wxx_matmul_add_noalloc(const float* A, const float* B, const float* bias, float* C,
+                           int64_t M, int64_t N, int64_t K, int64_t batch, int64_t sA,
+                           int64_t sB, int64_t sBias, int bias_mode, int transpose_A,
+                           int transpose_B, int tile);
 /* No counterpart in the reference: the products of causal attention with
  * their exactly-zero triangles skipped (same results as wxx_matmul_add, no
  * bias).  tri 1: C square, tiles wholly above the diagonal set to 0 (Q K^T,

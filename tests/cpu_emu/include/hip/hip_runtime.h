@@ -32,6 +32,8 @@
 #define __forceinline__ inline
 #define __launch_bounds__(...)
 #define __shared__ static
+#define __align__(n) __attribute__((aligned(n)))
+#define HIP_SYMBOL(x) ((const void*)&(x))
 
 using std::max;
 using std::min;
@@ -192,6 +194,12 @@ struct hipDeviceProp_t { char name[256]; char gcnArchName[256]; int multiProcess
 
 hipError_t hipGetDeviceCount(int* n);
 hipError_t hipSetDevice(int d);
+inline hipError_t hipGetDevice(int* d) { *d = 0; return hipSuccess; }
+// a __device__ variable is ordinary host storage here: its address is the symbol's
+inline hipError_t hipGetSymbolAddress(void** p, const void* sym) {
+  *p = const_cast<void*>(sym);
+  return hipSuccess;
+}
 hipError_t hipGetDeviceProperties(hipDeviceProp_t* p, int d);
 hipError_t hipStreamCreateWithFlags(hipStream_t* s, unsigned f);
 hipError_t hipStreamSynchronize(hipStream_t s);

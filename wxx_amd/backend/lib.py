@@ -45,6 +45,10 @@ SIGNATURES = {
         I32,
         [P, P, P, P, I64, I64, I64, I64, I64, I64, I64, I32, I32, I32, I32],
     ),
+    "wxx_matmul_add_noalloc": (
+        I32,
+        [P, P, P, P, I64, I64, I64, I64, I64, I64, I64, I32, I32, I32, I32],
+    ),
     "wxx_matmul_tri": (I32, [P, P, P, I64, I64, I64, I64, I64, I64, I32, I32, I32]),
     # convolution / pooling
     "wxx_conv2d": (I32, [P, P, P, P] + [I64] * 13),

@@ -47,6 +47,9 @@ int set_error(int code, const char* fmt, ...);
 void* scratch_alloc(size_t bytes);   // stream-ordered temporary from the cache
 void scratch_free(void* p);
 int num_cus();
+// Looks up the device address of the allocation-free GEMM's scratch array on
+// `device` (which must be current); called once per device by wxx_init.
+int gemm_noalloc_setup(int device);
 
 constexpr int kMaxRank = 6;
 

@@ -63,6 +63,11 @@ struct GemmArgs {
   // pairs of row tiles and the workgroup of pair p runs tiles p and T - 1 - p:
   // every workgroup then has the same T + 1 chunks of work.
   int pair_m;
+  // Host side only (no kernel reads them): a caller-provided buffer for the
+  // split-K partials, used instead of an allocation when ws != nullptr, and
+  // its capacity in floats.
+  float* ws;
+  int64_t ws_floats;
 };
 
 constexpr int kGroupM = 8;
@@ -636,8 +641,21 @@ int launch_cfg(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits = 1) {
   splits = (int)((g.K + kps - 1) / kps);
   GemmArgs p = g;
   const int64_t n = g.M * g.N * batch;
-  float* part = (float*)wxx::scratch_alloc(sizeof(float) * (size_t)n * splits);
-  if (!part) return wxx::set_error(WXX_E_OOM, "GEMM split-K partials");
+  float* part;
+  if (g.ws) {
+    // every split writes every element of its partial (splits were
+    // recounted above so none has an empty K range): nothing to clear
+    if (n * splits > g.ws_floats)
+      return wxx::set_error(WXX_E_RANGE,
+                            "GEMM split-K partials need %lld floats (%lld x %d splits); the "
+                            "allocation-free scratch holds %lld",
+                            (long long)(n * splits), (long long)n, splits,
+                            (long long)g.ws_floats);
+    part = g.ws;
+  } else {
+    part = (float*)wxx::scratch_alloc(sizeof(float) * (size_t)n * splits);
+    if (!part) return wxx::set_error(WXX_E_OOM, "GEMM split-K partials");
+  }
   p.C = part;
   p.ldc = g.N;
   p.sC = g.M * g.N;
@@ -651,7 +669,7 @@ int launch_cfg(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits = 1) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) rc = wxx::set_error(WXX_E_HIP, "split-K reduce: %s", hipGetErrorString(e));
   }
-  wxx::scratch_free(part);
+  if (!g.ws) wxx::scratch_free(part);
   return rc;
 }
 
@@ -705,7 +723,8 @@ inline bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 namespace {
 int matmul_impl(const float* A, const float* B, const float* bias, float* C, int64_t M, int64_t N,
                 int64_t K, int64_t batch, int64_t sA, int64_t sB, int64_t sBias, int bias_mode,
-                int transpose_A, int transpose_B, int tile, int tri);
+                int transpose_A, int transpose_B, int tile, int tri, float* ws = nullptr,
+                int64_t ws_floats = 0);
 }  // namespace
 
 WXX_API int wxx_matmul_add(const float* A, const float* B, const float* bias, float* C,
@@ -737,10 +756,67 @@ WXX_API int wxx_matmul_tri(const float* A, const float* B, float* C, int64_t M, 
                      tri);
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free variant of wxx_matmul_add, for callers that cannot allocate
+// device memory (code under HIP graph capture, tight serving loops): its only
+// temporary, the split-K partials, lives in this fixed array instead of the
+// caching allocator.  Every GPU that loads the library holds its own copy
+// (64 MiB) until the process ends.  In host code `scratch` names a host-side
+// stand-in, never the device memory: the device address is looked up once
+// per device with hipGetSymbolAddress (wxx::gemm_noalloc_setup, run by
+// wxx_init with that device current) and only that address is used.
+constexpr int64_t kNoAllocScratchFloats = int64_t(16) << 20;
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+namespace {
+constexpr int kMaxDevices = 64;
+float* g_scratch_dev[kMaxDevices] = {};
+}  // namespace
+
+namespace wxx {
+int gemm_noalloc_setup(int device) {
+  if (device < 0 || device >= kMaxDevices)
+    return set_error(WXX_E_ARG, "device %d beyond the %d the library tracks", device,
+                     kMaxDevices);
+  if (g_scratch_dev[device]) return WXX_OK;
+  void* p = nullptr;
+  hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p)
+    return set_error(WXX_E_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+  g_scratch_dev[device] = (float*)p;
+  return WXX_OK;
+}
+}  // namespace wxx
+
+// Same arguments, kernels and results as wxx_matmul_add (bit for bit: the
+// tile and split choice is the same), but allocates nothing: a call whose
+// split-K partials would exceed the scratch (16 Mi floats) fails with
+// WXX_E_RANGE before anything is enqueued.  All calls on a GPU share its one
+// scratch array: calls that overlap on one GPU (other streams or processes
+// running the library's stream concurrently) race.  The partials of each
+// split are written in full before they are read, so nothing in the scratch
+// has to start at zero and a call never depends on an earlier call's
+// contents.
+WXX_API int wxx_matmul_add_noalloc(const float* A, const float* B, const float* bias, float* C,
+                                   int64_t M, int64_t N, int64_t K, int64_t batch, int64_t sA,
+                                   int64_t sB, int64_t sBias, int bias_mode, int transpose_A,
+                                   int transpose_B, int tile) {
+  WXX_CHECK_INIT();
+  int dev = -1;
+  WXX_HIP(hipGetDevice(&dev));
+  float* ws = (dev >= 0 && dev < kMaxDevices) ? g_scratch_dev[dev] : nullptr;
+  if (!ws)
+    return wxx::set_error(WXX_E_INIT, "no allocation-free scratch on device %d (wxx_init "
+                          "sets it up)", dev);
+  return matmul_impl(A, B, bias, C, M, N, K, batch, sA, sB, sBias, bias_mode, transpose_A,
+                     transpose_B, tile, 0, ws, kNoAllocScratchFloats);
+}
+
 namespace {
 int matmul_impl(const float* A, const float* B, const float* bias, float* C, int64_t M, int64_t N,
                 int64_t K, int64_t batch, int64_t sA, int64_t sB, int64_t sBias, int bias_mode,
-                int transpose_A, int transpose_B, int tile, int tri) {
+                int transpose_A, int transpose_B, int tile, int tri, float* ws,
+                int64_t ws_floats) {
   WXX_CHECK_INIT();
   WXX_REQUIRE(A && B && C, "null pointer");
   WXX_REQUIRE(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "negative GEMM dims");
@@ -767,6 +843,9 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
   g.bias_mode = bias_mode;
   g.bias_rows = M;
   g.tri = tri;
+  g.pair_m = 0;
+  g.ws = ws;
+  g.ws_floats = ws_floats;
   int64_t nb = batch;
   // Fold the batch into M when B is shared and A's rows are contiguous across
   // batches: one larger GEMM fills the GPU better than `batch` small ones.

@@ -158,6 +158,10 @@ WXX_API int wxx_init(int device) {
     g_stage_used[i] = false;
   }
   for (int i = 0; i < kTimers; ++i) WXX_HIP(hipEventCreate(&g_timer[i]));
+  {
+    const int rc = wxx::gemm_noalloc_setup(device);
+    if (rc != WXX_OK) return rc;
+  }
   g_device = device;
   g_init = true;
   return WXX_OK;
