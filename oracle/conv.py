@@ -28,17 +28,17 @@ def conv_out(H, W, KH, KW, stride, padding, dilation):
     return (H + 2 * ph - dh * (KH - 1) - 1) // sh + 1, (W + 2 * pw - dw * (KW - 1) - 1) // sw + 1
 
 
-def im2col(X, KH, KW, stride, padding, dilation):
+def im2col(X, KH, KW, stride, padding, dilation, dtype=np.float64):
     """(B*Ho*Wo, Cin*KH*KW) patch matrix, zero outside the input."""
-    X = np.asarray(X, np.float64)
+    X = np.asarray(X, dtype)
     B, Cin, H, W = X.shape
     sh, sw = stride
     ph, pw = padding
     dh, dw = dilation
     Ho, Wo = conv_out(H, W, KH, KW, stride, padding, dilation)
-    Xp = np.zeros((B, Cin, H + 2 * ph + dh * KH + sh, W + 2 * pw + dw * KW + sw))
+    Xp = np.zeros((B, Cin, H + 2 * ph + dh * KH + sh, W + 2 * pw + dw * KW + sw), dtype)
     Xp[:, :, ph:ph + H, pw:pw + W] = X
-    cols = np.empty((B, Ho, Wo, Cin, KH, KW))
+    cols = np.empty((B, Ho, Wo, Cin, KH, KW), dtype)
     for kh in range(KH):
         for kw in range(KW):
             h0, w0 = kh * dh, kw * dw
@@ -47,27 +47,30 @@ def im2col(X, KH, KW, stride, padding, dilation):
     return cols.reshape(B * Ho * Wo, Cin * KH * KW), (Ho, Wo)
 
 
-def conv2d(X, Wt, stride, padding, dilation, bias=None):
+def conv2d(X, Wt, stride, padding, dilation, bias=None, dtype=np.float64):
+    """``dtype=np.float32`` evaluates the same sums in single precision (an
+    fp32 BLAS product): the rounding a float32 evaluation carries, against
+    which a device result's error is judged."""
     B = X.shape[0]
     Cout, Cin, KH, KW = Wt.shape
-    cols, (Ho, Wo) = im2col(X, KH, KW, stride, padding, dilation)
-    y = cols @ np.asarray(Wt, np.float64).reshape(Cout, -1).T  # (B Ho Wo, Cout)
+    cols, (Ho, Wo) = im2col(X, KH, KW, stride, padding, dilation, dtype)
+    y = cols @ np.asarray(Wt, dtype).reshape(Cout, -1).T  # (B Ho Wo, Cout)
     if bias is not None:
-        y = y + np.asarray(bias, np.float64)[None, :]
+        y = y + np.asarray(bias, dtype)[None, :]
     return y.reshape(B, Ho, Wo, Cout).transpose(0, 3, 1, 2)
 
 
-def conv2ddx(dY, Wt, stride, padding, dilation, Xshape):
+def conv2ddx(dY, Wt, stride, padding, dilation, Xshape, dtype=np.float64):
     """Literal restatement of the conv2ddx gather (vectorised over b, ci)."""
-    dY = np.asarray(dY, np.float64)
-    Wt = np.asarray(Wt, np.float64)
+    dY = np.asarray(dY, dtype)
+    Wt = np.asarray(Wt, dtype)
     B, Cin, H, W = Xshape
     Cout, _, KH, KW = Wt.shape
     sh, sw = stride
     ph, pw = padding
     dh, dw = dilation
     Ho, Wo = dY.shape[2], dY.shape[3]
-    dX = np.zeros((B, Cin, H, W))
+    dX = np.zeros((B, Cin, H, W), dtype)
     for kh in range(KH):
         for kw in range(KW):
             for ih in range(H):
@@ -84,10 +87,10 @@ def conv2ddx(dY, Wt, stride, padding, dilation, Xshape):
     return dX
 
 
-def conv2ddw(dY, X, stride, padding, dilation, wshape):
+def conv2ddw(dY, X, stride, padding, dilation, wshape, dtype=np.float64):
     Cout, Cin, KH, KW = wshape
-    cols, _ = im2col(X, KH, KW, stride, padding, dilation)
-    g = np.asarray(dY, np.float64).transpose(0, 2, 3, 1).reshape(-1, Cout)
+    cols, _ = im2col(X, KH, KW, stride, padding, dilation, dtype)
+    g = np.asarray(dY, dtype).transpose(0, 2, 3, 1).reshape(-1, Cout)
     return (g.T @ cols).reshape(wshape)
 
 
@@ -247,17 +250,17 @@ def conv2dtranspose(X, Wt, stride, padding, dilation, out_hw, bias=None):
     return y
 
 
-def conv2dtranspose_dx(dY, Wt, stride, padding, dilation, Xshape):
+def conv2dtranspose_dx(dY, Wt, stride, padding, dilation, Xshape, dtype=np.float64):
     """dX[b,ci,h,w] = sum_{co,kh,kw} dY[b,co,h sh - ph + kh dh, ...] W[ci,co,kh,kw]."""
-    dY = np.asarray(dY, np.float64)
-    Wt = np.asarray(Wt, np.float64)
+    dY = np.asarray(dY, dtype)
+    Wt = np.asarray(Wt, dtype)
     B, Cin, H, W = Xshape
     _, Cout, KH, KW = Wt.shape
     sh, sw = stride
     ph, pw = padding
     dh, dw = dilation
     Ho, Wo = dY.shape[2], dY.shape[3]
-    dX = np.zeros((B, Cin, H, W))
+    dX = np.zeros((B, Cin, H, W), dtype)
     for kh in range(KH):
         for kw in range(KW):
             for h in range(H):

@@ -19,6 +19,14 @@ with the semantics of the kernels it calls:
 
 Gradients are torch's float64 autograd of that forward; torch's max-pool
 gradient also goes to the first maximum of the window in row-major order.
+
+``forced`` replays another evaluation's discrete decisions: the ReLU masks
+(in call order) and the max-pool indices (flat input indices, the
+reference's u32 index format).  An fp32 evaluation can see a ReLU input or a
+max-pool near-tie on the other side of 0 / of the tie than float64 does; at
+batch 128 one such flip moves a whole batch element's gradient.  With the
+decisions fixed the remaining differences are rounding alone, and the
+decisions themselves are compared with the oracle's own separately.
 Pinned in tests/test_oracle_models.py against the numpy per-op oracles
 (oracle/conv.py, oracle/norms.py) and finite differences of the loss.
 """
@@ -45,14 +53,39 @@ def batchnorm_train(x, gamma, beta, rm, rv, eps=1e-5, momentum=0.1):
     return y, rm, rv
 
 
-def _block(P, S, p, x, stride, has_shortcut):
+class _Decisions:
+    """The ReLU inputs / max-pool inputs seen (``seen``) and, when replaying
+    (``forced``), the masks and indices to use instead of the oracle's own."""
+
+    def __init__(self, forced=None):
+        self.relu_masks = list(forced["relu"]) if forced else None
+        self.pool_idx = forced["pool"] if forced else None
+        self.relu_inputs = []
+        self.pool_inputs = []
+
+    def relu(self, x):
+        self.relu_inputs.append(x.detach())
+        if self.relu_masks is None:
+            return TF.relu(x)
+        mask = torch.as_tensor(np.asarray(self.relu_masks.pop(0)), dtype=x.dtype)
+        return x * mask
+
+    def maxpool(self, x):
+        self.pool_inputs.append(x.detach())
+        if self.pool_idx is None:
+            return TF.max_pool2d(x, 3, stride=2, padding=1)
+        idx = torch.as_tensor(np.asarray(self.pool_idx, np.int64))
+        return torch.take(x, idx)
+
+
+def _block(P, S, p, x, stride, has_shortcut, D):
     out = TF.conv2d(x, P[p + "conv1.W"], stride=stride, padding=1)
     y, rm, rv = batchnorm_train(out, P[p + "bn1.weight"], P[p + "bn1.bias"],
                                 S[p + "bn1.running_mean"], S[p + "bn1.running_std"])
     # second evaluation of bn1 on the same input (reference resnet.py:33)
     y, rm, rv = batchnorm_train(out, P[p + "bn1.weight"], P[p + "bn1.bias"], rm, rv)
     S[p + "bn1.running_mean"], S[p + "bn1.running_std"] = rm, rv
-    out = TF.relu(y)
+    out = D.relu(y)
     out = TF.conv2d(out, P[p + "conv2.W"], stride=1, padding=1)
     out, S[p + "bn2.running_mean"], S[p + "bn2.running_std"] = batchnorm_train(
         out, P[p + "bn2.weight"], P[p + "bn2.bias"], S[p + "bn2.running_mean"],
@@ -64,36 +97,44 @@ def _block(P, S, p, x, stride, has_shortcut):
             S[p + "shortcut.1.running_mean"], S[p + "shortcut.1.running_std"])
     else:
         sc = x
-    return TF.relu(out + sc)
+    return D.relu(out + sc)
 
 
-def resnet18_forward(P, S, x):
+def resnet18_forward(P, S, x, D=None):
     """Logits of ResNet18 on x (B, 3, H, W); ``S`` (running statistics,
-    name -> float64 tensor) is updated in place as the train forward does."""
+    name -> float64 tensor) is updated in place as the train forward does;
+    ``D`` (a _Decisions) records, or replays, the ReLU and max-pool choices."""
+    D = D or _Decisions()
     out, S["bn1.running_mean"], S["bn1.running_std"] = batchnorm_train(
         TF.conv2d(x, P["conv1.W"], stride=2, padding=3), P["bn1.weight"], P["bn1.bias"],
         S["bn1.running_mean"], S["bn1.running_std"])
-    out = TF.max_pool2d(TF.relu(out), 3, stride=2, padding=1)
+    out = D.maxpool(D.relu(out))
     cin = 64
     for li, cout in enumerate((64, 128, 256, 512), start=1):
         for bi in range(2):
             stride = 2 if (bi == 0 and li > 1) else 1
             has_sc = bi == 0 and (stride != 1 or cin != cout)
-            out = _block(P, S, f"layer{li}.{bi}.", out, stride, has_sc)
+            out = _block(P, S, f"layer{li}.{bi}.", out, stride, has_sc, D)
             cin = cout
     out = TF.adaptive_avg_pool2d(out, 1).reshape(out.shape[0], -1)
     return out @ P["fc.weight"] + P["fc.bias"]
 
 
-def resnet18_loss_and_grads(params, stats, x, labels, dtype=np.float64):
+def resnet18_loss_and_grads(params, stats, x, labels, dtype=np.float64, forced=None,
+                            record=None):
     """(loss, {name: grad}, {name: new running stat}, logits) of one train
     step.  ``dtype=np.float32`` runs the same restatement in single
-    precision: the rounding error of an fp32 evaluation of this network,
-    against which a device result's error is judged."""
+    precision.  ``forced`` = {"relu": masks, "pool": indices} replays those
+    decisions; ``record`` (a dict) receives the ReLU and max-pool inputs this
+    evaluation saw ("relu_inputs", "pool_input")."""
     torch.set_num_threads(max(1, min(16, torch.get_num_threads())))
     P = {k: torch.tensor(np.asarray(v, dtype), requires_grad=True) for k, v in params.items()}
     S = {k: torch.tensor(np.asarray(v, dtype)) for k, v in stats.items()}
-    logits = resnet18_forward(P, S, torch.tensor(np.asarray(x, dtype)))
+    D = _Decisions(forced)
+    logits = resnet18_forward(P, S, torch.tensor(np.asarray(x, dtype)), D)
+    if record is not None:
+        record["relu_inputs"] = [t.numpy() for t in D.relu_inputs]
+        record["pool_input"] = D.pool_inputs[0].numpy()
     tg = torch.as_tensor(np.asarray(labels, np.int64))
     loss = (torch.logsumexp(logits, 1) - logits[torch.arange(logits.shape[0]), tg]).mean()
     loss.backward()

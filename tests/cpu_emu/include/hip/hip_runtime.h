@@ -124,6 +124,9 @@ inline void __builtin_amdgcn_global_load_lds(const void* src, void* lds, unsigne
   std::memcpy(static_cast<char*>(lds) + offset + (size_t)size * wxx_emu::lane(), src, size);
 }
 inline void __builtin_amdgcn_s_waitcnt(int) {}
+// the inline-asm form of a dword global_load_lds (wxx_amd/csrc/common.h)
+#define WXX_LDS_DMA_DWORD(src, dst) __builtin_amdgcn_global_load_lds((src), (dst), 4, 0, 0)
+#define WXX_S_BARRIER() __syncthreads()
 
 inline float __int_as_float(int v) { float f; std::memcpy(&f, &v, 4); return f; }
 inline float __uint_as_float(uint32_t v) { float f; std::memcpy(&f, &v, 4); return f; }

@@ -12,6 +12,7 @@ import numpy as np
 import pytest
 
 from conftest import rng
+from oracle import conv as oc
 from oracle import models as om
 
 pytestmark = pytest.mark.gpu
@@ -462,29 +463,57 @@ def _walk(module, prefix=""):
 
 def _within_error_floor(got, want64, ref32, name, c=4.0, rtol=1e-4, atol=1e-5):
     """|got - want64| <= atol + rtol |want64| + c |ref32 - want64| element by
-    element, where ref32 is the same restated network evaluated in float32:
-    the device result may miss the float64 value by no more than the
-    north star's bar plus c times what single precision itself misses by."""
+    element, where ref32 is the same restated computation in float32 (same
+    discrete decisions): the device may miss the float64 value by the north
+    star's bar plus c times what single precision itself misses by."""
     got, w, f = (np.asarray(a, np.float64) for a in (got, want64, ref32))
     err, floor = np.abs(got - w), np.abs(f - w)
     bad = err > atol + rtol * np.abs(w) + c * floor
     assert not bad.any(), (f"{name}: {int(bad.sum())} of {bad.size} elements beyond the fp32 "
                            f"error floor; max err {err.max():.3g}, fp32 max err {floor.max():.3g}")
+    return err.max(), floor.max()
 
 
-def test_resnet18_config3_train_step_matches_oracle(device):
+def test_resnet18_config3_train_step_matches_oracle(device, monkeypatch):
     # BASELINE config 3: ResNet18(10), batch 128 x 3 x 32 x 32, CCELoss;
     # logits, loss, every gradient and every BatchNorm running statistic after
-    # the training forward, against the float64 restatement oracle/resnet.py.
-    # Gradients are judged against the fp32 error floor: at this depth a ReLU
-    # whose input lies within fp32 rounding of 0 (layer4 runs at 1 x 1 with
-    # batch 128) flips between single and double precision and moves a whole
-    # batch element's gradient; the same restatement run in float32 shows the
-    # same flip, and the device must agree with float64 as well as it does.
+    # the training forward, against the float64 restatement oracle/resnet.py,
+    # element by element at rtol 1e-4 / atol 1e-5.
+    # The oracle replays the device's discrete decisions (ReLU masks, max-pool
+    # indices): an fp32 ReLU input or max-pool near-tie within rounding of the
+    # other side flips between single and double precision and, at batch 128
+    # with layer4 at 1 x 1, moves a whole batch element's gradient.  Those
+    # decisions are checked on their own: each one that differs from the
+    # oracle's own float64 choice must be a near-tie.
     from oracle import resnet as orn
+    from wxx_amd.autograd import convolution as ac
+    from wxx_amd.autograd import pointwise as ap
 
     wxx = W()
+    relu_in, pool = [], {}
+    relu_fwd = ap.relu.forward
+
+    def recording_relu(self, t):
+        relu_in.append(t.numpy())
+        return relu_fwd(self, t)
+
+    pool_fwd = ac.maxpooling2d._fwd
+
+    def recording_pool(*args):
+        out, idx = pool_fwd(*args)
+        pool["idx"] = idx.numpy()
+        return out, idx
+
+    monkeypatch.setattr(ap.relu, "forward", recording_relu)
+    monkeypatch.setattr(ac.maxpooling2d, "_fwd", staticmethod(recording_pool))
+
     model = wxx.nn.ResNet18(num_classes=10)
+    r = rng(32)
+    state = {n: (r.normal(0, np.sqrt(2.0 / (np.prod(a.shape[1:]))), a.shape) if a.ndim == 4
+                 else (1.0 + r.normal(0, 0.1, a.shape) if n.endswith("weight") and a.ndim == 1
+                       else r.normal(0, 0.1, a.shape))).astype(np.float32)
+             for n, a in model.state_dict().items()}
+    model.load_state_dict(state)
     params = {n: p.numpy().astype(np.float64) for n, p in model.named_parameters()}
     stats = {}
     for name, m in _walk(model):
@@ -496,13 +525,34 @@ def test_resnet18_config3_train_step_matches_oracle(device):
     logits = model(up(x))
     loss = wxx.nn.CCELoss()(logits, up_u32(y))
     loss.backward()
-    ol, og, ostats, ologits = orn.resnet18_loss_and_grads(params, stats, x, y)
-    fl, fg, fstats, flogits = orn.resnet18_loss_and_grads(params, stats, x, y, dtype=np.float32)
+    assert len(relu_in) == 17 and "idx" in pool
+
+    forced = {"relu": [a > 0 for a in relu_in], "pool": pool["idx"]}
+    seen = {}
+    ol, og, ostats, ologits = orn.resnet18_loss_and_grads(params, stats, x, y, forced=forced,
+                                                          record=seen)
+    fl, fg, fstats, flogits = orn.resnet18_loss_and_grads(params, stats, x, y, np.float32,
+                                                          forced=forced)
+    # the device's decisions against the oracle's own float64 ones
+    for k, (pre64, mask) in enumerate(zip(seen["relu_inputs"], forced["relu"])):
+        differ = (pre64 > 0) != mask
+        scale = np.abs(pre64).max()
+        assert np.all(np.abs(pre64[differ]) <= 1e-5 * scale), f"relu {k}: a decision far from 0"
+        assert differ.sum() <= 4, f"relu {k}: {int(differ.sum())} flipped decisions"
+    xin = seen["pool_input"].reshape(-1)
+    _, own_idx = oc.pool2d(seen["pool_input"], (3, 3), (2, 2), (1, 1), False)
+    differ = own_idx != pool["idx"]
+    assert differ.sum() <= 4
+    assert np.all(np.abs(xin[own_idx[differ]] - xin[pool["idx"][differ]])
+                  <= 1e-5 * np.abs(xin).max())
+
+    # values: through 20 layers of fp32 arithmetic and batch statistics some
+    # elements sit at the single-precision floor rather than inside the bar,
+    # so the bar is widened by what the float32 restatement itself misses by
     _within_error_floor(logits.numpy(), ologits, flogits, "logits")
     assert abs(float(loss.numpy().reshape(-1)[0]) - ol) <= 1e-5 * abs(ol)
     for n, p in model.named_parameters():
         _within_error_floor(p.grad.numpy(), og[n], fg[n], n)
-    # the running statistics do not go through any ReLU decision: plain bar
     for name, m in _walk(model):
         if hasattr(m, "running_mean"):
             _elementwise(m.running_mean.numpy(), ostats[name + ".running_mean"], name + " mean")

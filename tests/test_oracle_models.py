@@ -262,3 +262,25 @@ def test_hyena_oracle_gradient_by_finite_differences(tie, cap):
         lg = oh.hyena_forward({k: torch.tensor(v) for k, v in P.items()}, ids, L, order,
                               row_cap=cap, tie_weights=tie).detach().numpy().reshape(-1, V)
         assert np.all(lg[cap:] == 0)
+
+
+def test_resnet_oracle_replaying_its_own_decisions_changes_nothing():
+    P, S = _resnet_params()
+    r = rng(11)
+    x = r.standard_normal((4, 3, 32, 32))
+    y = r.integers(0, 5, 4)
+    seen = {}
+    l1, g1, _, lg1 = orn.resnet18_loss_and_grads(P, S, x, y, record=seen)
+    _, idx = oc.pool2d(seen["pool_input"], (3, 3), (2, 2), (1, 1), False)
+    forced = {"relu": [a > 0 for a in seen["relu_inputs"]], "pool": idx}
+    l2, g2, _, lg2 = orn.resnet18_loss_and_grads(P, S, x, y, forced=forced)
+    assert len(seen["relu_inputs"]) == 17
+    assert l1 == l2
+    assert np.array_equal(lg1, lg2)
+    for k in g1:
+        assert np.array_equal(g1[k], g2[k]), k
+    # a planted wrong decision changes the gradients
+    bad = {"relu": [m.copy() for m in forced["relu"]], "pool": idx}
+    bad["relu"][3].reshape(-1)[:50] ^= True
+    _, g3, _, _ = orn.resnet18_loss_and_grads(P, S, x, y, forced=bad)
+    assert any(not np.array_equal(g1[k], g3[k]) for k in g1)

@@ -23,6 +23,35 @@
 #define WXX_OPAQUE(x) asm volatile("" : "+v"(x))
 #endif
 
+// A bare workgroup barrier (s_barrier) that is only a compiler memory
+// clobber, not a memory fence: __syncthreads() also waits for every
+// outstanding global load (vmcnt(0)), which would drain a pipeline of loads
+// that a kernel keeps in flight across the barrier on purpose.
+#ifndef WXX_S_BARRIER
+#define WXX_S_BARRIER() asm volatile("s_barrier" ::: "memory")
+#endif
+
+// One global_load_lds_dword: every lane's 4 bytes at `src` (any address)
+// land at the wave-uniform LDS address `lds_dst` + 4 * lane.  Written as
+// inline asm so that the compiler does not track it as an LDS store: a
+// kernel that keeps several chunks of these in flight waits for them itself
+// (s_waitcnt vmcnt, which counts them in issue order) instead of getting the
+// full vmcnt(0) the compiler inserts before any LDS read it cannot prove
+// disjoint.  M0 carries the LDS address; the kernels that use this helper
+// have no other M0 user.
+#ifndef WXX_LDS_DMA_DWORD
+#define WXX_LDS_DMA_DWORD wxx_lds_dma_dword
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved; see above
+__device__ __forceinline__ void wxx_lds_dma_dword(const float* src, float* lds_dst) {
+  const unsigned lds = __builtin_amdgcn_readfirstlane(
+      (unsigned)(uintptr_t)(__attribute__((address_space(3))) float*)lds_dst);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+#endif
+
 WXX_API int wxx_fill_u32(void* dst, int64_t n, uint32_t bits);
 WXX_API int wxx_h2d(void* dst, const void* src, size_t bytes);
 WXX_API void* wxx_alloc(size_t bytes);

@@ -20,8 +20,8 @@
 // Q is gathered on the fly into k-major LDS tiles (never materialised in
 // HBM).  Each lane owns one column j for the whole K loop, so its (b, oh, ow)
 // or (ci, kh, kw) decomposition is computed once; the k decomposition is
-// wave-uniform and runs on the scalar unit.  Tiles are BI x BJ (64 or 128)
-// with 4 waves of v_mfma_f32_32x32x2f32 and register-staged double buffering.
+// wave-uniform and runs on the scalar unit.  Tiles are BI x BJ with 4 waves
+// of v_mfma_f32_32x32x2f32, gathered straight into a 3-stage LDS ring.
 // When the tile grid is too small to fill 256 CUs (ResNet's deep layers, and
 // every dW whose K = B Ho Wo is long) the K range is split: each split writes
 // a partial tile and a second pass adds the partials in split order, so the
@@ -46,115 +46,202 @@ struct ConvArgs {
   int tiles_i, tiles_j;
 };
 
-constexpr int BK = 16;
-constexpr int kPad = 4;
+// ---------------------------------------------------------------------------
+// The implicit-GEMM tile kernel.
+//
+// Out[i][j] = sum_k P[i][k] Q[k][j] over one K range (a split), for a BI x BJ
+// output tile with 4 waves of v_mfma_f32_32x32x2f32 (each wave a BI/2 x BJ/2
+// quarter).  Both operand tiles are gathered straight into LDS with
+// global_load_lds_dword: one wave instruction takes one 4-byte word per lane
+// from any 64 addresses and writes them as 64 consecutive LDS words, so a
+// tile row k (BI or BJ words, k-major layout) is BI/64 or BJ/64
+// instructions, no VGPR holds the data on its way and no ds_write runs.
+// Elements outside the tensor (padding, ragged tile edges, the end of the K
+// range) are taken from a word of zeros.  A ring of three LDS stages keeps
+// two chunks of loads in flight while the matrix cores work on the third: at
+// chunk c a wave waits until only its loads of chunk c + 1 are outstanding
+// (s_waitcnt vmcnt, loads complete in order), one barrier makes every wave's
+// part of chunk c visible and frees the stage of chunk c - 1, which then
+// receives chunk c + 2.
+//
+// The k index of a row decomposes as k = (t0 R1 + t1) R2 + t2 with
+// (t0, t1, t2) = (ci, kh, kw) for the forward, (co, kh, kw) for dX and
+// (b, oh, ow) for dW.  A wave loads 8 consecutive rows per chunk, so it
+// carries the decomposition of its first row on the scalar unit and steps it
+// (by 1 per row, by BK per chunk) with carries instead of dividing.
+constexpr int BK = 32;
+constexpr int kStages = 3;
+constexpr int kRowsPerWave = BK / 4;
+
+__device__ const float g_conv_zero[4] = {0.f, 0.f, 0.f, 0.f};
+
+// (t0, t1, t2) digits of k in radices (R1, R2) and the step arithmetic.
+struct KDigits {
+  int t0, t1, t2;
+};
+
+__device__ __forceinline__ void kd_step1(KDigits& d, int R1, int R2) {
+  if (++d.t2 == R2) {
+    d.t2 = 0;
+    if (++d.t1 == R1) {
+      d.t1 = 0;
+      ++d.t0;
+    }
+  }
+}
+
+// d += n where n = (n0 R1 + n1) R2 + n2 with n1 < R1, n2 < R2.
+__device__ __forceinline__ void kd_add(KDigits& d, int n0, int n1, int n2, int R1, int R2) {
+  d.t2 += n2;
+  int c = 0;
+  if (d.t2 >= R2) {
+    d.t2 -= R2;
+    c = 1;
+  }
+  d.t1 += n1 + c;
+  c = 0;
+  if (d.t1 >= R1) {
+    d.t1 -= R1;
+    c = 1;
+  }
+  d.t0 += n0 + c;
+}
 
 template <int MODE, int BI, int BJ>
-__global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
-  constexpr int WI = BI / 2, WJ = BJ / 2;  // 2 x 2 waves
+__global__ __launch_bounds__(256) void conv_lds_kernel(ConvArgs a) {
+  constexpr int WI = BI / 2, WJ = BJ / 2;
   constexpr int TM = WI / 32, TN = WJ / 32;
-  constexpr int LP = BI + kPad, LQ = BJ + kPad;
-  constexpr int PPT = BI * BK / 256;  // P elements per thread per chunk
-  constexpr int QPT = BJ * BK / 256;  // Q elements per thread per chunk
-  constexpr int P_TPR = BK / PPT;     // threads per P row
-  static_assert(PPT >= 1 && QPT >= 1 && BK % PPT == 0, "tile shape");
-
-  __shared__ __attribute__((aligned(16))) float Ps[2][BK * LP];
-  __shared__ __attribute__((aligned(16))) float Qs[2][BK * LQ];
+  constexpr int LP = BI + 2, LQ = BJ + 2;  // rows k and k + 16 land 32 banks apart
+  constexpr int HP = BI / 64, HQ = BJ / 64;  // instructions per tile row
+  // separate objects per stage, so the compiler can tell the loads into one
+  // stage from the reads of another
+  __shared__ float P0[BK * LP], P1[BK * LP], P2[BK * LP];
+  __shared__ float Q0[BK * LQ], Q1[BK * LQ], Q2[BK * LQ];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wi = wave >> 1, wj = wave & 1;
 
-  // tile ids: consecutive blocks walk j first (neighbouring j tiles share P)
   const int tile = blockIdx.x;
-  const int ti = tile / a.tiles_j, tj = tile % a.tiles_j;
+  const int ti = tile / a.tiles_j, tj = tile - (tile / a.tiles_j) * a.tiles_j;
   const int i0 = ti * BI, j0 = tj * BJ;
   const int z = blockIdx.y;
   const int kbeg = z * a.kps;
   const int kend = min(a.K, kbeg + a.kps);
+  const int nk = (kend - kbeg + BK - 1) / BK;
 
-  const int KK = a.KH * a.KW;
-  const int HW = a.H * a.W, HoWo = a.Ho * a.Wo;
+  const int HW = a.H * a.W, HoWo = a.Ho * a.Wo, KK = a.KH * a.KW;
+  // radices of k's digits
+  const int R1 = MODE == kDw ? a.Ho : a.KH;
+  const int R2 = MODE == kDw ? a.Wo : a.KW;
+  const int R12 = R1 * R2;
+  const float* __restrict__ zero = g_conv_zero;
 
-  // ---- per-thread P row and Q column ------------------------------------
-  const int p_i = i0 + tid / P_TPR;
-  const int p_k = (tid % P_TPR) * PPT;
-  const bool p_ok = p_i < a.I;
-  const int q_j = j0 + tid % BJ;
-  const int q_k = (tid / BJ) * QPT;  // wave-uniform when BJ >= 64
-  const bool q_ok = q_j < a.J;
-
-  // Q column decomposition (constant over K)
-  int qb = 0, qy = 0, qx = 0;     // forward / dX: (b, y, x) of column j
-  int qci = 0, qkh = 0, qkw = 0;  // dW: (ci, kh, kw) of column j
-  if (MODE == kDw) {
-    qci = q_j / KK;
-    const int r = q_j - qci * KK;
-    qkh = r / a.KW;
-    qkw = r - qkh * a.KW;
-  } else {
-    const int S = MODE == kFwd ? HoWo : HW;
-    const int SW = MODE == kFwd ? a.Wo : a.W;
-    qb = q_j / S;
-    const int r = q_j - qb * S;
-    qy = r / SW;
-    qx = r - qy * SW;
+  // ---- per-lane column data (constant over K) ------------------------------
+  // P: lane's row i of each instruction half; Q: lane's column j.
+  int p_i[HP];
+  int64_t p_off[HP];
+#pragma unroll
+  for (int h = 0; h < HP; ++h) {
+    p_i[h] = i0 + 64 * h + lane;
+    const int64_t stride = MODE == kFwd ? a.K : (MODE == kDx ? KK : HoWo);
+    p_off[h] = (int64_t)p_i[h] * stride;
+  }
+  // Q column: forward (b, oh, ow) -> base offset and input corner;
+  //           dX (b, y, x) of dX;  dW (ci, kh, kw).
+  int q_ok[HQ], q_b[HQ], q_y[HQ], q_x[HQ];
+  int64_t q_off[HQ];
+#pragma unroll
+  for (int h = 0; h < HQ; ++h) {
+    const int j = j0 + 64 * h + lane;
+    q_ok[h] = j < a.J;
+    const int jj = q_ok[h] ? j : 0;
+    if (MODE == kDw) {
+      const int ci = jj / KK, kk = jj - (jj / KK) * KK;
+      const int kh = kk / a.KW, kw = kk - (kk / a.KW) * a.KW;
+      q_b[h] = 0;
+      q_y[h] = kh * a.dh;  // added to the row's oh sh - ph
+      q_x[h] = kw * a.dw;
+      q_off[h] = (int64_t)ci * HW;
+    } else {
+      const int S = MODE == kFwd ? HoWo : HW;
+      const int SW = MODE == kFwd ? a.Wo : a.W;
+      const int b = jj / S, r = jj - (jj / S) * S;
+      const int y = r / SW, x = r - (r / SW) * SW;
+      q_b[h] = b;
+      if (MODE == kFwd) {
+        q_y[h] = y * a.sh - a.ph;
+        q_x[h] = x * a.sw - a.pw;
+        q_off[h] = (int64_t)b * a.Cin * HW;
+      } else {
+        q_y[h] = y + a.ph;
+        q_x[h] = x + a.pw;
+        q_off[h] = (int64_t)b * a.Cout * HoWo;
+      }
+    }
   }
 
-  auto loadP = [&](int k) -> float {
-    if (!p_ok || k >= kend) return 0.f;
-    if (MODE == kFwd) return a.P[(int64_t)p_i * a.K + k];
-    if (MODE == kDx) {
-      const int co = k / KK, kk = k - co * KK;
-      return a.P[((int64_t)co * a.Cin + p_i) * KK + kk];
-    }
-    const int b = k / HoWo, pos = k - b * HoWo;
-    return a.P[((int64_t)b * a.Cout + p_i) * HoWo + pos];
-  };
+  // ---- the wave's first row of the first chunk, as digits ------------------
+  KDigits base;
+  {
+    const int k = kbeg + kRowsPerWave * wave;
+    base.t0 = k / R12;
+    const int r = k - base.t0 * R12;
+    base.t1 = r / R2;
+    base.t2 = r - base.t1 * R2;
+  }
+  // BK as digits, for the per-chunk advance
+  const int n0 = BK / R12, n1 = (BK - n0 * R12) / R2, n2 = BK - n0 * R12 - n1 * R2;
 
-  auto loadQ = [&](int k) -> float {
-    if (!q_ok || k >= kend) return 0.f;
-    if (MODE == kFwd) {
-      const int ci = k / KK, kk = k - ci * KK;
-      const int kh = kk / a.KW, kw = kk - kh * a.KW;
-      const int ih = qy * a.sh - a.ph + kh * a.dh;
-      const int iw = qx * a.sw - a.pw + kw * a.dw;
-      if (ih < 0 || ih >= a.H || iw < 0 || iw >= a.W) return 0.f;
-      return a.Q[(((int64_t)qb * a.Cin + ci) * a.H + ih) * a.W + iw];
+  auto issue = [&](int c, float* ps, float* qs) __attribute__((always_inline)) {
+    KDigits d = base;
+    const int krow0 = kbeg + c * BK + kRowsPerWave * wave;
+#pragma unroll
+    for (int m = 0; m < kRowsPerWave; ++m) {
+      const int k = krow0 + m;
+      const bool kin = k < kend;
+      const int row = kRowsPerWave * wave + m;
+      // P row k
+#pragma unroll
+      for (int h = 0; h < HP; ++h) {
+        const float* src = zero;
+        if (kin && p_i[h] < a.I) {
+          int64_t off;
+          if (MODE == kFwd) off = k;
+          else if (MODE == kDx) off = (int64_t)d.t0 * a.Cin * KK + d.t1 * a.KW + d.t2;
+          else off = (int64_t)d.t0 * a.Cout * HoWo + d.t1 * a.Wo + d.t2;
+          src = a.P + p_off[h] + off;
+        }
+        WXX_LDS_DMA_DWORD(src, ps + row * LP + 64 * h);
+      }
+      // Q row k
+#pragma unroll
+      for (int h = 0; h < HQ; ++h) {
+        const float* src = zero;
+        if (kin && q_ok[h]) {
+          if (MODE == kFwd) {
+            const int iy = q_y[h] + d.t1 * a.dh, ix = q_x[h] + d.t2 * a.dw;
+            if ((unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W)
+              src = a.Q + q_off[h] + (int64_t)d.t0 * HW + iy * a.W + ix;
+          } else if (MODE == kDx) {
+            const int th = q_y[h] - d.t1 * a.dh, tw = q_x[h] - d.t2 * a.dw;
+            if (th >= 0 && tw >= 0) {
+              const int oh = th / a.sh, ow = tw / a.sw;
+              if (oh * a.sh == th && ow * a.sw == tw && oh < a.Ho && ow < a.Wo)
+                src = a.Q + q_off[h] + (int64_t)d.t0 * HoWo + oh * a.Wo + ow;
+            }
+          } else {
+            const int iy = d.t1 * a.sh - a.ph + q_y[h], ix = d.t2 * a.sw - a.pw + q_x[h];
+            if ((unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W)
+              src = a.Q + (int64_t)d.t0 * a.Cin * HW + q_off[h] + iy * a.W + ix;
+          }
+        }
+        WXX_LDS_DMA_DWORD(src, qs + row * LQ + 64 * h);
+      }
+      kd_step1(d, R1, R2);
     }
-    if (MODE == kDx) {
-      const int co = k / KK, kk = k - co * KK;
-      const int kh = kk / a.KW, kw = kk - kh * a.KW;
-      const int th = qy + a.ph - kh * a.dh;
-      const int tw = qx + a.pw - kw * a.dw;
-      if (th < 0 || tw < 0) return 0.f;
-      const int oh = th / a.sh, ow = tw / a.sw;
-      if (oh * a.sh != th || ow * a.sw != tw || oh >= a.Ho || ow >= a.Wo) return 0.f;
-      return a.Q[(((int64_t)qb * a.Cout + co) * a.Ho + oh) * a.Wo + ow];
-    }
-    const int b = k / HoWo, pos = k - b * HoWo;
-    const int oh = pos / a.Wo, ow = pos - oh * a.Wo;
-    const int ih = oh * a.sh - a.ph + qkh * a.dh;
-    const int iw = ow * a.sw - a.pw + qkw * a.dw;
-    if (ih < 0 || ih >= a.H || iw < 0 || iw >= a.W) return 0.f;
-    return a.Q[(((int64_t)b * a.Cin + qci) * a.H + ih) * a.W + iw];
-  };
-
-  float rp[PPT], rq[QPT];
-  auto load_chunk = [&](int k0) {
-#pragma unroll
-    for (int e = 0; e < PPT; ++e) rp[e] = loadP(k0 + p_k + e);
-#pragma unroll
-    for (int e = 0; e < QPT; ++e) rq[e] = loadQ(k0 + q_k + e);
-  };
-  auto store_chunk = [&](int buf) {
-    const int pi = tid / P_TPR, qj = tid % BJ;
-#pragma unroll
-    for (int e = 0; e < PPT; ++e) Ps[buf][(p_k + e) * LP + pi] = rp[e];
-#pragma unroll
-    for (int e = 0; e < QPT; ++e) Qs[buf][(q_k + e) * LQ + qj] = rq[e];
+    kd_add(base, n0, n1, n2, R1, R2);
   };
 
   floatx16 acc[TM][TN];
@@ -170,15 +257,7 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
   const int pa = wi * WI + l32;
   const int qa = wj * WJ + l32;
 
-  const int nk = (kend - kbeg + BK - 1) / BK;
-  load_chunk(kbeg);
-  store_chunk(0);
-  __syncthreads();
-  for (int c = 0; c < nk; ++c) {
-    const int cur = c & 1;
-    if (c + 1 < nk) load_chunk(kbeg + (c + 1) * BK);
-    const float* ps = Ps[cur];
-    const float* qs = Qs[cur];
+  auto compute = [&](const float* ps, const float* qs) __attribute__((always_inline)) {
 #pragma unroll
     for (int s = 0; s < BK / 2; ++s) {
       const int kk = s + half * (BK / 2);
@@ -193,8 +272,36 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
         for (int y = 0; y < TN; ++y)
           acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[x], bf[y], acc[x][y], 0, 0, 0);
     }
-    if (c + 1 < nk) store_chunk(cur ^ 1);
-    __syncthreads();
+  };
+
+  // s_waitcnt with vmcnt = n (expcnt and lgkmcnt left alone): on gfx9 the
+  // vmcnt field is bits 0-3 and 14-15
+  constexpr int kPerChunk = kRowsPerWave * (HP + HQ);  // loads per wave per chunk
+  static_assert(kPerChunk < 64, "vmcnt holds at most 63");
+  constexpr int kWaitOne = 0x0F70 | (kPerChunk & 15) | ((kPerChunk >> 4) << 14);
+
+  // Three stages: chunk c lives in stage c % 3.  The loop is unrolled by 3
+  // so that every stage is a named LDS object.
+  auto step = [&](int c, float* ps, float* qs, float* ps2, float* qs2)
+      __attribute__((always_inline)) {
+    if (c + 1 < nk)
+      __builtin_amdgcn_s_waitcnt(kWaitOne);
+    else
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+    // a bare barrier: __syncthreads() is also a release fence, which would
+    // wait for every outstanding load (vmcnt(0)) and serialise the ring.
+    // Each wave's words of chunk c are in LDS by the wait above; its reads
+    // of chunk c - 1 have all returned (the MFMAs consumed them).
+    WXX_S_BARRIER();
+    if (c + 2 < nk) issue(c + 2, ps2, qs2);
+    compute(ps, qs);
+  };
+  if (nk > 0) issue(0, P0, Q0);
+  if (nk > 1) issue(1, P1, Q1);
+  for (int c = 0; c < nk; c += 3) {
+    step(c, P0, Q0, P2, Q2);
+    if (c + 1 < nk) step(c + 1, P1, Q1, P0, Q0);
+    if (c + 2 < nk) step(c + 2, P2, Q2, P1, Q1);
   }
 
   // ---- epilogue: D[i][j] of a 32x32 tile is in lane j + 32 ((i/4)%2),
@@ -203,18 +310,18 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
   for (int y = 0; y < TN; ++y) {
     const int j = j0 + wj * WJ + 32 * y + l32;
     if (j >= a.J) continue;
-    int64_t base = 0, istride = 0;
+    int64_t obase = 0, istride = 0;
     if (a.splits > 1) {
-      base = (int64_t)z * a.I * a.J + j;
+      obase = (int64_t)z * a.I * a.J + j;
       istride = a.J;
     } else if (MODE == kDw) {
-      base = j;
+      obase = j;
       istride = a.J;
     } else {
       const int S = MODE == kFwd ? HoWo : HW;
       const int C = MODE == kFwd ? a.Cout : a.Cin;
       const int b = j / S, pos = j - b * S;
-      base = (int64_t)b * C * S + pos;
+      obase = (int64_t)b * C * S + pos;
       istride = S;
     }
 #pragma unroll
@@ -225,7 +332,7 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
         if (i < a.I) {
           float v = acc[x][y][r];
           if (MODE != kDw && a.splits == 1 && a.bias) v += a.bias[i];
-          a.out[base + (int64_t)i * istride] = v;
+          a.out[obase + (int64_t)i * istride] = v;
         }
       }
     }
@@ -262,11 +369,11 @@ int launch(ConvArgs& a, float* final_out) {
   a.tiles_j = (a.J + BJ - 1) / BJ;
   const int64_t tiles = (int64_t)a.tiles_i * a.tiles_j;
   const int64_t cus = wxx::num_cus() > 0 ? wxx::num_cus() : 256;
-  // Split K when the tile grid leaves CUs idle; keep >= 8 chunks per split.
+  // Split K when the tile grid leaves CUs idle; keep >= 4 chunks per split.
   int splits = 1;
   if (tiles < 2 * cus) {
     const int64_t want = (2 * cus + tiles - 1) / tiles;
-    const int64_t maxs = std::max<int64_t>(1, a.K / (8 * BK));
+    const int64_t maxs = std::max<int64_t>(1, a.K / (4 * BK));
     splits = (int)std::min<int64_t>(std::min<int64_t>(want, maxs), 64);
   }
   int kps = (a.K + splits - 1) / splits;
@@ -284,7 +391,7 @@ int launch(ConvArgs& a, float* final_out) {
   } else {
     a.out = final_out;
   }
-  hipLaunchKernelGGL((conv_mfma_kernel<MODE, BI, BJ>), dim3((unsigned)tiles, (unsigned)splits),
+  hipLaunchKernelGGL((conv_lds_kernel<MODE, BI, BJ>), dim3((unsigned)tiles, (unsigned)splits),
                      dim3(256), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e == hipSuccess && splits > 1) {
@@ -300,10 +407,6 @@ int launch(ConvArgs& a, float* final_out) {
 
 template <int MODE>
 int dispatch(ConvArgs& a, float* final_out) {
-  const bool bi = a.I >= 128, bj = a.J >= 128;
-  if (bi && bj) return launch<MODE, 128, 128>(a, final_out);
-  if (bj) return launch<MODE, 64, 128>(a, final_out);
-  if (bi) return launch<MODE, 128, 64>(a, final_out);
   return launch<MODE, 64, 64>(a, final_out);
 }
 
