@@ -19,7 +19,7 @@ import numbers
 
 import numpy as np
 
-from . import validation
+from . import _views, validation
 from .backend import lib as _lib
 from .backend.device import get_buffer_pool, get_cmd_buffer
 
@@ -133,97 +133,43 @@ class Tensor:
     # Indexing
     # ------------------------------------------------------------------
     def __getitem__(self, index):
-        if not isinstance(index, tuple):
-            index = (index,)
-        if any(item is Ellipsis for item in index):
-            at = next(i for i, item in enumerate(index) if item is Ellipsis)
-            missing = len(self.shape) - (len(index) - 1)
-            if missing < 0:
-                raise IndexError("too many indices for tensor")
-            index = index[:at] + (slice(None),) * missing + index[at + 1:]
+        """A view for ints / slices / ``...`` (through autograd while
+        recording), a gathered copy for list / array / tensor entries."""
+        from .functional.utils import from_numpy
 
-        items = []
-        advanced = False
-        for item in index:
-            if isinstance(item, (list, np.ndarray)):
-                from .functional.utils import from_numpy
-
-                item = from_numpy(np.asarray(item))
-            if hasattr(item, "buffer"):
-                advanced = True
-            items.append(item)
-        index = tuple(items)
+        entries, advanced = _views.expand(index, len(self.shape), from_numpy)
         if advanced:
-            return self._advanced_getitem(index)
-
-        if len(index) < len(self.shape):
-            index = index + (slice(None),) * (len(self.shape) - len(index))
-        if len(index) > len(self.shape):
-            raise IndexError("too many indices for tensor")
-
+            return self._advanced_getitem(entries)
         from .backend import context
 
         if self.requires_grad and context.MODE == 0:
             from . import autograd
 
-            return autograd.getitem(self).forward(self, index)
-        return self._basic_getitem(index)
+            return autograd.getitem(self).forward(self, entries)
+        return self._basic_getitem(entries)
 
-    def _basic_getitem(self, index):
-        """Zero-copy view for ints and slices."""
-        offset = self.offset
-        shape = list(self.shape)
-        stride = list(self.stride)
-        for axis, item in enumerate(index):
-            if isinstance(item, slice):
-                start, stop, step = item.indices(self.shape[axis])
-                offset += start * self.stride[axis]
-                length = max(0, (stop - start + (step - 1 if step > 0 else step + 1)) // step)
-                shape[axis] = length
-                stride[axis] = self.stride[axis] * step
-            elif isinstance(item, int) and not isinstance(item, bool):
-                pos = item if item >= 0 else self.shape[axis] + item
-                if not 0 <= pos < self.shape[axis]:
-                    raise IndexError(
-                        f"index {item} out of bounds for axis {axis} with size {self.shape[axis]}"
-                    )
-                offset += pos * self.stride[axis]
-                shape[axis] = None
-                stride[axis] = None
-            else:
-                raise IndexError(f"unsupported index type {type(item).__name__}")
-        out = Tensor(
-            shape=[s for s in shape if s is not None],
-            buffer=self.buffer,
-            stride=[s for s in stride if s is not None],
-            offset=offset,
-            requires_grad=self.requires_grad,
-            dtype=self.type,
-        )
+    def _view(self, offset, shape, stride):
+        out = Tensor(shape=shape, buffer=self.buffer, stride=stride, offset=offset,
+                     requires_grad=self.requires_grad, dtype=self.type)
         out._base = self
         return out
 
+    def _basic_getitem(self, index):
+        """Zero-copy view selected by ints and slices (one entry per axis)."""
+        return self._view(*_views.basic(self.shape, self.stride, self.offset, index))
+
     def _advanced_getitem(self, index):
-        """Gather by integer/boolean arrays (host round trip, as in the reference)."""
+        """Gather by integer / mask entries through a host copy (as the
+        reference does); a new tensor of this one's dtype."""
         from .functional.utils import from_numpy
 
-        host = self.numpy()
-        first = index[0]
-        if isinstance(first, (bool, np.bool_)):
-            picked = host.reshape(-1)[np.flatnonzero(np.asarray(first))]
-        else:
-            idx = tuple(
-                it.numpy().astype(np.int64) if hasattr(it, "numpy") else it for it in index
-            )
-            picked = host[idx]
-        if self.type == "u32":
-            out = from_numpy(picked, dtype=np.uint32)
-        elif self.type == "c64":
+        picked = _views.gather(self.numpy(), index)
+        if self.type == "c64":
             from .functional.fft import from_numpy_complex
 
             out = from_numpy_complex(picked)
         else:
-            out = from_numpy(picked)
+            out = from_numpy(picked, dtype=np.uint32) if self.type == "u32" else from_numpy(picked)
         out.requires_grad = self.requires_grad
         return out
 
@@ -236,29 +182,9 @@ class Tensor:
     # Views
     # ------------------------------------------------------------------
     def narrow(self, dim, start, length):
-        rank = len(self.shape)
-        dim = validation.normalize_dim(dim, rank)
-        if not isinstance(start, int) or isinstance(start, bool):
-            raise TypeError(f"start must be an int, got {type(start).__name__}")
-        if not isinstance(length, int) or isinstance(length, bool):
-            raise TypeError(f"length must be an int, got {type(length).__name__}")
-        if start < 0 or length < 0 or start + length > self.shape[dim]:
-            raise IndexError(
-                f"narrow bounds out of range: start={start}, length={length}, "
-                f"dim {dim} has size {self.shape[dim]}"
-            )
-        shape = list(self.shape)
-        shape[dim] = length
-        out = Tensor(
-            shape=shape,
-            buffer=self.buffer,
-            stride=self.stride,
-            offset=self.offset + start * self.stride[dim],
-            requires_grad=self.requires_grad,
-            dtype=self.type,
-        )
-        out._base = self
-        return out
+        dim = validation.normalize_dim(dim, len(self.shape))
+        offset, shape = _views.narrow(self.shape, self.stride, self.offset, dim, start, length)
+        return self._view(offset, shape, self.stride)
 
     def slice(self, dim, start, length):
         from . import autograd

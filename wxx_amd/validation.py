@@ -1,169 +1,161 @@
-"""Host-side shape, dimension and layout checks shared by the ops.
+"""Host-side argument checks on tensor metadata (reference src/wxx/validation.py).
 
-These inspect metadata only (shape, stride, offset) and never touch device
-memory, mirroring the contract of the reference's validators
-(reference src/wxx/validation.py:1-208): the same checks raise the same
-exception types (``TypeError`` for wrong kinds, ``ValueError`` for bad
-values, ``IndexError`` for out-of-range dimensions) before any kernel is
-enqueued.
+Everything here looks at shapes, strides and offsets only: no device memory
+is read and nothing is enqueued, so a bad argument is reported before any
+kernel runs.  The error contract is the reference's: ``TypeError`` when a
+value has the wrong kind, ``ValueError`` when it has a bad value, and
+``IndexError`` when a dimension index is out of range.  The module imports
+nothing from the package, so ``Tensor`` and the backend can both use it.
 """
 
 import math
 
 MAX_RANK = 6
-"""Highest rank the strided kernels address (shape/stride arrays of six)."""
+"""Highest rank the strided kernels take (their shape / stride arrays hold six)."""
 
 
 def numel(shape):
-    """Element count of ``shape`` (1 for a 0-d shape)."""
+    """Number of elements of ``shape``; a 0-d shape holds one."""
     return int(math.prod(shape)) if len(shape) else 1
 
 
-def _is_int(v):
-    return isinstance(v, int) and not isinstance(v, bool)
+def _as_int(value):
+    """``value`` if it is an int (bools are not), else None."""
+    return value if isinstance(value, int) and not isinstance(value, bool) else None
+
+
+def _as_tuple(seq, name):
+    """``seq`` as a tuple; a lone int becomes a 1-tuple."""
+    if _as_int(seq) is not None:
+        return (seq,)
+    try:
+        return tuple(seq)
+    except TypeError:
+        raise TypeError(f"{name} must be an int or an iterable of ints, "
+                        f"got {type(seq).__name__}") from None
 
 
 def normalize_shape(shape, *, name="shape", allow_infer=False):
-    """Return ``shape`` as a tuple of non-negative ints (one ``-1`` if allowed)."""
-    if _is_int(shape):
-        shape = (shape,)
-    try:
-        dims = tuple(shape)
-    except TypeError:
-        raise TypeError(
-            f"{name} must be an int or an iterable of ints, got {type(shape).__name__}"
-        ) from None
-    n_infer = 0
-    for pos, d in enumerate(dims):
-        if not _is_int(d):
-            raise TypeError(f"{name}[{pos}] must be an int, got {type(d).__name__}")
-        if d == -1 and allow_infer:
-            n_infer += 1
-            if n_infer > 1:
-                raise ValueError(f"{name} may contain at most one -1, got {dims}")
-        elif d < 0:
-            raise ValueError(f"{name}[{pos}] must be non-negative, got {d}")
+    """``shape`` as a tuple of non-negative ints; with ``allow_infer`` one
+    entry may be -1 (resolved by :func:`infer_shape`)."""
+    dims = _as_tuple(shape, name)
+    wildcards = 0
+    for pos, size in enumerate(dims):
+        if _as_int(size) is None:
+            raise TypeError(f"{name}[{pos}] must be an int, got {type(size).__name__}")
+        if size >= 0:
+            continue
+        if size == -1 and allow_infer and wildcards == 0:
+            wildcards = 1
+            continue
+        if size == -1 and allow_infer:
+            raise ValueError(f"{name} may contain at most one -1, got {dims}")
+        raise ValueError(f"{name}[{pos}] must be non-negative, got {size}")
     return dims
 
 
 def infer_shape(shape, total, *, name="shape"):
-    """Resolve a ``-1`` entry and check that ``shape`` holds ``total`` elements."""
+    """Fill in a -1 entry of ``shape`` from ``total`` and require the
+    result to hold exactly ``total`` elements."""
     dims = normalize_shape(shape, name=name, allow_infer=True)
     if -1 in dims:
         at = dims.index(-1)
-        known = 1
-        for pos, d in enumerate(dims):
-            if pos != at:
-                known *= d
-        if known == 0 or total % known:
+        rest = numel(dims[:at] + dims[at + 1:])
+        if rest == 0 or total % rest:
             raise ValueError(f"cannot infer {name} {dims} for {total} elements")
-        dims = dims[:at] + (total // known,) + dims[at + 1:]
-    if numel(dims) != total:
-        raise ValueError(f"{name} {dims} describes {numel(dims)} elements, expected {total}")
+        dims = dims[:at] + (total // rest,) + dims[at + 1:]
+    count = numel(dims)
+    if count != total:
+        raise ValueError(f"{name} {dims} describes {count} elements, expected {total}")
     return dims
 
 
 def normalize_dim(dim, rank, *, name="dim"):
-    """Map a possibly negative dimension index into ``[0, rank)``."""
-    if not _is_int(dim):
+    """A dimension index (negative counts from the end) as one in [0, rank)."""
+    if _as_int(dim) is None:
         raise TypeError(f"{name} must be an int, got {type(dim).__name__}")
     if rank == 0:
         raise IndexError(f"{name}={dim} is invalid for a 0-d tensor")
-    d = dim + rank if dim < 0 else dim
-    if not 0 <= d < rank:
+    pos = dim % rank if -rank <= dim < rank else None
+    if pos is None:
         raise IndexError(f"{name}={dim} is out of range for a tensor of rank {rank}")
-    return d
+    return pos
 
 
 def normalize_dims(dims, rank, *, name="dims", allow_duplicates=True):
-    """Normalise an int or an iterable of dimension indices into a tuple."""
-    if _is_int(dims):
-        dims = (dims,)
-    try:
-        items = tuple(dims)
-    except TypeError:
-        raise TypeError(
-            f"{name} must be an int or an iterable of ints, got {type(dims).__name__}"
-        ) from None
-    out = tuple(normalize_dim(d, rank, name=f"{name}[{i}]") for i, d in enumerate(items))
-    if not allow_duplicates and len(set(out)) != len(out):
-        raise ValueError(f"{name} contains duplicate dimensions: {out}")
-    return out
+    """Each entry of an int or iterable of dimension indices, normalised."""
+    picked = tuple(normalize_dim(d, rank, name=f"{name}[{i}]")
+                   for i, d in enumerate(_as_tuple(dims, name)))
+    if not allow_duplicates and len(set(picked)) < len(picked):
+        raise ValueError(f"{name} contains duplicate dimensions: {picked}")
+    return picked
 
 
 def check_rank(shape, *, min_rank=0, max_rank=MAX_RANK, name="tensor"):
-    """Raise ``ValueError`` unless ``min_rank <= len(shape) <= max_rank``."""
+    """The rank of ``shape``, which must lie in [min_rank, max_rank]
+    (``max_rank`` None: no upper bound)."""
     rank = len(shape)
-    if rank < min_rank or (max_rank is not None and rank > max_rank):
-        if max_rank is None:
-            want = f"at least {min_rank}"
-        elif min_rank == max_rank:
-            want = str(min_rank)
-        else:
-            want = f"{min_rank}..{max_rank}"
-        raise ValueError(f"{name} must have rank {want}, got {rank}")
-    return rank
+    high = math.inf if max_rank is None else max_rank
+    if min_rank <= rank <= high:
+        return rank
+    if max_rank is None:
+        allowed = f"at least {min_rank}"
+    elif min_rank == max_rank:
+        allowed = f"{min_rank}"
+    else:
+        allowed = f"{min_rank}..{max_rank}"
+    raise ValueError(f"{name} must have rank {allowed}, got {rank}")
 
 
 def check_same_shape(*shapes, name="tensors"):
-    """Require identical shapes; return the common shape."""
-    if not shapes:
+    """The shape every argument shares; ``ValueError`` on the first mismatch."""
+    if len(shapes) == 0:
         raise ValueError(f"{name} must contain at least one shape")
-    first = tuple(shapes[0])
-    for i, s in enumerate(shapes[1:], 1):
-        if tuple(s) != first:
-            raise ValueError(
-                f"{name} must have the same shape, got {first} and {tuple(s)} (at index {i})"
-            )
-    return first
+    ref = tuple(shapes[0])
+    mismatch = next((i for i, s in enumerate(shapes) if tuple(s) != ref), None)
+    if mismatch is not None:
+        raise ValueError(f"{name} must have the same shape, got {ref} and "
+                         f"{tuple(shapes[mismatch])} (at index {mismatch})")
+    return ref
 
 
 def check_broadcastable(shape, out_shape, *, name="tensor"):
-    """Raise unless ``shape`` broadcasts to ``out_shape``."""
-    if len(shape) > len(out_shape):
+    """``out_shape`` if ``shape`` broadcasts to it (numpy rules), else ``ValueError``."""
+    lead = len(out_shape) - len(shape)
+    fits = lead >= 0 and all(d in (1, out_shape[lead + i]) for i, d in enumerate(shape))
+    if not fits:
         raise ValueError(f"{name} of shape {tuple(shape)} cannot broadcast to {tuple(out_shape)}")
-    pad = len(out_shape) - len(shape)
-    for i, d in enumerate(shape):
-        if d != out_shape[i + pad] and d != 1:
-            raise ValueError(
-                f"{name} of shape {tuple(shape)} cannot broadcast to {tuple(out_shape)}"
-            )
     return tuple(out_shape)
 
 
 def contiguous_strides(shape):
-    """Row-major strides (in elements) for ``shape``."""
-    strides = [1] * len(shape)
-    for i in range(len(shape) - 2, -1, -1):
-        strides[i] = strides[i + 1] * shape[i + 1]
-    return tuple(strides)
+    """Row-major element strides of ``shape``."""
+    out, step = [], 1
+    for size in reversed(shape):
+        out.append(step)
+        step *= size
+    return tuple(reversed(out))
 
 
 def is_contiguous_layout(shape, stride):
-    """True when ``stride`` is row-major for ``shape`` (size-1 dims may have any stride)."""
-    expect = 1
-    for size, step in zip(reversed(shape), reversed(stride)):
-        if size > 1 and step != expect:
-            return False
-        expect *= size
-    return True
+    """Whether ``stride`` lays ``shape`` out row-major and dense (the stride
+    of a dimension of size 0 or 1 does not matter)."""
+    want = contiguous_strides(shape)
+    return all(size <= 1 or s == w for size, s, w in zip(shape, stride, want))
 
 
 def check_contiguous(tensor, *, name="tensor"):
-    if not tensor.is_contiguous():
-        raise ValueError(
-            f"{name} must be contiguous, got shape={tuple(tensor.shape)} "
-            f"stride={tuple(tensor.stride)} offset={tensor.offset}"
-        )
-    return tensor
+    if tensor.is_contiguous():
+        return tensor
+    raise ValueError(f"{name} must be contiguous, got shape={tuple(tensor.shape)} "
+                     f"stride={tuple(tensor.stride)} offset={tensor.offset}")
 
 
 def check_no_negative_stride(tensor, *, name="tensor"):
-    if any(s < 0 for s in tensor.stride):
-        raise ValueError(
-            f"{name} has a negative stride {tuple(tensor.stride)}; call .contiguous() first"
-        )
-    return tensor
+    if min(tensor.stride, default=0) >= 0:
+        return tensor
+    raise ValueError(f"{name} has a negative stride {tuple(tensor.stride)}; "
+                     "call .contiguous() first")
 
 
 __all__ = [
