@@ -20,9 +20,13 @@ FFT / inverse FFT on [2048 x 16384], a row sum over [8192 x 4096]) and a
 the train steps of configs 1 and 5 (GPT-2), 3 (ResNet18) and 4 (Hyena):
 forward, CCE loss, backward, clip_grad_norm_, AdamW, LR schedule, in tokens/s
 or images/s, timed on the host clock between device synchronisations.
-``cpu_baseline`` times the oracle's exact-order fp32 GEMM restatement
-(oracle/csrc/gemm_ref.c, OpenMP on the host cores) on a bounded row sample of
-the 4096^3 GEMM, on rank 0 at N=1 only.
+``gpt2_train_step`` reports the config-5 train step (the metric's first
+quantity, on the north star's target config) with its model-FLOP rate;
+``train_steps`` holds all four model configs.  ``cpu_baseline`` times the
+oracle's exact-order fp32 GEMM restatement (oracle/csrc/gemm_ref.c, OpenMP on
+the host cores) on a bounded row sample of the 4096^3 GEMM, and under
+``components`` the oracle's numpy softmax, LayerNorm, rfft and config-1
+train step on bounded samples, on rank 0 at N=1 only.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--reps R] [--no-cpu]
                        [--no-train] [--only NAME]
@@ -98,6 +102,70 @@ def cpu_gemm_baseline(budget_s):
         "sample": f"{total_rows} rows of the 4096x4096x4096 fp32 GEMM "
                   f"({elapsed:.1f} s), oracle/csrc/gemm_ref.c fma chain, OpenMP",
     }
+
+
+def _cpu_rate(fn, budget_s):
+    """(calls, seconds) of repeating ``fn`` for about ``budget_s`` (one
+    untimed warm call first)."""
+    fn()
+    calls, elapsed = 0, 0.0
+    while elapsed < budget_s or calls == 0:
+        t0 = time.perf_counter()
+        fn()
+        elapsed += time.perf_counter() - t0
+        calls += 1
+    return calls, elapsed
+
+
+def cpu_component_baselines(budget_s):
+    """The oracle's numpy restatements of the HBM-bound config-2/4 kernels and
+    of the config-1 train step, timed on the host cores (numpy float64 math;
+    BLAS threads for the train step)."""
+    from oracle import activations as oa
+    from oracle import fft as of
+    from oracle import models as om
+    from oracle import norms as on
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    rows = ROWS // 16
+    r = np.random.default_rng(20)
+    x = r.standard_normal((rows, COLS), dtype=np.float32)
+    g, b = np.ones(COLS, np.float32), np.zeros(COLS, np.float32)
+    out = {}
+    n, t = _cpu_rate(lambda: oa.softmax(x, -1), budget_s)
+    out["softmax"] = {"gbs": n * 2.0 * rows * COLS * 4 / t / 1e9, "cores": 1,
+                      "sample": f"{n} x [{rows}x4096] row softmax (1/16 of config 2's rows), "
+                                "oracle/activations.py (numpy, float64)"}
+    n, t = _cpu_rate(lambda: on.meanvarnorm(x, g, b, -1), budget_s)
+    out["layernorm"] = {"gbs": n * 2.0 * rows * COLS * 4 / t / 1e9, "cores": 1,
+                        "sample": f"{n} x [{rows}x4096] LayerNorm (1/16 of config 2's rows), "
+                                  "oracle/norms.py (numpy, float64)"}
+    fx = np.random.default_rng(41).standard_normal((FFT_ROWS // 8, FFT_N), dtype=np.float32)
+    nb = FFT_N // 2 + 1
+    n, t = _cpu_rate(lambda: of.rfft(fx, FFT_N), budget_s)
+    out["rfft"] = {"gbs": n * (FFT_ROWS // 8) * (FFT_N * 4.0 + nb * 8) / t / 1e9, "cores": 1,
+                   "sample": f"{n} x [256x16384] rfft (1/8 of config 4's rows), oracle/fft.py "
+                             "(numpy pocketfft, float64)"}
+    V, D, H, L, B, S = 1024, 256, 8, 6, 4, 128
+    rp = np.random.default_rng(1234)
+    P = {"tok_emb.weight": rp.normal(0, 0.02, (V, D)), "pos_emb.weight": rp.normal(0, 0.02, (256, D)),
+         "ln_f.weightg": np.ones(D), "ln_f.weightb": np.zeros(D)}
+    for i in range(L):
+        p = f"blocks.{i}."
+        for nm in ("q", "k", "v", "out"):
+            P[p + f"attn.{nm}.weight"] = rp.normal(0, 0.02, (D, D))
+        P[p + "mlp.0.weight"], P[p + "mlp.0.bias"] = rp.normal(0, 0.02, (D, 4 * D)), np.zeros(4 * D)
+        P[p + "mlp.2.weight"], P[p + "mlp.2.bias"] = rp.normal(0, 0.02, (4 * D, D)), np.zeros(D)
+        for ln in ("ln1", "ln2"):
+            P[p + f"{ln}.weightg"], P[p + f"{ln}.weightb"] = np.ones(D), np.zeros(D)
+    ids = np.random.default_rng(0).integers(0, V, (B, S))
+    tg = np.random.default_rng(1).integers(0, V, (B, S))
+    n, t = _cpu_rate(lambda: om.gpt2_loss_and_grads(P, ids, tg, H, L), budget_s)
+    out["gpt2_train_config1"] = {
+        "tokens_per_s": n * B * S / t, "cores": threads,
+        "sample": f"{n} forward+backward passes of GPT2(1024, 256, 8, 6) on 4 x 128 tokens, "
+                  "oracle/models.py (numpy float64, BLAS threads)"}
+    return out
 
 
 class Kernels:
@@ -348,7 +416,8 @@ def main():
                         "row softmax and LayerNorm on [8192x4096]",
             "value_is": "aggregate fp32 GEMM TFLOP/s over the five GEMMs of the step",
             "timing": "per kernel: median over steps of (HIP-event time of R back-to-back "
-                      "launches on the library stream) / R",
+                      "launches on the library stream) / R; the rocprofv3 per-dispatch trace "
+                      "of the same command is in profiles/kernels_bench_config2.md",
         },
         "roofline": {
             "kernel": "gemm_f32_dtl_kernel<false,false> (4096x4096x4096)",
@@ -364,10 +433,23 @@ def main():
         "wall_s": wall_s,
     }
     if not args.no_train:
-        for name in TRAIN_CONFIGS:
-            out["extra"][name] = train_step(lib, name, steps=5, warmup=2)
+        out["train_steps"] = {name: train_step(lib, name, steps=5, warmup=2)
+                              for name in TRAIN_CONFIGS}
+        c5 = out["train_steps"]["gpt2_train_config5"]
+        # the metric's first quantity, on the north star's target config
+        out["gpt2_train_step"] = {
+            "tokens_per_s": c5["tokens_per_s"], "ms_per_step": c5["ms"],
+            "model_tflops": c5["tflops"], "frac_of_fp32_peak": c5["frac_of_peak"],
+            "steps_timed": c5["steps_timed"], "loss": c5["loss"],
+            "config": c5["model"] + "; forward, CCELoss, backward, clip_grad_norm_(1.0), "
+                      "AdamW, WarmupCosineLR",
+            "model_flop_per_step": TRAIN_CONFIGS["gpt2_train_config5"]["flop"],
+            "timing": "host clock around 5 steps between device synchronisations",
+            "profile": "profiles/gpt2_config5_train_step.md"}
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_gemm_baseline(args.cpu_seconds)
+        base = cpu_gemm_baseline(args.cpu_seconds)
+        base["components"] = cpu_component_baselines(args.cpu_seconds / 4)
+        out["cpu_baseline"] = base
     print(json.dumps(out))
 
 
