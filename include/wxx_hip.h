@@ -262,9 +262,10 @@ int wxx_unfolddx(const float* dy, float* dx, int64_t prefix, int64_t length, int
                  int64_t windows, int64_t size, int64_t step);
 
 /* ---- C: FFT and complex ops (functional/fft.py).  X/complex pointers are c64. */
-/* functional.rfft (fft.py:484-563): rows x in_len -> rows x (n/2+1); n = 2^k <= 32768 */
+/* functional.rfft (fft.py:484-563): rows x in_len -> rows x (n/2+1); n = 2^k <= 2^27
+ * (n <= 32768 in one LDS-resident pass per row, longer as a four-step transform) */
 int wxx_rfft(const float* x, void* X, int64_t rows, int64_t in_len, int64_t n);
-/* functional.irfft (fft.py:566-645): rows x in_len -> rows x n; n = 2^k, 2 <= n <= 32768 */
+/* functional.irfft (fft.py:566-645): rows x in_len -> rows x n; n = 2^k, 2 <= n <= 2^27 */
 int wxx_irfft(const void* X, float* x, int64_t rows, int64_t in_len, int64_t n);
 /* functional.irfft(..., length=L) and the Hyena crop irfft(...)[..., :L]
  * (nn/hyena.py:208-216): the first out_len samples of each row (row stride

@@ -136,6 +136,10 @@ inline uint32_t __float_as_uint(float f) { uint32_t v; std::memcpy(&v, &f, 4); r
 inline float __fmul_rn(float a, float b) { return a * b; }
 inline float __fadd_rn(float a, float b) { return a + b; }
 inline float rsqrtf(float x) { return 1.0f / std::sqrt(x); }
+inline void sincospi(double x, double* s, double* c) {
+  *s = std::sin(M_PI * x);
+  *c = std::cos(M_PI * x);
+}
 inline float __expf(float x) { return std::exp(x); }
 
 typedef float wxx_floatx16 __attribute__((ext_vector_type(16)));

@@ -76,6 +76,11 @@ int set_error(int code, const char* fmt, ...);
 void* scratch_alloc(size_t bytes);   // stream-ordered temporary from the cache
 void scratch_free(void* p);
 int num_cus();
+// Real FFT and its inverse for n = 2^(logm + 1) above one workgroup's LDS
+// (fft_big.hip): four-step transforms over global scratch.
+int rfft_four_step(const float* x, float2* X, int64_t rows, int64_t in_len, int logm);
+int irfft_four_step(const float2* X, float* x, int64_t rows, int64_t in_len, int logm,
+                    int64_t out_len, float post);
 // Looks up the device address of the allocation-free GEMM's scratch array on
 // `device` (which must be current); called once per device by wxx_init.
 int gemm_noalloc_setup(int device);

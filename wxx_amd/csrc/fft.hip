@@ -10,7 +10,8 @@
 // MI355X design.  A length-n real transform is computed as one length
 // M = n/2 complex transform of z[m] = x[2m] + i x[2m+1] followed by the
 // standard even/odd untangling X[k] = E[k] + W_n^k O[k] (and the mirror image
-// of that for the inverse).  For n <= 32768 the M complex points of a row
+// of that for the inverse).  Longer rows take the four-step path of
+// fft_big.hip.  For n <= 32768 the M complex points of a row
 // (64 KiB at n = 16384) stay in LDS for the whole transform: one workgroup
 // per row reads the input from HBM once and writes the spectrum once.
 // Inside the workgroup the transform is a Stockham auto-sort FFT: every pass
@@ -965,10 +966,8 @@ WXX_API int wxx_rfft(const float* x, void* X, int64_t rows, int64_t in_len, int6
   const int logn = log2_exact(n);
   WXX_REQUIRE(logn >= 0, "FFT length must be a positive power of two, got %lld", (long long)n);
   if (rows == 0) return WXX_OK;
-  if (logn - 1 > kMaxLogM)
-    return wxx::set_error(WXX_E_UNSUPPORTED, "rfft length %lld above %d", (long long)n,
-                          2 << kMaxLogM);
   float2* Xc = static_cast<float2*>(X);
+  if (logn - 1 > kMaxLogM) return wxx::rfft_four_step(x, Xc, rows, in_len, logn - 1);
   if (n == 1) {
     hipLaunchKernelGGL(rfft1_kernel, dim3(wxx::grid_1d(rows, 256)), dim3(256), 0, wxx::stream(),
                        x, Xc, rows, in_len);
@@ -999,8 +998,8 @@ WXX_API int wxx_irfft_crop(const void* X, float* x, int64_t rows, int64_t in_len
               (long long)out_len, (long long)n);
   if (rows == 0) return WXX_OK;
   if (logn - 1 > kMaxLogM)
-    return wxx::set_error(WXX_E_UNSUPPORTED, "irfft length %lld above %d", (long long)n,
-                          2 << kMaxLogM);
+    return wxx::irfft_four_step(static_cast<const float2*>(X), x, rows, in_len, logn - 1,
+                                out_len, post_scale);
   const float2* tw = twiddles(logn - 1);
   if (!tw) return wxx::set_error(WXX_E_OOM, "irfft twiddle table allocation failed");
   RowOut ro{};
