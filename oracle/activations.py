@@ -18,20 +18,24 @@ SELU_ALPHA = 1.6732632423543772848170429916717
 SELU_SCALE = 1.0507009873554804934193349852946
 
 
-def softmax(x, dim=-1):
-    x = np.asarray(x, dtype=np.float64)
-    m = np.maximum(np.max(x, axis=dim, keepdims=True), -1e38)
+def softmax(x, dim=-1, dtype=np.float64, rounded=True):
+    """``dtype=np.float32``: the same steps in single precision (the rounding
+    floor of an fp32 evaluation); ``rounded=False`` keeps the float64 values."""
+    x = np.asarray(x, dtype=np.float32).astype(dtype)
+    m = np.maximum(np.max(x, axis=dim, keepdims=True), dtype(-1e38))
     e = np.exp(x - m)
-    return (e * (1.0 / e.sum(axis=dim, keepdims=True))).astype(np.float32)
+    y = e * (dtype(1.0) / e.sum(axis=dim, keepdims=True))
+    return y.astype(np.float32) if rounded else y
 
 
-def softmax_backward(y, g, dim=-1):
+def softmax_backward(y, g, dim=-1, dtype=np.float64, rounded=True):
     """Softmax gradient from the output: y * (g - sum(g * y, dim)) (reference
     src/wxx/autograd/reductions.py:25-35)."""
-    y = np.asarray(y, dtype=np.float64)
-    g = np.asarray(g, dtype=np.float64)
+    y = np.asarray(y, dtype=dtype)
+    g = np.asarray(g, dtype=dtype)
     dot = (g * y).sum(axis=dim, keepdims=True)
-    return (y * (g - dot)).astype(np.float32)
+    out = y * (g - dot)
+    return out.astype(np.float32) if rounded else out
 
 
 def gelu(x):

@@ -58,7 +58,9 @@ def bias_mode(bias_shape, out_batch, M, N):
     raise ValueError(f"Bias shape {bias_shape} is not broadcastable")
 
 
-def matmul_add(A, B, bias=None, transpose_A=False, transpose_B=False):
+def matmul_add(A, B, bias=None, transpose_A=False, transpose_B=False, rounded=True):
+    """C = op(A) op(B) + bias in float64; ``rounded`` returns it rounded to
+    float32, else the float64 values themselves."""
     A = np.asarray(A, np.float32)
     B = np.asarray(B, np.float32)
     M, N, K, out_batch, _, _ = _dims(A.shape, B.shape, transpose_A, transpose_B)
@@ -72,7 +74,8 @@ def matmul_add(A, B, bias=None, transpose_A=False, transpose_B=False):
     c = np.matmul(a, b)
     if mode:
         c = c + np.asarray(bias, np.float64)
-    return c.astype(np.float32).reshape(tuple(out_batch) + (M, N))
+    c = c.reshape(tuple(out_batch) + (M, N))
+    return c.astype(np.float32) if rounded else c
 
 
 def matmul_add_fma(A, B, bias=None, transpose_A=False, transpose_B=False, rows=None):

@@ -1,6 +1,8 @@
 """LayerNorm, RMSNorm and BatchNorm restated from the reference (test
-infrastructure only).  Statistics are accumulated in float64 but follow the
-reference's formulas, including its special cases:
+infrastructure only).  Statistics are accumulated in float64 (or, with
+``dtype=np.float32``, in single precision: the rounding floor an fp32
+evaluation of the same formulas carries) and follow the reference's
+formulas, including its special cases:
 
 * LayerNorm (meanvarnorm.wgsl:29-111): single pass mu = S/n,
   var = max(0, Q/n - mu^2), inv_std = var > 0 ? 1/sqrt(var + eps) : 0,
@@ -26,16 +28,16 @@ def _view(x, axis):
     return x.reshape(outer, red, inner), out_shape
 
 
-def meanvarnorm(x, gamma, beta, axis=-1, eps=1e-5, row_cap=0):
+def meanvarnorm(x, gamma, beta, axis=-1, eps=1e-5, row_cap=0, dtype=np.float64):
     x = np.asarray(x, dtype=np.float32)
-    v, out_shape = _view(x.astype(np.float64), axis)
+    v, out_shape = _view(x.astype(dtype), axis)
     n = v.shape[1]
     mu = v.sum(axis=1) / n
     var = np.maximum(0.0, (v * v).sum(axis=1) / n - mu * mu)
     safe = np.where(var > 0, var + eps, 1.0)
     inv = np.where(var > 0, 1.0 / np.sqrt(safe), 0.0)
-    g = np.asarray(gamma, np.float64).reshape(1, n, 1)
-    b = np.asarray(beta, np.float64).reshape(1, n, 1)
+    g = np.asarray(gamma, dtype).reshape(1, n, 1)
+    b = np.asarray(beta, dtype).reshape(1, n, 1)
     y = (v - mu[:, None, :]) * inv[:, None, :] * g + b
     if row_cap:
         y[row_cap:] = 0.0
@@ -48,14 +50,14 @@ def meanvarnorm(x, gamma, beta, axis=-1, eps=1e-5, row_cap=0):
     )
 
 
-def meanvarnormdx(dy, x, gamma, mean, inv_std, axis=-1, row_cap=0):
+def meanvarnormdx(dy, x, gamma, mean, inv_std, axis=-1, row_cap=0, dtype=np.float64):
     x = np.asarray(x, np.float32)
-    v, _ = _view(x.astype(np.float64), axis)
-    d, _ = _view(np.asarray(dy, np.float64), axis)
+    v, _ = _view(x.astype(dtype), axis)
+    d, _ = _view(np.asarray(dy, dtype), axis)
     n = v.shape[1]
-    mu = np.asarray(mean, np.float64).reshape(v.shape[0], 1, v.shape[2])
-    inv = np.asarray(inv_std, np.float64).reshape(v.shape[0], 1, v.shape[2])
-    db = d * np.asarray(gamma, np.float64).reshape(1, n, 1)
+    mu = np.asarray(mean, dtype).reshape(v.shape[0], 1, v.shape[2])
+    inv = np.asarray(inv_std, dtype).reshape(v.shape[0], 1, v.shape[2])
+    db = d * np.asarray(gamma, dtype).reshape(1, n, 1)
     xh = (v - mu) * inv
     c1 = db.sum(axis=1, keepdims=True) / n
     c2 = (db * xh).sum(axis=1, keepdims=True) / n
@@ -65,57 +67,58 @@ def meanvarnormdx(dy, x, gamma, mean, inv_std, axis=-1, row_cap=0):
     return dx.astype(np.float32).reshape(x.shape)
 
 
-def meanvarnormdg(dy, x, mean, inv_std, axis=-1):
+def meanvarnormdg(dy, x, mean, inv_std, axis=-1, dtype=np.float64):
     x = np.asarray(x, np.float32)
-    v, _ = _view(x.astype(np.float64), axis)
-    d, _ = _view(np.asarray(dy, np.float64), axis)
-    mu = np.asarray(mean, np.float64).reshape(v.shape[0], 1, v.shape[2])
-    inv = np.asarray(inv_std, np.float64).reshape(v.shape[0], 1, v.shape[2])
+    v, _ = _view(x.astype(dtype), axis)
+    d, _ = _view(np.asarray(dy, dtype), axis)
+    mu = np.asarray(mean, dtype).reshape(v.shape[0], 1, v.shape[2])
+    inv = np.asarray(inv_std, dtype).reshape(v.shape[0], 1, v.shape[2])
     xh = (v - mu) * inv
     dg = (d * xh).sum(axis=(0, 2))
     db = d.sum(axis=(0, 2))
     return dg.astype(np.float32), db.astype(np.float32)
 
 
-def rmsnorm(x, gamma, axis=-1, eps=1e-6, row_cap=0):
+def rmsnorm(x, gamma, axis=-1, eps=1e-6, row_cap=0, dtype=np.float64):
     x = np.asarray(x, dtype=np.float32)
-    v, out_shape = _view(x.astype(np.float64), axis)
+    v, out_shape = _view(x.astype(dtype), axis)
     n = v.shape[1]
     ms = (v * v).sum(axis=1) / n
     r = np.where(ms > 0, 1.0 / np.sqrt(np.where(ms > 0, ms + eps, 1.0)), 0.0)
-    y = v * r[:, None, :] * np.asarray(gamma, np.float64).reshape(1, n, 1)
+    y = v * r[:, None, :] * np.asarray(gamma, dtype).reshape(1, n, 1)
     if row_cap:
         y[row_cap:] = 0.0
         r[row_cap:] = 0.0
     return y.astype(np.float32).reshape(x.shape), r.astype(np.float32).reshape(out_shape)
 
 
-def rmsnormdx(dy, x, gamma, inv_rms, axis=-1):
+def rmsnormdx(dy, x, gamma, inv_rms, axis=-1, dtype=np.float64):
     x = np.asarray(x, np.float32)
-    v, _ = _view(x.astype(np.float64), axis)
-    d, _ = _view(np.asarray(dy, np.float64), axis)
+    v, _ = _view(x.astype(dtype), axis)
+    d, _ = _view(np.asarray(dy, dtype), axis)
     n = v.shape[1]
-    r = np.asarray(inv_rms, np.float64).reshape(v.shape[0], 1, v.shape[2])
-    db = d * np.asarray(gamma, np.float64).reshape(1, n, 1)
+    r = np.asarray(inv_rms, dtype).reshape(v.shape[0], 1, v.shape[2])
+    db = d * np.asarray(gamma, dtype).reshape(1, n, 1)
     c = (r * r / n) * (db * v).sum(axis=1, keepdims=True)
     return (r * (db - v * c)).astype(np.float32).reshape(x.shape)
 
 
-def rmsnormdg(dy, x, inv_rms, axis=-1):
+def rmsnormdg(dy, x, inv_rms, axis=-1, dtype=np.float64):
     x = np.asarray(x, np.float32)
-    v, _ = _view(x.astype(np.float64), axis)
-    d, _ = _view(np.asarray(dy, np.float64), axis)
-    r = np.asarray(inv_rms, np.float64).reshape(v.shape[0], 1, v.shape[2])
+    v, _ = _view(x.astype(dtype), axis)
+    d, _ = _view(np.asarray(dy, dtype), axis)
+    r = np.asarray(inv_rms, dtype).reshape(v.shape[0], 1, v.shape[2])
     return (d * v * r).sum(axis=(0, 2)).astype(np.float32)
 
 
-def batchnorm(x, gamma, beta, running_mean, running_var, training, eps=1e-5, momentum=0.1):
+def batchnorm(x, gamma, beta, running_mean, running_var, training, eps=1e-5, momentum=0.1,
+              dtype=np.float64):
     """Returns (y, saved_mean, inv_std, new_running_mean, new_running_var)."""
-    x64 = np.asarray(x, np.float64)
+    x64 = np.asarray(x, dtype)
     B, C, H, W = x64.shape
     M = B * H * W
-    rm = np.asarray(running_mean, np.float64).copy()
-    rv = np.asarray(running_var, np.float64).copy()
+    rm = np.asarray(running_mean, dtype).copy()
+    rv = np.asarray(running_var, dtype).copy()
     if training:
         mu = x64.sum(axis=(0, 2, 3)) / M
         var = np.maximum(0.0, (x64 * x64).sum(axis=(0, 2, 3)) / M - mu * mu)
@@ -126,31 +129,31 @@ def batchnorm(x, gamma, beta, running_mean, running_var, training, eps=1e-5, mom
     else:
         mu = rm.copy()
         inv = 1.0 / np.sqrt(rv + eps)
-    g = np.asarray(gamma, np.float64).reshape(1, C, 1, 1)
-    b = np.asarray(beta, np.float64).reshape(1, C, 1, 1)
+    g = np.asarray(gamma, dtype).reshape(1, C, 1, 1)
+    b = np.asarray(beta, dtype).reshape(1, C, 1, 1)
     y = (x64 - mu.reshape(1, C, 1, 1)) * inv.reshape(1, C, 1, 1) * g + b
     f = np.float32
     return y.astype(f), mu.astype(f), inv.astype(f), rm.astype(f), rv.astype(f)
 
 
-def batchnormdg(dy, x, mean, inv_std):
-    x64 = np.asarray(x, np.float64)
+def batchnormdg(dy, x, mean, inv_std, dtype=np.float64):
+    x64 = np.asarray(x, dtype)
     C = x64.shape[1]
-    xh = (x64 - np.asarray(mean, np.float64).reshape(1, C, 1, 1)) * np.asarray(
-        inv_std, np.float64
+    xh = (x64 - np.asarray(mean, dtype).reshape(1, C, 1, 1)) * np.asarray(
+        inv_std, dtype
     ).reshape(1, C, 1, 1)
-    d = np.asarray(dy, np.float64)
+    d = np.asarray(dy, dtype)
     return (d * xh).sum(axis=(0, 2, 3)).astype(np.float32), d.sum(axis=(0, 2, 3)).astype(np.float32)
 
 
-def batchnormdx(dy, x, gamma, dgamma, dbeta, mean, inv_std):
-    x64 = np.asarray(x, np.float64)
+def batchnormdx(dy, x, gamma, dgamma, dbeta, mean, inv_std, dtype=np.float64):
+    x64 = np.asarray(x, dtype)
     B, C, H, W = x64.shape
     M = float(B * H * W)
 
     def r(a):
-        return np.asarray(a, np.float64).reshape(1, C, 1, 1)
+        return np.asarray(a, dtype).reshape(1, C, 1, 1)
 
     xh = (x64 - r(mean)) * r(inv_std)
-    dx = (r(gamma) * r(inv_std) / M) * (M * np.asarray(dy, np.float64) - r(dbeta) - xh * r(dgamma))
+    dx = (r(gamma) * r(inv_std) / M) * (M * np.asarray(dy, dtype) - r(dbeta) - xh * r(dgamma))
     return dx.astype(np.float32)

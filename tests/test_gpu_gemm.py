@@ -1,14 +1,14 @@
 """GPU parity: the fp32 MFMA GEMM (functional.matmul_add) against the oracle.
 
-Small and ragged shapes are compared in full against the float64 oracle;
-the BASELINE config-2 sizes are compared on row samples against the
-exact-order fp32 restatement of the reference kernel (oracle/csrc/gemm_ref.c)
-plus a full-matrix linearity identity."""
+Every shape, the BASELINE config-2 sizes included, is compared element by
+element against the float64 product, within 4x the error of the reference's
+own fp32 arithmetic on the same operands (the exact-order fma chain of
+matmul.wgsl, restated in oracle/csrc/gemm_ref.c)."""
 
 import numpy as np
 import pytest
 
-from conftest import assert_close, rng
+from conftest import assert_close, assert_error_floor, rng
 from oracle import gemm as og
 
 pytestmark = pytest.mark.gpu
@@ -24,9 +24,14 @@ def up(a):
     return F().from_numpy(np.asarray(a, np.float32))
 
 
-def tol(K):
-    # fp32 dot products of length K with N(0,1) entries: |C| ~ sqrt(K)
-    return dict(rtol=1e-4, atol=1e-5 * max(1.0, np.sqrt(K)))
+def check(got, A, B, bias=None, ta=False, tb=False, msg=""):
+    """The device product against the float64 product, within 4x what the
+    reference's own fp32 arithmetic (the exact-order fma chain of
+    matmul.wgsl, oracle/csrc/gemm_ref.c) misses it by: a wrong, dropped or
+    doubled K chunk is far outside that floor."""
+    want = og.matmul_add(A, B, bias, ta, tb, rounded=False)
+    ref32 = og.matmul_add_fma(A, B, bias, ta, tb)
+    assert_error_floor(np.asarray(got), want, ref32, msg=msg)
 
 
 @pytest.mark.parametrize("ta", [False, True])
@@ -39,7 +44,7 @@ def test_matmul_transposes_ragged(device, ta, tb, M, N, K):
     A = r.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
     B = r.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
     got = F().matmul_add(up(A), up(B), None, transpose_A=ta, transpose_B=tb).numpy()
-    assert_close(got, og.matmul_add(A, B, None, ta, tb), **tol(K))
+    check(got, A, B, None, ta, tb)
 
 
 @pytest.mark.parametrize("bias_kind", ["none", "vec", "mat", "batched"])
@@ -53,7 +58,7 @@ def test_matmul_batch_and_bias_modes(device, bias_kind, layout):
             "batched": r.standard_normal((b, M, N))}[bias_kind]
     bt = None if bias is None else up(bias)
     got = F().matmul_add(up(A), up(B), bt).numpy()
-    assert_close(got, og.matmul_add(A, B, bias), **tol(K))
+    check(got, A, B, bias)
 
 
 def test_matmul_attention_shapes(device):
@@ -61,32 +66,26 @@ def test_matmul_attention_shapes(device):
     q = r.standard_normal((12, 128, 64)).astype(np.float32)
     k = r.standard_normal((12, 128, 64)).astype(np.float32)
     s = F().matmul_add(up(q), up(k), None, transpose_B=True).numpy()
-    assert_close(s, og.matmul_add(q, k, None, False, True), **tol(64))
+    check(s, q, k, None, False, True)
     p = r.standard_normal((12, 128, 128)).astype(np.float32)
     o = F().matmul_add(up(p), up(k), None).numpy()
-    assert_close(o, og.matmul_add(p, k), **tol(128))
+    check(o, p, k)
     # weight-gradient shape: A^T @ g with batch
     g = r.standard_normal((12, 128, 64)).astype(np.float32)
     dw = F().matmul_add(up(q), up(g), None, transpose_A=True).numpy()
-    assert_close(dw, og.matmul_add(q, g, None, True, False), **tol(128))
+    check(dw, q, g, None, True, False)
 
 
 @pytest.mark.parametrize("M,N,K", [(1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096),
                                    (8192, 3072, 768), (8192, 768, 3072), (8192, 768, 768)])
 def test_matmul_config2_sizes(device, M, N, K):
+    # every element of BASELINE config 2's GEMMs against float64, within 4x
+    # the reference's own fp32 fma-chain error on the same operands
     r = rng(10 + M % 7)
     A = r.standard_normal((M, K)).astype(np.float32)
     B = r.standard_normal((K, N)).astype(np.float32)
-    tA, tB = up(A), up(B)
-    C = F().matmul_add(tA, tB, None).numpy()
-    rows = r.integers(0, M - 8)
-    ref = og.matmul_add_fma(A, B, rows=(rows, rows + 8))[rows:rows + 8]
-    assert_close(C[rows:rows + 8], ref, **tol(K))
-    # full-matrix identity: A @ (B 1) == (A @ B) 1, checked in float64
-    ones = np.ones(N)
-    lhs = C.astype(np.float64) @ ones
-    rhs = A.astype(np.float64) @ (B.astype(np.float64) @ ones)
-    assert_close(lhs, rhs, rtol=1e-4, atol=1e-3 * np.sqrt(K * N))
+    C = F().matmul_add(up(A), up(B), None).numpy()
+    check(C, A, B, msg=f"{M}x{N}x{K}")
 
 
 def test_matmul_errors(device):
@@ -117,7 +116,7 @@ def test_matmul_split_k(device, ta, tb, M, N, K, bias_kind):
     bias = {"none": None, "vec": r.standard_normal(N), "mat": r.standard_normal((M, N))}[bias_kind]
     got = F().matmul_add(up(A), up(B), None if bias is None else up(bias), transpose_A=ta,
                          transpose_B=tb).numpy()
-    assert_close(got, og.matmul_add(A, B, bias, ta, tb), **tol(K))
+    check(got, A, B, bias, ta, tb)
     again = F().matmul_add(up(A), up(B), None if bias is None else up(bias), transpose_A=ta,
                            transpose_B=tb).numpy()
     assert np.array_equal(got, again), "split-K result must be deterministic"
@@ -129,7 +128,7 @@ def test_matmul_split_k_batched(device):
     B = r.standard_normal((3, 2048, 48)).astype(np.float32)
     bias = r.standard_normal((3, 64, 48)).astype(np.float32)
     got = F().matmul_add(up(A), up(B), up(bias)).numpy()
-    assert_close(got, og.matmul_add(A, B, bias), **tol(2048))
+    check(got, A, B, bias)
 
 
 @pytest.mark.parametrize("code", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
@@ -153,7 +152,7 @@ def test_matmul_every_tile_code(device, code, splits, ta, tb):
         P = C.c_void_p
         lib.call("wxx_matmul_add", P(tA.data_ptr()), P(tB.data_ptr()), P(tbias.data_ptr()),
                  P(out.data_ptr()), M, N, K, 1, 0, 0, 0, 1, int(ta), int(tb), code + 256 * splits)
-        assert_close(out.numpy(), og.matmul_add(A, B, bias, ta, tb), **tol(K))
+        check(out.numpy(), A, B, bias, ta, tb)
 
 
 @pytest.mark.parametrize("code", [11, 12, 13])
@@ -185,7 +184,7 @@ def test_matmul_direct_to_lds(device, code, ta, tb, batch, M, N, K, splits, bias
     lib.call("wxx_matmul_add", P(tA.data_ptr()), P(tB.data_ptr()), P(tbias.data_ptr()),
              P(out.data_ptr()), M, N, K, batch, M * K, K * N, M * N if bias_mode == 3 else 0,
              bias_mode, int(ta), int(tb), code + 256 * splits)
-    assert_close(out.numpy(), og.matmul_add(A, B, bias, ta, tb), **tol(K))
+    check(out.numpy(), A, B, bias, ta, tb)
 
 
 @pytest.mark.parametrize("K", [768, 3072])
@@ -201,13 +200,7 @@ def test_matmul_n768_every_transpose(device, ta, tb, K):
     B = r.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
     bias = r.standard_normal(N).astype(np.float32)
     got = F().matmul_add(up(A), up(B), up(bias), transpose_A=ta, transpose_B=tb).numpy()
-    Ad = (A.T if ta else A).astype(np.float64)
-    Bd = (B.T if tb else B).astype(np.float64)
-    rows = np.r_[0:8, 4092:4100, M - 8:M]
-    assert_close(got[rows], Ad[rows] @ Bd + bias, **tol(K))
-    ones = np.ones(N)
-    assert_close(got.astype(np.float64) @ ones, Ad @ (Bd @ ones) + bias.sum(),
-                 rtol=1e-4, atol=1e-3 * np.sqrt(K * N))
+    check(got, A, B, bias, ta, tb)
 
 
 def test_matmul_direct_to_lds_rejects_edge_tiles(device):
@@ -245,14 +238,16 @@ def test_matmul_tri_modes(device, S, d):
     # tri 1: scores, needed on / below the diagonal; above it 0 or the value
     s1 = F().matmul_add(up(q), up(k), None, transpose_B=True, tri=1).numpy()
     ref = og.matmul_add(q, k, None, False, True)
-    assert_close(s1[:, on_or_below], ref[:, on_or_below], **tol(d))
+    want = og.matmul_add(q, k, None, False, True, rounded=False)
+    assert_error_floor(s1[:, on_or_below], want[:, on_or_below],
+                       og.matmul_add_fma(q, k, None, False, True)[:, on_or_below])
     above = s1[:, ~on_or_below]
     assert np.all((above == 0) | np.isclose(above, ref[:, ~on_or_below], rtol=1e-4, atol=1e-3))
     # tri 2: P V with P lower triangular; tri 3: P^T V
     s2 = F().matmul_add(up(P), up(k), None, tri=2).numpy()
-    assert_close(s2, og.matmul_add(P, k), **tol(S))
+    check(s2, P, k)
     s3 = F().matmul_add(up(P), up(k), None, transpose_A=True, tri=3).numpy()
-    assert_close(s3, og.matmul_add(P, k, None, True, False), **tol(S))
+    check(s3, P, k, None, True, False)
     # equal to the untriangular product bit for bit (only exact zeros skipped)
     full2 = F().matmul_add(up(P), up(k), None).numpy()
     assert np.array_equal(s2, full2)
@@ -306,4 +301,4 @@ def test_matmul_per_batch_bias_strides(device, sbias_kind):
     P = C.c_void_p
     lib.call("wxx_matmul_add", P(tA.data_ptr()), P(tB.data_ptr()), P(tbias.data_ptr()),
              P(out.data_ptr()), M, N, K, b, M * K, 0, sb, 3, 0, 0, 0)
-    assert_close(out.numpy(), og.matmul_add(A, B, bias), **tol(K))
+    check(out.numpy(), A, B, bias)

@@ -3,7 +3,7 @@
 import numpy as np
 import pytest
 
-from conftest import assert_close, rng
+from conftest import assert_close, assert_error_floor, rng
 from oracle import activations as oa
 from oracle import reductions as orr
 
@@ -88,15 +88,18 @@ def test_maxmin_backward(device):
                                        ((2, 50304), -1), ((4, 6, 3), 1), ((5, 7), 0),
                                        ((33, 1), -1), ((10, 10), -1)])
 def test_softmax(device, shape, dim):
+    # every element (config 2's [8192 x 4096] included) against float64, at
+    # rtol 1e-5 plus 4x the error of the same steps in float32; the
+    # 96 x 1024 x 1024 attention case is checked on 64 of its rows, and its
+    # row sums everywhere
     x = (rng(7).standard_normal(shape) * 3).astype(np.float32)
     got = F().softmax(up(x), dim).numpy()
-    if np.prod(shape) > 20_000_000:
-        # large case: check invariants on all rows, values on a row sample
-        assert_close(got.sum(axis=dim), np.ones(got.sum(axis=dim).shape, np.float32), atol=2e-5)
-        idx = rng(8).integers(0, shape[0], 4)
-        assert_close(got[idx], oa.softmax(x[idx], dim))
-    else:
-        assert_close(got, oa.softmax(x, dim))
+    if np.prod(shape) > 50_000_000:
+        assert_close(got.sum(axis=dim), np.ones(got.sum(axis=dim).shape, np.float32), atol=2e-6)
+        idx = rng(8).integers(0, shape[0], 64)
+        got, x = got[idx], x[idx]
+    assert_error_floor(got, oa.softmax(x, dim, rounded=False), oa.softmax(x, dim, np.float32),
+                       rtol=1e-5)
 
 
 def test_softmax_reference_test_case(device):
@@ -120,7 +123,8 @@ def test_softmax_backward(device, shape, dim):
     y = oa.softmax(r.standard_normal(shape).astype(np.float32) * 2, dim)
     g = r.standard_normal(shape).astype(np.float32)
     got = F().softmax_backward(up(y), up(g), dim).numpy()
-    assert_close(got, oa.softmax_backward(y, g, dim), rtol=1e-4, atol=1e-6)
+    assert_error_floor(got, oa.softmax_backward(y, g, dim, rounded=False),
+                       oa.softmax_backward(y, g, dim, np.float32), rtol=1e-5)
 
 
 @pytest.mark.parametrize("src,shape,scale", [((1, 1), (4, 5), 1.0), ((4, 1), (4, 5), 0.25),
