@@ -284,10 +284,12 @@ def _train_setup(wxx, c, r):
     return m, loss, units, unit, desc
 
 
-def train_step(lib, name, steps, warmup):
+def train_step(lib, name, steps, warmup, graph_steps=None):
     """Full train step: forward, CCELoss, backward, clip_grad_norm_(1.0), AdamW,
     WarmupCosineLR (README.md:50-51 schedule), zero_grad.  Timed with the host
-    clock around ``steps`` steps between device synchronisations."""
+    clock around ``steps`` steps between device synchronisations, first run
+    eagerly (every op dispatched from Python), then recorded once as a step
+    graph and replayed ``graph_steps`` times (the same steps continue)."""
     import wxx_amd as wxx
 
     c = TRAIN_CONFIGS[name]
@@ -317,6 +319,23 @@ def train_step(lib, name, steps, warmup):
     if "flop" in c:
         out["tflops"] = c["flop"] / dt / 1e12
         out["frac_of_peak"] = out["tflops"] / PEAK_FP32_TFLOPS
+    graph_steps = steps if graph_steps is None else graph_steps
+    if graph_steps:
+        g = wxx.StepGraph(step).capture()
+        g.replay()  # first launch of a new graph uploads its code objects
+        lib.call("wxx_sync")
+        t0 = time.perf_counter()
+        for _ in range(graph_steps):
+            loss = g.replay()
+        lib.call("wxx_sync")
+        gdt = (time.perf_counter() - t0) / graph_steps
+        out["graph"] = {f"{unit}_per_s": units / gdt, "ms": gdt * 1e3,
+                        "steps_timed": graph_steps, "nodes": g.nodes,
+                        "loss": float(loss.numpy().reshape(-1)[0])}
+        if "flop" in c:
+            out["graph"]["tflops"] = c["flop"] / gdt / 1e12
+            out["graph"]["frac_of_peak"] = out["graph"]["tflops"] / PEAK_FP32_TFLOPS
+        g.close()
     return out
 
 

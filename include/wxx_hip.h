@@ -32,7 +32,8 @@ enum {
   WXX_E_OOM = -3,
   WXX_E_INIT = -4,
   WXX_E_RANGE = -5,
-  WXX_E_UNSUPPORTED = -6
+  WXX_E_UNSUPPORTED = -6,
+  WXX_E_CAPTURE = -7
 };
 
 /* ---- runtime: replaces WebGPUContext / GPUBufferPool / GPUCommandBuffer
@@ -62,6 +63,22 @@ int wxx_sync(void);
 void* wxx_stream(void);
 int wxx_timer_record(int slot);
 int wxx_timer_elapsed(int start, int stop, float* ms);
+
+/* ---- step graphs.  No reference counterpart: the reference re-encodes every
+ *      dispatch of every step (backend/device.py:15-16 notes that this host
+ *      cost dominates small models).  wxx_graph_begin starts recording the
+ *      library's stream; every entry point called until wxx_graph_end is
+ *      recorded, not run.  While recording: wxx_d2h, wxx_sync, the timers and
+ *      wxx_empty_cache fail with WXX_E_CAPTURE; wxx_h2d records a copy of the
+ *      bytes it is given (replays upload those same bytes); blocks allocated
+ *      belong to the graph until wxx_graph_destroy.  wxx_graph_launch replays
+ *      the whole recording with one launch, in stream order. */
+int wxx_graph_begin(void);
+int wxx_graph_end(void** graph, int64_t* nodes);
+int wxx_graph_abort(void);
+int wxx_graph_launch(void* graph);
+int wxx_graph_destroy(void* graph);
+int wxx_graph_capturing(int* on);
 
 /* ---- A: GEMM — functional.matmul_add (functional/utils.py:378-499) +
  *      shaders/matmul.wgsl.  sA/sB = batch strides (0 = unbatched);
@@ -311,6 +328,16 @@ int wxx_adamw_multi(void* const* p, void* const* g, void* const* m, void* const*
 int wxx_sumsq_multi(void* const* x, const int64_t* n, int count, float* out);
 /* No reference counterpart: the rescale loop of clip_grad_norm_ (nn/utils.py:97-101) */
 int wxx_scale_multi(void* const* x, const int64_t* n, int count, float c);
+/* No reference counterpart: wxx_adamw_multi reading its 7 hyperparameters
+ * (lr, beta1, beta2, eps, weight_decay, bc1, bc2) from device memory `hyper`
+ * when it runs, for recorded step graphs */
+int wxx_adamw_multi_dev(void* const* p, void* const* g, void* const* m, void* const* v,
+                        const int64_t* n, int count, const float* hyper);
+/* clip_grad_norm_'s decision and rescale (nn/utils.py:89-101) taken on the
+ * device from the sum of squares at `sumsq`: c = max_norm / (sqrt(s) + 1e-6)
+ * in float64, applied when c < 1; `norm` (may be null) gets sqrt(s) */
+int wxx_clip_scale_multi(void* const* x, const int64_t* n, int count, const float* sumsq,
+                         double max_norm, float* norm);
 
 /* ---- E6 / E7: embedding, dropout; C6: Hyena decay window ------------------ */
 /* functional.embed (functional/layers.py:161-206) */
@@ -321,6 +348,10 @@ int wxx_embeddx(const float* g, const uint32_t* ids, float* grad, int64_t ntok, 
                 int64_t V);
 /* functional.dropout / dropoutdx (functional/layers.py:73-158) */
 int wxx_dropout(const float* x, float* y, int64_t n, uint32_t seed, float p, float scale);
+/* No reference counterpart: wxx_dropout with the seed read from device memory
+ * `seed` when it runs, for recorded step graphs */
+int wxx_dropout_dev(const float* x, float* y, int64_t n, const uint32_t* seed, float p,
+                    float scale);
 /* functional.decay_window (functional/pointwise.py:357-404) */
 int wxx_decay_window(const float* decay, float* w, int64_t rows, int64_t channels,
                      int64_t length, int64_t stage);

@@ -73,7 +73,47 @@ hipError_t hipMalloc(void** p, size_t n) { *p = std::malloc(n ? n : 1); return *
 hipError_t hipFree(void* p) { std::free(p); return hipSuccess; }
 hipError_t hipHostMalloc(void** p, size_t n, unsigned) { *p = std::malloc(n); return hipSuccess; }
 hipError_t hipMemcpy(void* d, const void* s, size_t n, hipMemcpyKind) { std::memmove(d, s, n); return hipSuccess; }
-hipError_t hipMemcpyAsync(void* d, const void* s, size_t n, hipMemcpyKind, hipStream_t) { std::memmove(d, s, n); return hipSuccess; }
+hipError_t hipMemcpyAsync(void* d, const void* s, size_t n, hipMemcpyKind, hipStream_t) {
+  if (wxx_emu::capturing())
+    wxx_emu::record([d, s, n]() { std::memmove(d, s, n); });
+  else
+    std::memmove(d, s, n);
+  return hipSuccess;
+}
+hipError_t hipHostFree(void* p) { std::free(p); return hipSuccess; }
+
+namespace {
+using Ops = std::vector<std::function<void()>>;
+Ops* g_capture_ops = nullptr;
+}  // namespace
+namespace wxx_emu {
+bool capturing() { return g_capture_ops != nullptr; }
+void record(std::function<void()> op) { g_capture_ops->push_back(std::move(op)); }
+}  // namespace wxx_emu
+hipError_t hipStreamBeginCapture(hipStream_t, hipStreamCaptureMode) {
+  if (g_capture_ops) return 900;  // already capturing
+  g_capture_ops = new Ops;
+  return hipSuccess;
+}
+hipError_t hipStreamEndCapture(hipStream_t, hipGraph_t* g) {
+  *g = g_capture_ops;
+  g_capture_ops = nullptr;
+  return hipSuccess;
+}
+hipError_t hipGraphGetNodes(hipGraph_t g, hipGraphNode_t*, size_t* n) {
+  *n = static_cast<Ops*>(g)->size();
+  return hipSuccess;
+}
+hipError_t hipGraphInstantiate(hipGraphExec_t* e, hipGraph_t g, hipGraphNode_t*, char*, size_t) {
+  *e = new Ops(*static_cast<Ops*>(g));
+  return hipSuccess;
+}
+hipError_t hipGraphLaunch(hipGraphExec_t e, hipStream_t) {
+  for (auto& op : *static_cast<Ops*>(e)) op();
+  return hipSuccess;
+}
+hipError_t hipGraphExecDestroy(hipGraphExec_t e) { delete static_cast<Ops*>(e); return hipSuccess; }
+hipError_t hipGraphDestroy(hipGraph_t g) { delete static_cast<Ops*>(g); return hipSuccess; }
 hipError_t hipEventCreate(hipEvent_t* e) { *e = new float(0.f); return hipSuccess; }
 hipError_t hipEventCreateWithFlags(hipEvent_t* e, unsigned) { *e = new float(0.f); return hipSuccess; }
 hipError_t hipEventRecord(hipEvent_t e, hipStream_t) { *(float*)e = (g_fake_clock += 1.f); return hipSuccess; }

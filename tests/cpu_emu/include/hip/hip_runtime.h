@@ -229,5 +229,33 @@ inline hipError_t hipOccupancyMaxActiveBlocksPerMultiprocessor(int* n, F, int, s
 }
 const char* hipGetErrorString(hipError_t e);
 
+// Stream capture: while a capture is open, launches and copies are stored
+// (kernel arguments by value) and a graph launch runs them in order.
+typedef void* hipGraph_t;
+typedef void* hipGraphExec_t;
+typedef void* hipGraphNode_t;
+enum hipStreamCaptureMode { hipStreamCaptureModeGlobal, hipStreamCaptureModeThreadLocal,
+                            hipStreamCaptureModeRelaxed };
+hipError_t hipStreamBeginCapture(hipStream_t s, hipStreamCaptureMode m);
+hipError_t hipStreamEndCapture(hipStream_t s, hipGraph_t* g);
+hipError_t hipGraphGetNodes(hipGraph_t g, hipGraphNode_t* nodes, size_t* n);
+hipError_t hipGraphInstantiate(hipGraphExec_t* e, hipGraph_t g, hipGraphNode_t* err_node,
+                               char* log, size_t log_size);
+hipError_t hipGraphLaunch(hipGraphExec_t e, hipStream_t s);
+hipError_t hipGraphExecDestroy(hipGraphExec_t e);
+hipError_t hipGraphDestroy(hipGraph_t g);
+hipError_t hipHostFree(void* p);
+namespace wxx_emu {
+bool capturing();
+void record(std::function<void()> op);
+template <class F>
+inline void launch(F f, dim3 grid, dim3 block) {
+  if (capturing())
+    record([f, grid, block]() { run(f, grid, block); });
+  else
+    run(f, grid, block);
+}
+}  // namespace wxx_emu
+
 #define hipLaunchKernelGGL(KERNEL, GRID, BLOCK, SHMEM, STREAM, ...) \
-  wxx_emu::run([&]() { KERNEL(__VA_ARGS__); }, dim3(GRID), dim3(BLOCK))
+  wxx_emu::launch([=]() { KERNEL(__VA_ARGS__); }, dim3(GRID), dim3(BLOCK))

@@ -64,3 +64,19 @@ def test_reference_import_name_resolves_to_this_package():
     assert waf is aaf
     with pytest.raises(ModuleNotFoundError):
         __import__("wxx.no_such_module")
+
+
+def test_graph_hooks_outside_a_recording_are_refused():
+    # the per-replay words, hooks and checks exist only while a step graph is
+    # being recorded; outside one they raise instead of silently doing nothing
+    from wxx_amd import graphs
+
+    assert not graphs.capturing()
+    for fn, args in [(graphs.per_replay, (1, lambda w: None)), (graphs.on_replay, (print,)),
+                     (graphs.after_replay, (print,)), (graphs.keep_alive, (1,))]:
+        with pytest.raises(RuntimeError, match="recorded"):
+            fn(*args)
+    g = graphs.StepGraph(lambda: None)
+    with pytest.raises(RuntimeError, match="capture"):
+        g.replay()
+    g.close()  # closing an unrecorded graph is a no-op

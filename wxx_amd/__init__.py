@@ -8,7 +8,8 @@ first allocation.
 """
 
 from .Tensor import Parameter, Tensor
-from . import autograd, backend, functional, nn, serialization
+from . import autograd, backend, functional, graphs, nn, serialization
+from .graphs import StepGraph
 from .backend.device import get_device
 from .serialization import load, save
 

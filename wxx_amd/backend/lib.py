@@ -40,6 +40,13 @@ SIGNATURES = {
     "wxx_stream": (P, []),
     "wxx_timer_record": (I32, [I32]),
     "wxx_timer_elapsed": (I32, [I32, I32, C.POINTER(F32)]),
+    # step graphs
+    "wxx_graph_begin": (I32, []),
+    "wxx_graph_end": (I32, [C.POINTER(P), C.POINTER(I64)]),
+    "wxx_graph_abort": (I32, []),
+    "wxx_graph_launch": (I32, [P]),
+    "wxx_graph_destroy": (I32, [P]),
+    "wxx_graph_capturing": (I32, [C.POINTER(I32)]),
     # GEMM
     "wxx_matmul_add": (
         I32,
@@ -113,10 +120,13 @@ SIGNATURES = {
     "wxx_adamw_multi": (I32, [P, P, P, P, P, I32, F32, F32, F32, F32, F32, F32, F32]),
     "wxx_sumsq_multi": (I32, [P, P, I32, P]),
     "wxx_scale_multi": (I32, [P, P, I32, F32]),
+    "wxx_adamw_multi_dev": (I32, [P, P, P, P, P, I32, P]),
+    "wxx_clip_scale_multi": (I32, [P, P, I32, P, C.c_double, P]),
     # embedding / dropout / decay window
     "wxx_embed": (I32, [P, P, P, I64, I64, I64]),
     "wxx_embeddx": (I32, [P, P, P, I64, I64, I64]),
     "wxx_dropout": (I32, [P, P, I64, U32, F32, F32]),
+    "wxx_dropout_dev": (I32, [P, P, I64, P, F32, F32]),
     "wxx_decay_window": (I32, [P, P, I64, I64, I64, I64]),
     "wxx_decay_window_backward": (I32, [P, P, P, I64, I64, I64, I64]),
 }

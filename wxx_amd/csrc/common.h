@@ -64,7 +64,8 @@ enum {
   WXX_E_OOM = -3,        // device allocation failed
   WXX_E_INIT = -4,       // runtime not initialised / no device
   WXX_E_RANGE = -5,      // index data out of range (e.g. CCE target >= K)
-  WXX_E_UNSUPPORTED = -6 // shape/layout outside what a kernel supports
+  WXX_E_UNSUPPORTED = -6, // shape/layout outside what a kernel supports
+  WXX_E_CAPTURE = -7      // not allowed while a step graph is being captured
 };
 
 namespace wxx {
@@ -73,6 +74,7 @@ namespace wxx {
 hipStream_t stream();
 bool initialised();
 int set_error(int code, const char* fmt, ...);
+bool capturing();                    // a step graph is being captured
 void* scratch_alloc(size_t bytes);   // stream-ordered temporary from the cache
 void scratch_free(void* p);
 int num_cus();

@@ -979,6 +979,18 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
     } else {
       tile = 1;
       if (t64 < 2 * cus) splits = (int)std::min<int64_t>((8 * cus + t64 - 1) / t64, kmax);
+      // Short K (< 2048) over at most a quarter of the CUs' worth of tiles:
+      // these launches are latency-bound (about 1 us per 16-deep K step), so
+      // up to 8 power-of-two splits of >= 64 of K that keep the grid within
+      // one round of the CUs.  Measured on MI355X (config-1 shapes, split
+      // against unsplit): 256x256x512 (A^T) 11.1 / 20.8 us, 256x1024x512
+      // 13.4 / 21.1 us, 512x256x1024 13.3 / 32.6 us, 512x256x256 9.8 / 11.1
+      // us; 512x1024x256 (128 tiles) is fastest unsplit.
+      if (kmax == 1 && 4 * t64 <= cus) {
+        int s = 1;
+        while (s < 8 && t64 * s * 2 <= cus && g.K / (s * 2) >= 64) s *= 2;
+        splits = s;
+      }
     }
     splits = std::max(1, std::min(splits, tile == 4 ? 64 : 32));
   }

@@ -15,16 +15,16 @@
 //    backward (decay_window_backward.wgsl:24-46): dr_d = sum_t g[d,t] W[d,t]
 //    (-sign(r_d) t), written into the `stage` row of a zeroed (rows, channels).
 //
-// MI355X design: the embedding backward is deterministic.  Token ids are
-// stable-sorted with their token index (rocPRIM radix sort), ids are
-// histogrammed and scanned into per-row segments, and each vocabulary row is
-// produced by one pass that adds its tokens' gradient rows in token order
-// and writes zeros for unused rows (no separate zero-fill launch).
+// MI355X design: the embedding backward is deterministic and made of plain
+// kernels only (so it can be recorded into a step graph: no library sort, no
+// memset nodes).  Ids are histogrammed, the histogram is scanned into per-row
+// segment offsets, each segment is filled with its tokens in token order by
+// one thread per vocabulary row, and each vocabulary row is produced by one
+// pass that adds its tokens' gradient rows in token order and writes zeros
+// for unused rows (no separate zero-fill launch).
 #include "common.h"
 
 #include <cstring>
-#include <rocprim/device/device_radix_sort.hpp>
-#include <rocprim/device/device_scan.hpp>
 
 namespace {
 
@@ -53,16 +53,67 @@ __global__ __launch_bounds__(kBlock) void embed_kernel(const uint32_t* __restric
   }
 }
 
-__global__ __launch_bounds__(kBlock) void iota_hist_kernel(const uint32_t* __restrict__ ids,
-                                                           uint32_t* __restrict__ idx,
-                                                           uint32_t* __restrict__ counts,
-                                                           int64_t ntok, int64_t V) {
+// counts[v] = number of tokens with id v (ids >= V are not counted).  The
+// atomics only count, so the result does not depend on their order.
+__global__ __launch_bounds__(kBlock) void embed_hist_kernel(const uint32_t* __restrict__ ids,
+                                                            uint32_t* __restrict__ counts,
+                                                            int64_t ntok, int64_t V) {
   int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   const int64_t step = (int64_t)gridDim.x * kBlock;
   for (; t < ntok; t += step) {
-    idx[t] = (uint32_t)t;
     const uint32_t id = ids[t];
     if (id < (uint64_t)V) atomicAdd(&counts[id], 1u);
+  }
+}
+
+// out = exclusive prefix sum of in[0, n), by one workgroup: each thread sums a
+// contiguous run, the run totals are scanned in LDS, then each run is written.
+constexpr int kScanBlock = 1024;
+__global__ __launch_bounds__(kScanBlock) void exclusive_scan_u32_kernel(
+    const uint32_t* __restrict__ in, uint32_t* __restrict__ out, int64_t n) {
+  __shared__ uint32_t part[kScanBlock];
+  const int tid = threadIdx.x;
+  const int64_t per = (n + kScanBlock - 1) / kScanBlock;
+  const int64_t lo = min((int64_t)tid * per, n), hi = min(lo + per, n);
+  uint32_t run = 0;
+  for (int64_t i = lo; i < hi; ++i) run += in[i];
+  part[tid] = run;
+  __syncthreads();
+  for (int off = 1; off < kScanBlock; off <<= 1) {
+    const uint32_t add = tid >= off ? part[tid - off] : 0u;
+    __syncthreads();
+    part[tid] += add;
+    __syncthreads();
+  }
+  run = tid ? part[tid - 1] : 0u;
+  for (int64_t i = lo; i < hi; ++i) {
+    const uint32_t c = in[i];
+    out[i] = run;
+    run += c;
+  }
+}
+
+// sorted_tok[offsets[v] ...] = the tokens whose id is v, in token order: one
+// thread per id walks the ids (staged through LDS, read by every lane at the
+// same address) and appends each match, so each segment is stable without a
+// sort.  Work is V x ntok compares, V / 64 waves each reading ntok ids.
+constexpr int kPlaceChunk = 4096;
+__global__ __launch_bounds__(kBlock) void embed_place_kernel(const uint32_t* __restrict__ ids,
+                                                             const uint32_t* __restrict__ offsets,
+                                                             uint32_t* __restrict__ sorted_tok,
+                                                             int64_t ntok, int64_t V) {
+  __shared__ uint32_t sid[kPlaceChunk];
+  const int64_t v = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  uint32_t pos = v < V ? offsets[v] : 0u;
+  for (int64_t base = 0; base < ntok; base += kPlaceChunk) {
+    const int len = (int)min((int64_t)kPlaceChunk, ntok - base);
+    __syncthreads();
+    for (int i = threadIdx.x; i < len; i += kBlock) sid[i] = ids[base + i];
+    __syncthreads();
+    if (v < V) {
+      for (int i = 0; i < len; ++i)
+        if (sid[i] == (uint32_t)v) sorted_tok[pos++] = (uint32_t)(base + i);
+    }
   }
 }
 
@@ -106,9 +157,13 @@ __device__ __forceinline__ uint32_t drop_hash(uint32_t x) {
   return x;
 }
 
+// `seed_dev`, when set, holds the seed on the device (a step graph's replays
+// write a fresh one before each launch) and replaces `seed`.
 __global__ __launch_bounds__(kBlock) void dropout_kernel(const float* __restrict__ x,
                                                          float* __restrict__ y, int64_t n,
-                                                         uint32_t seed, float p, float scale) {
+                                                         uint32_t seed, float p, float scale,
+                                                         const uint32_t* __restrict__ seed_dev) {
+  if (seed_dev) seed = *seed_dev;
   int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   const int64_t step = (int64_t)gridDim.x * kBlock;
   for (; i < n; i += step) {
@@ -181,42 +236,29 @@ WXX_API int wxx_embeddx(const float* g, const uint32_t* ids, float* grad, int64_
   if (ntok <= 0) return wxx_fill_u32(grad, V * D, 0u);
   hipStream_t s = wxx::stream();
   const size_t n = (size_t)ntok;
-  uint32_t* buf = (uint32_t*)wxx::scratch_alloc(sizeof(uint32_t) * (4 * n + 2 * (size_t)V));
+  uint32_t* buf = (uint32_t*)wxx::scratch_alloc(sizeof(uint32_t) * (n + 2 * (size_t)V));
   if (!buf) return wxx::set_error(WXX_E_OOM, "embeddx scratch");
-  uint32_t* idx = buf;
-  uint32_t* keys_sorted = idx + n;
-  uint32_t* idx_sorted = keys_sorted + n;
-  uint32_t* counts = idx_sorted + n + n;
+  uint32_t* sorted_tok = buf;
+  uint32_t* counts = sorted_tok + n;
   uint32_t* offsets = counts + V;
   int rc = wxx_fill_u32(counts, V, 0u);
   if (rc) {
     wxx::scratch_free(buf);
     return rc;
   }
-  hipLaunchKernelGGL(iota_hist_kernel, dim3(wxx::grid_1d(ntok, kBlock, 16384)), dim3(kBlock), 0,
-                     s, ids, idx, counts, ntok, V);
+  hipLaunchKernelGGL(embed_hist_kernel, dim3(wxx::grid_1d(ntok, kBlock, 16384)), dim3(kBlock), 0,
+                     s, ids, counts, ntok, V);
+  hipLaunchKernelGGL(exclusive_scan_u32_kernel, dim3(1), dim3(kScanBlock), 0, s, counts, offsets,
+                     V);
+  hipLaunchKernelGGL(embed_place_kernel, dim3((unsigned)((V + kBlock - 1) / kBlock)),
+                     dim3(kBlock), 0, s, ids, offsets, sorted_tok, ntok, V);
   WXX_LAUNCHED();
-  size_t sort_bytes = 0, scan_bytes = 0;
-  WXX_HIP(rocprim::radix_sort_pairs(nullptr, sort_bytes, ids, keys_sorted, idx, idx_sorted, n, 0,
-                                    32, s));
-  WXX_HIP(rocprim::exclusive_scan(nullptr, scan_bytes, counts, offsets, 0u, (size_t)V,
-                                  rocprim::plus<uint32_t>(), s));
-  void* tmp = wxx::scratch_alloc(std::max(sort_bytes, scan_bytes) + 256);
-  if (!tmp) {
-    wxx::scratch_free(buf);
-    return wxx::set_error(WXX_E_OOM, "embeddx sort scratch");
-  }
-  WXX_HIP(rocprim::radix_sort_pairs(tmp, sort_bytes, ids, keys_sorted, idx, idx_sorted, n, 0, 32,
-                                    s));
-  WXX_HIP(rocprim::exclusive_scan(tmp, scan_bytes, counts, offsets, 0u, (size_t)V,
-                                  rocprim::plus<uint32_t>(), s));
   const int vec = (D % 4 == 0) && ((((uintptr_t)g) | ((uintptr_t)grad)) % 16 == 0);
   const int64_t dwork = vec ? D / 4 : D;
   const unsigned gy = (unsigned)std::min<int64_t>((dwork + kBlock - 1) / kBlock, 65535);
   hipLaunchKernelGGL(embed_segsum_kernel, dim3((unsigned)V, gy), dim3(kBlock), 0, s, g,
-                     idx_sorted, offsets, counts, grad, D, V, vec);
+                     sorted_tok, offsets, counts, grad, D, V, vec);
   WXX_LAUNCHED();
-  wxx::scratch_free(tmp);
   wxx::scratch_free(buf);
   return WXX_OK;
 }
@@ -229,7 +271,20 @@ WXX_API int wxx_dropout(const float* x, float* y, int64_t n, uint32_t seed, floa
   WXX_REQUIRE(x && y, "null pointer");
   if (n <= 0) return WXX_OK;
   hipLaunchKernelGGL(dropout_kernel, dim3(wxx::grid_1d(n, kBlock, 16384)), dim3(kBlock), 0,
-                     wxx::stream(), x, y, n, seed, p, scale);
+                     wxx::stream(), x, y, n, seed, p, scale, (const uint32_t*)nullptr);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// wxx_dropout with the seed read on the device from `seed` when the kernel
+// runs (for recorded step graphs; no reference counterpart).
+WXX_API int wxx_dropout_dev(const float* x, float* y, int64_t n, const uint32_t* seed, float p,
+                            float scale) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(x && y && seed, "null pointer");
+  if (n <= 0) return WXX_OK;
+  hipLaunchKernelGGL(dropout_kernel, dim3(wxx::grid_1d(n, kBlock, 16384)), dim3(kBlock), 0,
+                     wxx::stream(), x, y, n, 0u, p, scale, seed);
   WXX_LAUNCHED();
   return WXX_OK;
 }

@@ -73,8 +73,12 @@ __device__ __forceinline__ int find_tensor(const TensorDesc* d, int nt, int64_t 
   return lo;
 }
 
+// `hd`, when set, is a device copy of the hyperparameters that replaces `h`
+// (a step graph's replays update it between launches).
 __global__ __launch_bounds__(kBlock) void adamw_multi_kernel(const TensorDesc* __restrict__ d,
-                                                             int nt, AdamHyper h) {
+                                                             int nt, AdamHyper h,
+                                                             const AdamHyper* __restrict__ hd) {
+  if (hd) h = *hd;
   const int ti = find_tensor(d, nt, blockIdx.x);
   const TensorDesc td = d[ti];
   const int64_t base = (blockIdx.x - td.first_block) * (int64_t)kChunk;
@@ -135,8 +139,26 @@ __global__ __launch_bounds__(kBlock) void sum_partials_kernel(const float* __res
   if (threadIdx.x == 0) out[0] = acc;
 }
 
+// The clip coefficient from the device sum of squares, with the host's
+// float64 arithmetic: norm = sqrt(s), c = max_norm / (norm + 1e-6), applied
+// (rounded to f32) only when c < 1.  Both operations are correctly rounded, so
+// the coefficient equals the one the host computes from the same sum.
+__device__ __forceinline__ float clip_coef(const float* sumsq, double max_norm, bool* apply) {
+  const double norm = sqrt((double)sumsq[0]);
+  const double c = max_norm / (norm + 1e-6);
+  *apply = c < 1.0;
+  return (float)c;
+}
+
 __global__ __launch_bounds__(kBlock) void scale_multi_kernel(const TensorDesc* __restrict__ d,
-                                                             int nt, float c) {
+                                                             int nt, float c,
+                                                             const float* __restrict__ sumsq,
+                                                             double max_norm) {
+  if (sumsq) {
+    bool apply;
+    c = clip_coef(sumsq, max_norm, &apply);
+    if (!apply) return;
+  }
   const int ti = find_tensor(d, nt, blockIdx.x);
   const TensorDesc td = d[ti];
   const int64_t base = (blockIdx.x - td.first_block) * (int64_t)kChunk;
@@ -201,7 +223,29 @@ WXX_API int wxx_adamw_multi(void* const* p, void* const* g, void* const* m, void
   AdamHyper h{lr, beta1, beta2, eps, weight_decay, bc1, bc2};
   if (blocks > 0)
     hipLaunchKernelGGL(adamw_multi_kernel, dim3((unsigned)blocks), dim3(kBlock), 0,
-                       wxx::stream(), d, count, h);
+                       wxx::stream(), d, count, h, (const AdamHyper*)nullptr);
+  wxx::scratch_free(d);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// wxx_adamw_multi with the hyperparameters read on the device from `hyper`
+// (7 floats: lr, beta1, beta2, eps, weight_decay, bc1, bc2) when the kernel
+// runs, so a recorded step graph picks up each step's learning rate and bias
+// corrections.  No reference counterpart (the reference has no graphs).
+WXX_API int wxx_adamw_multi_dev(void* const* p, void* const* g, void* const* m, void* const* v,
+                                const int64_t* n, int count, const float* hyper) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(p && g && m && v && n && hyper && count >= 0, "null pointer");
+  if (count == 0) return WXX_OK;
+  TensorDesc* d = nullptr;
+  int64_t blocks = 0;
+  int rc = upload_table(p, g, m, v, n, count, &d, &blocks);
+  if (rc) return rc;
+  AdamHyper h{};
+  if (blocks > 0)
+    hipLaunchKernelGGL(adamw_multi_kernel, dim3((unsigned)blocks), dim3(kBlock), 0,
+                       wxx::stream(), d, count, h, (const AdamHyper*)hyper);
   wxx::scratch_free(d);
   WXX_LAUNCHED();
   return WXX_OK;
@@ -245,7 +289,37 @@ WXX_API int wxx_scale_multi(void* const* x, const int64_t* n, int count, float c
   if (rc) return rc;
   if (blocks > 0)
     hipLaunchKernelGGL(scale_multi_kernel, dim3((unsigned)blocks), dim3(kBlock), 0,
-                       wxx::stream(), d, count, c);
+                       wxx::stream(), d, count, c, (const float*)nullptr, 0.0);
+  wxx::scratch_free(d);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+__global__ void clip_norm_kernel(const float* __restrict__ sumsq, float* __restrict__ norm) {
+  if (threadIdx.x == 0) norm[0] = (float)sqrt((double)sumsq[0]);
+}
+
+// The rescale of clip_grad_norm_ (reference src/wxx/nn/utils.py:95-101) with
+// the coefficient decided on the device from `sumsq` (wxx_sumsq_multi's
+// output), so no readback sits between the norm and the rescale; `norm`
+// (optional) receives sqrt(sumsq) rounded to f32.
+WXX_API int wxx_clip_scale_multi(void* const* x, const int64_t* n, int count,
+                                 const float* sumsq, double max_norm, float* norm) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(x && n && sumsq && count >= 0, "null pointer");
+  if (norm)
+    hipLaunchKernelGGL(clip_norm_kernel, dim3(1), dim3(64), 0, wxx::stream(), sumsq, norm);
+  if (count == 0) {
+    WXX_LAUNCHED();
+    return WXX_OK;
+  }
+  TensorDesc* d = nullptr;
+  int64_t blocks = 0;
+  int rc = upload_table(x, nullptr, nullptr, nullptr, n, count, &d, &blocks);
+  if (rc) return rc;
+  if (blocks > 0)
+    hipLaunchKernelGGL(scale_multi_kernel, dim3((unsigned)blocks), dim3(kBlock), 0,
+                       wxx::stream(), d, count, 0.f, sumsq, max_norm);
   wxx::scratch_free(d);
   WXX_LAUNCHED();
   return WXX_OK;

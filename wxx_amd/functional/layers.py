@@ -4,7 +4,7 @@ import ctypes as C
 import math
 import random
 
-from .. import validation
+from .. import graphs, validation
 from ._common import Tensor, call, empty, ptr
 
 
@@ -38,6 +38,56 @@ def adamw_multi(params, grads, exp_avgs, exp_avg_sqs, lr, beta1, beta2, eps, wei
         sizes[i] = n
     call("wxx_adamw_multi", *arrs, sizes, count, float(lr), float(beta1), float(beta2),
          float(eps), float(weight_decay), float(bc1), float(bc2))
+
+
+def _multi_tables(groups, what):
+    """ctypes pointer arrays (one per tensor role) and element counts for a
+    multi-tensor launch; every group holds contiguous tensors of one size."""
+    count = len(groups)
+    arrs = [(C.c_void_p * count)() for _ in range(len(groups[0]))]
+    sizes = (C.c_int64 * count)()
+    for i, group in enumerate(groups):
+        n = validation.numel(group[0].shape)
+        for a, t in zip(arrs, group):
+            if validation.numel(t.shape) != n or not t.is_contiguous() or t.type != "f32":
+                raise ValueError(f"{what} expects contiguous f32 tensors of matching size")
+            a[i] = t.data_ptr()
+        sizes[i] = n
+    return arrs, sizes
+
+
+def adamw_multi_dev(params, grads, exp_avgs, exp_avg_sqs, hyper):
+    """:func:`adamw_multi` with the hyper-parameters (lr, beta1, beta2, eps,
+    weight_decay, bc1, bc2 as 7 f32 words) read from device address ``hyper``
+    when the kernel runs."""
+    if not params:
+        return
+    arrs, sizes = _multi_tables(list(zip(params, grads, exp_avgs, exp_avg_sqs)), "adamw_multi")
+    call("wxx_adamw_multi_dev", *arrs, sizes, len(params), C.c_void_p(hyper))
+
+
+def _unique_storages(tensors):
+    seen, uniq = set(), []
+    for t in tensors:
+        key = (t.data_ptr(), validation.numel(t.shape))
+        if key not in seen:
+            seen.add(key)
+            uniq.append(t)
+    return uniq
+
+
+def clip_scale_multi(tensors, sumsq, max_norm):
+    """Rescale ``tensors`` in place by max_norm / (sqrt(s) + 1e-6) when that
+    is below 1, with s the device scalar ``sumsq`` (decided on the device);
+    returns a (1,) tensor holding sqrt(s)."""
+    norm = empty((1,))
+    uniq = _unique_storages(tensors)
+    if uniq:
+        (arr,), sizes = _multi_tables([(t,) for t in uniq], "clip_scale_multi")
+    else:
+        arr, sizes = (C.c_void_p * 1)(), (C.c_int64 * 1)()
+    call("wxx_clip_scale_multi", arr, sizes, len(uniq), ptr(sumsq), float(max_norm), ptr(norm))
+    return norm
 
 
 def sumsq_multi(tensors):
@@ -91,6 +141,20 @@ def _copy_of(t):
     return out
 
 
+class DeviceSeed:
+    """A dropout seed that lives in a step graph's per-replay words (device
+    address ``ptr``): each replay writes a fresh draw of the host RNG there."""
+
+    __slots__ = ("ptr",)
+
+    def __init__(self, ptr):
+        self.ptr = ptr
+
+
+def _draw_seed(words):
+    words[0] = random.randint(0, 2**32 - 1)
+
+
 def dropout(tensor1, p, share_at_zero=False):
     """Inverted dropout; returns ``(y, seed)`` with a fresh 32-bit seed per call.
 
@@ -106,11 +170,19 @@ def dropout(tensor1, p, share_at_zero=False):
         tensor1 = tensor1.contiguous()
     n = math.prod(tensor1.shape)
     scale = 1 / (1 - p)
-    r = random.randint(0, 2**32 - 1)
+    if graphs.capturing():
+        # each replay draws this call's seed from the host RNG, in call order
+        r = DeviceSeed(graphs.per_replay(1, _draw_seed))
+    else:
+        r = random.randint(0, 2**32 - 1)
     if p == 0:
         return (_same_values(tensor1) if share_at_zero else _copy_of(tensor1)), r
     out = empty(tensor1.shape)
-    call("wxx_dropout", ptr(tensor1), ptr(out), n, r, float(p), float(scale))
+    if isinstance(r, DeviceSeed):
+        call("wxx_dropout_dev", ptr(tensor1), ptr(out), n, C.c_void_p(r.ptr), float(p),
+             float(scale))
+    else:
+        call("wxx_dropout", ptr(tensor1), ptr(out), n, r, float(p), float(scale))
     return out, r
 
 
@@ -124,8 +196,12 @@ def dropoutdx(tensor1, p, seed, share_at_zero=False):
         return _same_values(tensor1) if share_at_zero else _copy_of(tensor1)
     n = math.prod(tensor1.shape)
     out = empty(tensor1.shape)
-    call("wxx_dropout", ptr(tensor1), ptr(out), n, int(seed) & 0xFFFFFFFF, float(p),
-         float(1 / (1 - p)))
+    if isinstance(seed, DeviceSeed):
+        call("wxx_dropout_dev", ptr(tensor1), ptr(out), n, C.c_void_p(seed.ptr), float(p),
+             float(1 / (1 - p)))
+    else:
+        call("wxx_dropout", ptr(tensor1), ptr(out), n, int(seed) & 0xFFFFFFFF, float(p),
+             float(1 / (1 - p)))
     return out
 
 

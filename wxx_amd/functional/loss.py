@@ -4,7 +4,7 @@ import ctypes as C
 
 import numpy as np
 
-from .. import validation
+from .. import graphs, validation
 from ..backend import lib as _lib
 from ._common import call, empty, ptr
 
@@ -12,12 +12,34 @@ _bad_flag = {"buf": None}
 
 
 def _flag():
-    """A persistent 4-byte device word for the out-of-range-target flag."""
-    if _bad_flag["buf"] is None:
-        from ..backend.device import get_buffer_pool
+    """The 4-byte device word for the out-of-range-target flag: a persistent
+    one, or inside a step graph recording one per call (checked after every
+    replay)."""
+    from ..backend.device import get_buffer_pool
 
+    if graphs.capturing():
+        return get_buffer_pool().create_buffer(4, label="cceloss flag (graph)")
+    if _bad_flag["buf"] is None:
         _bad_flag["buf"] = get_buffer_pool().create_buffer(4, label="cceloss flag")
     return _bad_flag["buf"]
+
+
+def _raise_if_flagged(flag, targets, K):
+    bad = np.zeros(1, np.int32)
+    _lib.call("wxx_d2h", bad.ctypes.data_as(C.c_void_p), C.c_void_p(flag.ptr), 4)
+    if bad[0]:
+        tmax = int(targets.numpy().max())
+        raise ValueError(f"cceloss targets must be in [0, {K}), got max target {tmax}")
+
+
+def _check_targets(flag, targets, K):
+    """Raise now (eager), or after every replay of the step graph being
+    recorded, when a target was out of range."""
+    if graphs.capturing():
+        graphs.keep_alive(flag, targets)
+        graphs.after_replay(lambda: _raise_if_flagged(flag, targets, K))
+    else:
+        _raise_if_flagged(flag, targets, K)
 
 
 def cceloss(tensor1, tensor2):
@@ -50,20 +72,8 @@ def cceloss(tensor1, tensor2):
     grad = empty(tensor1.shape)
     call("wxx_cceloss", ptr(tensor1), ptr(tensor2), ptr(loss), ptr(grad), B, K,
          C.c_void_p(flag.ptr))
-    bad = np.zeros(1, np.int32)
-    _lib.call("wxx_d2h", bad.ctypes.data_as(C.c_void_p), C.c_void_p(flag.ptr), 4)
-    if bad[0]:
-        tmax = int(tensor2.numpy().max())
-        raise ValueError(f"cceloss targets must be in [0, {K}), got max target {tmax}")
+    _check_targets(flag, tensor2, K)
     return loss, grad
-
-
-def _check_targets(tensor1, tensor2, flag, K):
-    bad = np.zeros(1, np.int32)
-    _lib.call("wxx_d2h", bad.ctypes.data_as(C.c_void_p), C.c_void_p(flag.ptr), 4)
-    if bad[0]:
-        tmax = int(tensor2.numpy().max())
-        raise ValueError(f"cceloss targets must be in [0, {K}), got max target {tmax}")
 
 
 def cceloss_stats(tensor1, tensor2):
@@ -89,7 +99,7 @@ def cceloss_stats(tensor1, tensor2):
     stats = empty((B, 2))
     call("wxx_cceloss_stats", ptr(tensor1), ptr(tensor2), ptr(loss), ptr(stats), B, K,
          C.c_void_p(flag.ptr))
-    _check_targets(tensor1, tensor2, flag, K)
+    _check_targets(flag, tensor2, K)
     return loss, stats, tensor1, tensor2
 
 

@@ -11,7 +11,7 @@ which every storage appears once, and the rounds run in order.
 
 import numpy as np
 
-from .. import functional
+from .. import functional, graphs
 from ..backend.device import get_cmd_buffer
 from ..Tensor import Tensor
 
@@ -46,6 +46,17 @@ class SGD(Optimizer):
         self.lr = lr
 
     def step(self):
+        if graphs.capturing():
+            # the rate is a kernel argument of the recorded update: a replay
+            # with another rate would silently apply the recorded one
+            recorded = self.lr
+
+            def same_rate():
+                if self.lr != recorded:
+                    raise RuntimeError(f"SGD's learning rate {recorded} is recorded in this "
+                                       f"step graph; record it again to use {self.lr}")
+
+            graphs.on_replay(same_rate)
         for _, w in self.parameters:
             functional._pointwise(w, -self.lr * w.grad, 0)
 
@@ -115,10 +126,34 @@ class AdamW(Optimizer):
         self.eps = float(state["eps"])
         self.weight_decay = float(state["weight_decay"])
 
-    def step(self):
+    def _advance(self):
+        """Host half of a step: the step count and its bias corrections."""
         self.step_count += 1
-        bc1 = 1.0 - self.beta1 ** self.step_count
-        bc2 = 1.0 - self.beta2 ** self.step_count
+        return 1.0 - self.beta1 ** self.step_count, 1.0 - self.beta2 ** self.step_count
+
+    def _replay_words(self, words):
+        bc1, bc2 = self._advance()
+        words.view(np.float32)[:] = (self.lr, self.beta1, self.beta2, self.eps,
+                                     self.weight_decay, bc1, bc2)
+
+    def _record_step(self):
+        """The step inside a step graph: the update kernels read this step's
+        hyper-parameters from per-replay device words, which each replay
+        fills from the host state (step count, current learning rate)."""
+        hyper = graphs.per_replay(7, self._replay_words)
+        live = [(w, st) for (_, w), st in zip(self.params, self.state) if w.grad is not None]
+        for rnd in _rounds(live, key=lambda ws: (ws[0].buffer.ptr, ws[0].offset)):
+            ps = [w for w, _ in rnd]
+            if not all(p.is_contiguous() for p in ps):
+                raise RuntimeError("a step graph needs contiguous parameters for AdamW")
+            gs = [w.grad if w.grad.is_contiguous() else w.grad.contiguous() for w, _ in rnd]
+            functional.adamw_multi_dev(ps, gs, [st["exp_avg"] for _, st in rnd],
+                                       [st["exp_avg_sq"] for _, st in rnd], hyper)
+
+    def step(self):
+        if graphs.capturing():
+            return self._record_step()
+        bc1, bc2 = self._advance()
         live = [(w, st) for (_, w), st in zip(self.params, self.state) if w.grad is not None]
         for rnd in _rounds(live, key=lambda ws: (ws[0].buffer.ptr, ws[0].offset)):
             ps, gs, ms, vs = [], [], [], []

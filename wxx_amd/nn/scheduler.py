@@ -15,6 +15,8 @@ form, since it climbs from base_lr / warmup to base_lr.
 
 import math
 
+from .. import graphs
+
 
 def _half_cosine(done, span=1.0):
     """1 at done = 0, 0 at done = span, along half a cosine period."""
@@ -52,7 +54,15 @@ class LRScheduler:
         return self._last_lr
 
     def step(self, epoch=None):
-        """Advance to the next step (or to ``epoch``) and write its rate."""
+        """Advance to the next step (or to ``epoch``) and write its rate.
+        Inside a step graph recording the advance runs before every replay
+        instead (the optimizer's recorded update reads the rate then)."""
+        if graphs.capturing():
+            graphs.on_replay(lambda: self._advance(epoch))
+            return self._last_lr
+        return self._advance(epoch)
+
+    def _advance(self, epoch):
         self.last_epoch = self.last_epoch + 1 if epoch is None else int(epoch)
         return self._write(self.get_lr())
 

@@ -2,7 +2,7 @@
 
 import numpy as np
 
-from .. import functional
+from .. import functional, graphs
 
 
 def _iter_params(parameters):
@@ -26,12 +26,27 @@ def clip_grad_norm_(parameters, max_norm, norm_type=2.0):
     rescale.  A gradient listed twice (aliased parameters) counts twice in the
     norm and is rescaled once, as in the reference.  Other norms read the
     gradients back to the host, as the reference's fallback does.
+
+    Inside a step graph recording nothing may be read back: the coefficient
+    is decided on the device (same float64 arithmetic) and the norm is
+    returned as a (1,) device tensor that each replay rewrites.
     """
     pairs = [(p, p.grad) for p in _iter_params(parameters) if p.grad is not None]
     if not pairs:
         return 0.0
     grads = [g for _, g in pairs]
-    if norm_type == 2.0 and all(g.type == "f32" and g.offset == 0 for g in grads):
+    l2_f32 = norm_type == 2.0 and all(g.type == "f32" and g.offset == 0 for g in grads)
+    if graphs.capturing():
+        if not l2_f32:
+            raise RuntimeError("inside a step graph clip_grad_norm_ supports the L2 norm "
+                               "of f32 gradients only")
+        dense = [g if g.is_contiguous() else g.contiguous() for g in grads]
+        norm = functional.clip_scale_multi(dense, functional.sumsq_multi(dense), max_norm)
+        for (p, g), d in zip(pairs, dense):
+            if d is not g:
+                p.grad = d
+        return norm
+    if l2_f32:
         dense = [g if g.is_contiguous() else g.contiguous() for g in grads]
         total = float(functional.sumsq_multi(dense).numpy()[0]) ** 0.5
         coef = max_norm / (total + 1e-6)

@@ -16,7 +16,7 @@ MAX_RANK = 6
 
 def numel(shape):
     """Number of elements of ``shape``; a 0-d shape holds one."""
-    return int(math.prod(shape)) if len(shape) else 1
+    return math.prod(shape)
 
 
 def _as_int(value):
@@ -130,18 +130,29 @@ def check_broadcastable(shape, out_shape, *, name="tensor"):
 
 def contiguous_strides(shape):
     """Row-major element strides of ``shape``."""
-    out, step = [], 1
-    for size in reversed(shape):
-        out.append(step)
-        step *= size
-    return tuple(reversed(out))
+    rank = len(shape)
+    if rank == 1:
+        return (1,)
+    if rank == 2:
+        return (shape[1], 1)
+    out = [1] * rank
+    step = 1
+    for d in range(rank - 1, 0, -1):
+        step *= shape[d]
+        out[d - 1] = step
+    return tuple(out)
 
 
 def is_contiguous_layout(shape, stride):
     """Whether ``stride`` lays ``shape`` out row-major and dense (the stride
     of a dimension of size 0 or 1 does not matter)."""
-    want = contiguous_strides(shape)
-    return all(size <= 1 or s == w for size, s, w in zip(shape, stride, want))
+    want = 1
+    for d in range(len(shape) - 1, -1, -1):
+        size = shape[d]
+        if size > 1 and stride[d] != want:
+            return False
+        want *= size
+    return True
 
 
 def check_contiguous(tensor, *, name="tensor"):
