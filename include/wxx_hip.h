@@ -352,6 +352,22 @@ int wxx_dropout(const float* x, float* y, int64_t n, uint32_t seed, float p, flo
  * `seed` when it runs, for recorded step graphs */
 int wxx_dropout_dev(const float* x, float* y, int64_t n, const uint32_t* seed, float p,
                     float scale);
+/* ---- fused attention: MultiHeadAttention's score / softmax / dropout /
+ *      value path (nn/module.py:460-495) for (B, S, H, d) projections, d in
+ *      {32, 64, 128}, 16-byte aligned; causal 1 = GPT-2's causal mask, 0 = no
+ *      mask; dropout keeps element (b*H+h, i, j) of the probabilities as
+ *      functional.dropout does for that flat index under `seed` (or *seed_dev
+ *      when seed_dev is set).  lse: B*H*S row log-sum-exps for the backward. */
+int wxx_attention_fwd(const float* q, const float* k, const float* v, float* out, float* lse,
+                      int64_t batch, int64_t seq, int64_t heads, int64_t head_dim, int causal,
+                      float scale, float p_drop, float drop_scale, uint32_t seed,
+                      const uint32_t* seed_dev);
+int wxx_attention_bwd(const float* q, const float* k, const float* v, const float* out,
+                      const float* dout, const float* lse, float* dq, float* dk, float* dv,
+                      int64_t batch, int64_t seq, int64_t heads, int64_t head_dim, int causal,
+                      float scale, float p_drop, float drop_scale, uint32_t seed,
+                      const uint32_t* seed_dev);
+
 /* functional.decay_window (functional/pointwise.py:357-404) */
 int wxx_decay_window(const float* decay, float* w, int64_t rows, int64_t channels,
                      int64_t length, int64_t stage);

@@ -81,18 +81,20 @@ def assert_close(actual, expected, rtol=1e-4, atol=1e-5, msg=""):
         )
 
 
-def assert_error_floor(got, want64, ref32, c=4.0, rtol=1e-4, msg=""):
+def assert_error_floor(got, want64, ref32, c=4.0, rtol=1e-4, msg="", atol=0.0):
     """A float result against float64 with the float32 rounding floor as the
     yardstick: ref32 is the same sums evaluated in single precision (another
     order), and the device may miss the float64 value by at most c times
-    the largest miss of ref32 (plus rtol of the element itself).  Unlike a
-    tolerance scaled by sqrt(K), a wrong or dropped term (an error far above
-    what single precision produces) fails."""
+    the largest miss of ref32 (plus rtol of the element itself, plus atol).
+    Unlike a tolerance scaled by sqrt(K), a wrong or dropped term (an error
+    far above what single precision produces) fails.  ``atol`` is for
+    results that are exact zeros in the composition the floor is taken
+    from but sums of cancelling terms in another order."""
     got, w, f = (np.asarray(a, np.float64) for a in (got, want64, ref32))
     assert got.shape == w.shape, f"{msg} shape {got.shape} != {w.shape}"
     floor = float(np.abs(f - w).max()) if f.size else 0.0
     err = np.abs(got - w)
-    bad = err > c * floor + rtol * np.abs(w) + 1e-30
+    bad = err > c * floor + rtol * np.abs(w) + atol + 1e-30
     if bad.any():
         raise AssertionError(f"{msg} {int(bad.sum())} of {bad.size} elements beyond {c} x the "
                              f"fp32 floor {floor:.3g}; max err {err.max():.3g}")

@@ -284,3 +284,41 @@ def test_resnet_oracle_replaying_its_own_decisions_changes_nothing():
     bad["relu"][3].reshape(-1)[:50] ^= True
     _, g3, _, _ = orn.resnet18_loss_and_grads(P, S, x, y, forced=bad)
     assert any(not np.array_equal(g1[k], g3[k]) for k in g1)
+
+
+@pytest.mark.parametrize("causal,p", [(False, 0.0), (True, 0.0), (True, 0.3), (False, 0.25)])
+def test_attention_oracle_against_torch(causal, p):
+    # forward against torch's own float64 scaled_dot_product_attention (no
+    # dropout), and forward + gradients against torch autograd of the
+    # composition with the oracle's dropout mask as a constant multiplier
+    from oracle import attention as oa
+    from oracle.layers import dropout_keep
+
+    B, S, H, d, seed = 2, 19, 3, 4, 1234
+    r = rng(5)
+    q, k, v, do = (r.standard_normal((B, S, H * d)) for _ in range(4))
+    got = oa.attention(q, k, v, H, causal, p, seed)
+    grads = oa.attention_grads(q, k, v, do, H, causal, p, seed)
+
+    tq, tk, tv = (torch.tensor(t, dtype=torch.float64, requires_grad=True) for t in (q, k, v))
+    split = lambda t: t.reshape(B, S, H, d).permute(0, 2, 1, 3)  # noqa: E731
+    if p == 0:
+        sd = TF.scaled_dot_product_attention(split(tq), split(tk), split(tv), is_causal=causal)
+        assert_close(sd.permute(0, 2, 1, 3).reshape(B, S, H * d).detach().numpy(), got,
+                     rtol=1e-12, atol=1e-12)
+    scores = split(tq) @ split(tk).transpose(-1, -2) / np.sqrt(d)
+    if causal:
+        scores = scores.masked_fill(torch.ones(S, S, dtype=torch.bool).triu(1), float("-inf"))
+    probs = torch.softmax(scores, -1)
+    if p:
+        keep = dropout_keep(B * H * S * S, seed, p).reshape(B, H, S, S)
+        probs = probs * torch.tensor(keep / (1 - p), dtype=torch.float64)
+    out = (probs @ split(tv)).permute(0, 2, 1, 3).reshape(B, S, H * d)
+    assert_close(out.detach().numpy(), got, rtol=1e-12, atol=1e-12)
+    out.backward(torch.tensor(do))
+    for name, t, g in zip("qkv", (tq, tk, tv), grads):
+        assert_close(g, t.grad.numpy(), rtol=1e-10, atol=1e-12, msg=f"d{name}")
+    # dropout reaches the gradients (a dropped-out oracle is not the plain one)
+    if p:
+        plain = oa.attention_grads(q, k, v, do, H, causal, 0.0, seed)
+        assert not np.allclose(plain[2], grads[2])

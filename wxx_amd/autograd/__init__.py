@@ -12,7 +12,7 @@ from .convolution import (
     maxpooling1d,
     maxpooling2d,
 )
-from .layers import CrossEntropyLoss, Dropout, Embedding
+from .layers import CrossEntropyLoss, Dropout, Embedding, FusedAttention
 from .normalization import batchnorm, meanvarnorm, rmsnorm
 from .pointwise import (
     abs,

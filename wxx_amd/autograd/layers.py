@@ -58,3 +58,31 @@ class Embedding(Function):
             return None, None
         ids, self.ids = self.ids, None
         return None, functional.embeddx(g, ids, self.n_token, self.embed_dim, self.vocab_size)
+
+
+class FusedAttention(Function):
+    """Per head softmax(q k^T / sqrt(d) [+ causal mask]), dropout, times v, as
+    one Function over the (B, S, D) projections: the reference's head
+    permutes, score matmul, scale, mask add, softmax, dropout and value
+    matmul (nn/module.py:460-495).  Inputs: q, k, v."""
+
+    def forward(self, q, k, v, n_heads, causal, p=None):
+        # p None: inference (the reference's Dropout is the identity and draws
+        # no seed); otherwise one seed per call, drawn even at p == 0
+        seed = 0 if p is None else functional.attention_ops.draw_seed()
+        p = 0.0 if p is None else float(p)
+        out, lse = functional.fused_attention(q, k, v, n_heads, causal, p, seed)
+        out.requires_grad = any(t.requires_grad for t in (q, k, v))
+        # the output is kept through a second tensor over its storage, so the
+        # output does not reference its creator through the saved state
+        saved_out = functional.layers._same_values(out) if out.requires_grad else None
+        return self.attach(out, q=q, k=k, v=v, o=saved_out, lse=lse, seed=seed,
+                           n_heads=n_heads, causal=causal, p=p)
+
+    def backward(self, g):
+        if not any(self.needs_input_grad):
+            return None, None, None
+        grads = functional.fused_attention_backward(self.q, self.k, self.v, self.o, g, self.lse,
+                                                    self.n_heads, self.causal, self.p, self.seed)
+        self.q = self.k = self.v = self.o = self.lse = None
+        return tuple(d if need else None for d, need in zip(grads, self.needs_input_grad))

@@ -127,6 +127,9 @@ SIGNATURES = {
     "wxx_embeddx": (I32, [P, P, P, I64, I64, I64]),
     "wxx_dropout": (I32, [P, P, I64, U32, F32, F32]),
     "wxx_dropout_dev": (I32, [P, P, I64, P, F32, F32]),
+    # fused attention
+    "wxx_attention_fwd": (I32, [P, P, P, P, P, I64, I64, I64, I64, I32, F32, F32, F32, U32, P]),
+    "wxx_attention_bwd": (I32, [P] * 9 + [I64, I64, I64, I64, I32, F32, F32, F32, U32, P]),
     "wxx_decay_window": (I32, [P, P, I64, I64, I64, I64]),
     "wxx_decay_window_backward": (I32, [P, P, P, I64, I64, I64, I64]),
 }

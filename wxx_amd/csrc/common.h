@@ -169,6 +169,21 @@ __device__ __forceinline__ float block_max(float v, float* red) {
   return t;
 }
 
+// Dropout's keep decision for element `idx` (its flat index, truncated to 32
+// bits) under `seed` (reference shaders/layers/dropout.wgsl:14-36): with
+// h(x) = ((x>>16)^x)*0x45d9f3b twice then (x>>16)^x, the element is kept when
+// f32(h(idx ^ seed) >> 8) * 2^-24 >= p.
+__device__ __forceinline__ uint32_t drop_hash(uint32_t x) {
+  x = ((x >> 16) ^ x) * 0x45d9f3bu;
+  x = ((x >> 16) ^ x) * 0x45d9f3bu;
+  x = (x >> 16) ^ x;
+  return x;
+}
+
+__device__ __forceinline__ bool dropout_keep(uint32_t idx, uint32_t seed, float p) {
+  return (float)(drop_hash(idx ^ seed) >> 8) * (1.0f / 16777216.0f) >= p;
+}
+
 inline unsigned int grid_1d(int64_t n, int block, int64_t cap = 1 << 20) {
   int64_t g = (n + block - 1) / block;
   if (g < 1) g = 1;

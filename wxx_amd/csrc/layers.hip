@@ -150,12 +150,6 @@ __global__ __launch_bounds__(kBlock) void embed_segsum_kernel(
 }
 
 // ---- dropout -----------------------------------------------------------------
-__device__ __forceinline__ uint32_t drop_hash(uint32_t x) {
-  x = ((x >> 16) ^ x) * 0x45d9f3bu;
-  x = ((x >> 16) ^ x) * 0x45d9f3bu;
-  x = (x >> 16) ^ x;
-  return x;
-}
 
 // `seed_dev`, when set, holds the seed on the device (a step graph's replays
 // write a fresh one before each launch) and replaces `seed`.
@@ -167,8 +161,7 @@ __global__ __launch_bounds__(kBlock) void dropout_kernel(const float* __restrict
   int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   const int64_t step = (int64_t)gridDim.x * kBlock;
   for (; i < n; i += step) {
-    const float r = (float)(drop_hash((uint32_t)i ^ seed) >> 8) * (1.0f / 16777216.0f);
-    y[i] = r >= p ? x[i] * scale : 0.f;
+    y[i] = wxx::dropout_keep((uint32_t)i, seed, p) ? x[i] * scale : 0.f;
   }
 }
 

@@ -388,8 +388,27 @@ class MultiHeadAttention(Module):
             return autograd.scaled_masked_softmax(scores).forward(scores, scale, mask), None
         return ((scores * scale) + mask).softmax(dim=-1), None
 
+    def _fused_mode(self, x, mask, seq):
+        """None, or whether the fused kernels run causal: GPT-2's marked causal
+        mask or no mask, over head sizes the kernels are built for."""
+        if not functional.attention_ops.supported(x, self.n_heads):
+            return None
+        if mask is None:
+            return False
+        if getattr(mask, "_causal", False) and tuple(mask.shape) == (seq, seq):
+            return True
+        return None
+
     def forward(self, x, mask=None):
         b, seq, _ = x.shape
+        causal = self._fused_mode(x, mask, seq)
+        if causal is not None:
+            # the whole score / softmax / dropout / value path in two kernels
+            # (forward, backward) on the projections' own layout
+            q, k, v = self.q(x), self.k(x), self.v(x)
+            p = self.drop.p if context.MODE == 0 else None
+            ctx = autograd.FusedAttention(q, k, v).forward(q, k, v, self.n_heads, causal, p)
+            return self.out(ctx)
         q, k, v = (self._split(proj(x), b, seq) for proj in (self.q, self.k, self.v))
         probs, causal = self._probabilities(q, k, mask, seq)
         probs = self.drop(probs)
