@@ -110,6 +110,23 @@ inline T __shfl_xor(T v, int off, int width = 64) {
   return r;
 }
 
+// Wave vote: true on every lane when the predicate holds on any lane.
+inline int __any(int pred) {
+  auto* L = wxx_emu::g_launch;
+  const int t = wxx_emu::flat_tid(), w = t >> 6;
+  L->slot[t][0] = pred ? 1 : 0;
+  L->wave[w].wait();
+  int any = 0;
+  for (int i = 0; i < 64; ++i)
+    if (((w << 6) | i) < (int)(wxx_emu::g_block_dim.x * wxx_emu::g_block_dim.y * wxx_emu::g_block_dim.z))
+      any |= (int)L->slot[(w << 6) | i][0];
+  L->wave[w].wait();
+  return any;
+}
+
+// v_exp_f32
+inline float __builtin_amdgcn_exp2f(float x) { return std::exp2(x); }
+
 // Register-allocation hint of the device build; nothing to do on the CPU.
 #define WXX_OPAQUE(x) ((void)(x))
 

@@ -34,6 +34,15 @@ CFLAGS = [
 ]
 
 
+# Per-source additions.  The attention kernels keep every MFMA accumulator in
+# ordinary VGPRs (the VGPR form of v_mfma): their softmax reads and rescales
+# the accumulators between products, which the AGPR form turns into
+# accvgpr read / write copies around every tile.
+EXTRA_FLAGS = {
+    "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def sources():
     return sorted(
         os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip")
@@ -42,7 +51,7 @@ def sources():
 
 def _compile(src):
     obj = os.path.join(BUILD, os.path.basename(src)[:-4] + ".o")
-    cmd = [HIPCC, *CFLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *CFLAGS, *EXTRA_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(

@@ -57,6 +57,7 @@ struct AttnArgs {
   const float* lse_in;  // backward: read
   float* dvec;
   int64_t S, H, ld;  // ld = H * d: row stride of every (B, S, H, d) operand
+  int64_t BH;        // batch * heads
   float scale, p_drop, drop_scale;
   uint32_t seed;
   const uint32_t* seed_dev;
@@ -114,9 +115,14 @@ __device__ __forceinline__ void accum_tile(floatx16 (&acc)[HD / 32], const float
 template <int HD>
 __device__ __forceinline__ void load_row(float4 (&reg)[HD / 8], const float* base, int64_t row,
                                          int64_t S, int64_t ld, int h) {
+  // rows past the end read the last row (in bounds, no branch) and become 0
+  const float* src = base + (row < S ? row : S - 1) * ld + 4 * h;
+  const float keep = row < S ? 1.f : 0.f;
 #pragma unroll
-  for (int g = 0; g < HD / 8; ++g)
-    reg[g] = row < S ? ld4(base + row * ld + 8 * g + 4 * h) : make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int g = 0; g < HD / 8; ++g) {
+    const float4 v = ld4(src + 8 * g);
+    reg[g] = make_float4(v.x * keep, v.y * keep, v.z * keep, v.w * keep);
+  }
 }
 
 // Store a (d x 32) accumulator transposed back to rows: lane (j, h) writes
@@ -143,16 +149,16 @@ struct Stage {
   static constexpr int kPasses = HD / 16;
   float4 a[kPasses], b[kPasses];
 
+  // Rows past the end load the last row (in bounds, no branch); the kernels
+  // mask every product that involves them.
   __device__ __forceinline__ void load(const float* pa, const float* pb, int64_t r0, int64_t S,
                                        int64_t ld, int tid) {
     const int64_t row = r0 + (tid & 63);
-    const int d0 = 4 * (tid >> 6);
+    const int64_t off = (row < S ? row : S - 1) * ld + 4 * (tid >> 6);
 #pragma unroll
     for (int p = 0; p < kPasses; ++p) {
-      const int d = 16 * p + d0;
-      const bool in = row < S;
-      a[p] = in ? ld4(pa + row * ld + d) : make_float4(0.f, 0.f, 0.f, 0.f);
-      if (pb) b[p] = in ? ld4(pb + row * ld + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+      a[p] = ld4(pa + off + 16 * p);
+      b[p] = ld4(pb + off + 16 * p);
     }
   }
 };
@@ -183,6 +189,50 @@ __device__ __forceinline__ uint32_t seed_of(const AttnArgs& a) {
   return a.seed_dev ? *a.seed_dev : a.seed;
 }
 
+// Workgroup -> (row block, batch-head).  The grid is one-dimensional and
+// ordered by work: in causal mode the row blocks that see the most of the
+// other side (the last query blocks, the first key blocks) come first, all
+// batch-heads of one block level next to each other.  Workgroups are dealt
+// to the 8 XCDs round robin, so every XCD gets an equal share of every level
+// (with a 2-D grid of 8 row blocks, one XCD would get every heaviest block).
+struct RowBlock {
+  int block;
+  int64_t bh;
+};
+__device__ __forceinline__ RowBlock row_block(const AttnArgs& a, int nblocks, bool queries) {
+  const int64_t i = blockIdx.x;
+  const int level = (int)(i / a.BH);
+  const int64_t bh = i - (int64_t)level * a.BH;
+  const int block = a.causal && queries ? nblocks - 1 - level : level;
+  return RowBlock{block, bh};
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// 2^x on the exponent unit (v_exp_f32): the softmax weights are formed as
+// 2^(s * scale * log2(e) - m), one fused multiply-add and one exp per score.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Offsets i (0..31) of a 32-row tile at `t0` that a row at `row` may see:
+// i in [lo, hi].  Keys (or queries) past the end are never visible; in causal
+// mode a query sees keys at or before it.
+struct Window {
+  int lo, hi;
+};
+__device__ __forceinline__ Window keys_visible(int64_t t0, int64_t row, int64_t S, int causal) {
+  int64_t hi = S - 1 - t0;
+  if (causal && row - t0 < hi) hi = row - t0;
+  return Window{0, (int)(hi < -1 ? -1 : hi > 31 ? 31 : hi)};
+}
+__device__ __forceinline__ Window queries_visible(int64_t t0, int64_t key, int64_t S, int causal) {
+  const int64_t hi = S - 1 - t0;
+  int64_t lo = causal ? key - t0 : 0;
+  if (key >= S) lo = 32;
+  return Window{(int)(lo < 0 ? 0 : lo > 32 ? 32 : lo), (int)(hi > 31 ? 31 : hi)};
+}
+__device__ __forceinline__ bool inside(Window w, int i) { return i >= w.lo && i <= w.hi; }
+
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
@@ -194,8 +244,9 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, j = lane & 31, h = lane >> 5;
   const int64_t S = a.S, ld = a.ld;
   const int nqb = (int)((S + kGroupRows - 1) / kGroupRows);
-  const int qb = a.causal ? nqb - 1 - (int)blockIdx.x : (int)blockIdx.x;
-  const int64_t bh = blockIdx.y, bb = bh / a.H;
+  const RowBlock rb = row_block(a, nqb, true);
+  const int qb = rb.block;
+  const int64_t bh = rb.bh, bb = bh / a.H;
   const int64_t base = bb * S * ld + (bh - bb * a.H) * HD;
   const int64_t q0 = (int64_t)qb * kGroupRows + w * kWaveRows, qj = q0 + j;
   const uint32_t seed = DROP ? seed_of(a) : 0u;
@@ -205,7 +256,13 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnArgs a) {
   floatx16 acc[HD / 32];
 #pragma unroll
   for (int blk = 0; blk < HD / 32; ++blk) acc[blk] = floatx16{};
+  // m: the reference point of the weights, in units of log2 (scores times
+  // scale * log2(e)); it is raised only when a score exceeds it by more than
+  // 8 (a factor 256), so the accumulators are rescaled rarely.  The result,
+  // acc / l with both taken against the same m, is the softmax either way.
+  const float c2 = a.scale * kLog2e;
   float m = -INFINITY, l = 0.f;
+  const uint32_t drop_row = DROP ? (uint32_t)((bh * S + qj) * S) : 0u;
 
   const int64_t q_stop = (int64_t)(qb + 1) * kGroupRows;
   const int64_t k_end = a.causal && q_stop < S ? q_stop : S;
@@ -223,32 +280,35 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnArgs a) {
       const int64_t kt = (int64_t)kb * kBlock + 32 * t;
       if (kt >= k_end || (a.causal && kt > q0 + kWaveRows - 1)) break;  // wave-uniform
       const floatx16 s = dot_tile<HD, KP>(k_lds, 32 * t, qreg, j, h);
-      float x[16];
-      float tmax = -INFINITY;
+      // a tile wholly visible to every row of the wave needs no mask
+      const bool full = kt + 31 < S && (!a.causal || kt + 31 <= q0);
+      const Window win = keys_visible(kt, qj, S, a.causal);
+      float smax = -INFINITY;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t key = kt + tile_row(r, h);
-        const bool ok = key < S && (!a.causal || key <= qj);
-        x[r] = ok ? s[r] * a.scale : -INFINITY;
-        tmax = fmaxf(tmax, x[r]);
+      for (int r = 0; r < 16; ++r)
+        smax = fmaxf(smax, full || inside(win, tile_row(r, h)) ? s[r] : -INFINITY);
+      smax = fmaxf(smax, __shfl_xor(smax, 32, 64));
+      const float tmax = smax * c2;  // finite: every row sees key 0 of its first tile
+      const bool grow = tmax > m + 8.f;
+      if (__any(grow)) {
+        const float mn = grow ? tmax : m;
+        const float alpha = exp2_fast(m - mn);
+        l *= alpha;
+#pragma unroll
+        for (int blk = 0; blk < HD / 32; ++blk) acc[blk] *= alpha;
+        m = mn;
       }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-      const float mn = fmaxf(m, tmax);  // finite: key kt (or key 0) is visible
-      const float alpha = expf(m - mn);
-      m = mn;
-      l *= alpha;
-#pragma unroll
-      for (int blk = 0; blk < HD / 32; ++blk) acc[blk] *= alpha;
       float p[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        p[r] = expf(x[r] - mn);
-        l += p[r];
-        if (DROP) {
-          const int64_t key = kt + tile_row(r, h);
-          const uint32_t idx = (uint32_t)((bh * S + qj) * S + key);
-          p[r] = wxx::dropout_keep(idx, seed, a.p_drop) ? p[r] * a.drop_scale : 0.f;
-        }
+        const float e = exp2_fast(fmaf(s[r], c2, -m));
+        const float pr = full || inside(win, tile_row(r, h)) ? e : 0.f;
+        l += pr;
+        p[r] = pr;
+        if (DROP)
+          p[r] = wxx::dropout_keep(drop_row + (uint32_t)(kt + tile_row(r, h)), seed, a.p_drop)
+                     ? pr * a.drop_scale
+                     : 0.f;
       }
       accum_tile<HD, TP>(acc, vt_lds, 32 * t, p, j, h);
     }
@@ -256,7 +316,7 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnArgs a) {
   const float lt = l + __shfl_xor(l, 32, 64);
   if (qj < S) {
     store_row<HD>(a.out + base, qj, ld, acc, 1.f / lt, h);
-    if (h == 0) a.lse[bh * S + qj] = m + logf(lt);
+    if (h == 0) a.lse[bh * S + qj] = (m + log2f(lt)) * kLn2;
   }
 }
 
@@ -272,8 +332,9 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, j = lane & 31, h = lane >> 5;
   const int64_t S = a.S, ld = a.ld;
   const int nqb = (int)((S + kGroupRows - 1) / kGroupRows);
-  const int qb = a.causal ? nqb - 1 - (int)blockIdx.x : (int)blockIdx.x;
-  const int64_t bh = blockIdx.y, bb = bh / a.H;
+  const RowBlock rb = row_block(a, nqb, true);
+  const int qb = rb.block;
+  const int64_t bh = rb.bh, bb = bh / a.H;
   const int64_t base = bb * S * ld + (bh - bb * a.H) * HD;
   const int64_t q0 = (int64_t)qb * kGroupRows + w * kWaveRows, qj = q0 + j;
   const uint32_t seed = DROP ? seed_of(a) : 0u;
@@ -293,7 +354,10 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(AttnArgs a) {
   const float dq_row = dpart + __shfl_xor(dpart, 32, 64);
   const bool valid = qj < S;
   if (valid && h == 0) a.dvec[bh * S + qj] = dq_row;
-  const float lse = valid ? a.lse_in[bh * S + qj] : 0.f;
+  // the row's weights are 2^(s * c2 - lse * log2(e))
+  const float c2 = a.scale * kLog2e;
+  const float lse2 = valid ? a.lse_in[bh * S + qj] * kLog2e : 0.f;
+  const uint32_t drop_row = DROP ? (uint32_t)((bh * S + qj) * S) : 0u;
   floatx16 acc[HD / 32];
 #pragma unroll
   for (int blk = 0; blk < HD / 32; ++blk) acc[blk] = floatx16{};
@@ -316,17 +380,18 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(AttnArgs a) {
       if (kt >= k_end || (a.causal && kt > q0 + kWaveRows - 1)) break;
       const floatx16 s = dot_tile<HD, KP>(k_lds, 32 * t, qreg, j, h);
       const floatx16 dp = dot_tile<HD, KP>(v_lds, 32 * t, doreg, j, h);
+      const bool full = kt + 31 < S && (!a.causal || kt + 31 <= q0) && q0 + 31 < S;
+      const Window win = keys_visible(kt, qj, S, a.causal);
       float ds[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t key = kt + tile_row(r, h);
-        const bool ok = valid && key < S && (!a.causal || key <= qj);
-        const float p = ok ? expf(s[r] * a.scale - lse) : 0.f;
+        const float e = exp2_fast(fmaf(s[r], c2, -lse2));
+        const float p = full || (valid && inside(win, tile_row(r, h))) ? e : 0.f;
         float dpr = dp[r];
-        if (DROP) {
-          const uint32_t idx = (uint32_t)((bh * S + qj) * S + key);
-          dpr = wxx::dropout_keep(idx, seed, a.p_drop) ? dpr * a.drop_scale : 0.f;
-        }
+        if (DROP)
+          dpr = wxx::dropout_keep(drop_row + (uint32_t)(kt + tile_row(r, h)), seed, a.p_drop)
+                    ? dpr * a.drop_scale
+                    : 0.f;
         ds[r] = p * (dpr - dq_row);
       }
       accum_tile<HD, TP>(acc, kt_lds, 32 * t, ds, j, h);
@@ -338,8 +403,11 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(AttnArgs a) {
 // ---------------------------------------------------------------------------
 // backward: dK, dV
 // ---------------------------------------------------------------------------
+// Two waves per SIMD where the registers allow it without spilling (the
+// dropout variant at d = 64 would spill, d = 128 does not fit).
 template <int HD, bool DROP>
-__global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(
+    HD == 32 || (HD == 64 && !DROP) ? 2 : 1))) void attn_bwd_dkdv_kernel(AttnArgs a) {
   constexpr int KP = HD + 4, TP = kBlock + 4;
   __shared__ __align__(16) float q_lds[kBlock * KP];
   __shared__ __align__(16) float qt_lds[HD * TP];
@@ -348,10 +416,11 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(AttnArgs a) {
   __shared__ float lse_lds[kBlock], d_lds[kBlock];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, j = lane & 31, h = lane >> 5;
   const int64_t S = a.S, ld = a.ld;
-  const int64_t bh = blockIdx.y, bb = bh / a.H;
+  const RowBlock rb = row_block(a, (int)((S + kGroupRows - 1) / kGroupRows), false);
+  const int64_t bh = rb.bh, bb = bh / a.H;
   const int64_t base = bb * S * ld + (bh - bb * a.H) * HD;
   // key blocks in order: in causal mode the first ones see the most queries
-  const int64_t kg0 = (int64_t)blockIdx.x * kGroupRows;
+  const int64_t kg0 = (int64_t)rb.block * kGroupRows;
   const int64_t k0 = kg0 + w * kWaveRows, kj = k0 + j;
   const uint32_t seed = DROP ? seed_of(a) : 0u;
 
@@ -362,6 +431,7 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(AttnArgs a) {
 #pragma unroll
   for (int blk = 0; blk < HD / 32; ++blk) dk[blk] = dv[blk] = floatx16{};
 
+  const float c2 = a.scale * kLog2e;
   const int64_t q_begin = a.causal ? kg0 : 0;  // kg0 is a multiple of kBlock
   const int nqb = (int)((S - q_begin + kBlock - 1) / kBlock);
   Stage<HD> st;
@@ -370,7 +440,7 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(AttnArgs a) {
     st.load(a.q + base, a.dout + base, r0, S, ld, tid);
     if (tid < kBlock) {
       const int64_t row = r0 + tid;
-      lse_st = row < S ? a.lse_in[bh * S + row] : 0.f;
+      lse_st = row < S ? a.lse_in[bh * S + row] * kLog2e : 0.f;
       d_st = row < S ? a.dvec[bh * S + row] : 0.f;
     }
   };
@@ -395,16 +465,18 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(AttnArgs a) {
       if (a.causal && qt + kWaveRows - 1 < k0) continue;              // wholly above
       const floatx16 s = dot_tile<HD, KP>(q_lds, 32 * t, kreg, j, h);
       const floatx16 dp = dot_tile<HD, KP>(do_lds, 32 * t, vreg, j, h);
+      // every (query, key) pair of the tile visible: no mask
+      const bool full = qt + 31 < S && k0 + 31 < S && (!a.causal || qt >= k0 + 31);
+      const Window win = queries_visible(qt, kj, S, a.causal);
       float pd[16], ds[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int i = 32 * t + tile_row(r, h);
-        const int64_t qrow = r0 + i;
-        const bool ok = qrow < S && kj < S && (!a.causal || kj <= qrow);
-        const float p = ok ? expf(s[r] * a.scale - lse_lds[i]) : 0.f;
+        const float e = exp2_fast(fmaf(s[r], c2, -lse_lds[i]));
+        const float p = full || inside(win, tile_row(r, h)) ? e : 0.f;
         float dpr = dp[r], pk = p;
         if (DROP) {
-          const uint32_t idx = (uint32_t)((bh * S + qrow) * S + kj);
+          const uint32_t idx = (uint32_t)((bh * S + r0 + i) * S + kj);
           const bool keep = wxx::dropout_keep(idx, seed, a.p_drop);
           pk = keep ? p * a.drop_scale : 0.f;
           dpr = keep ? dpr * a.drop_scale : 0.f;
@@ -424,7 +496,7 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(AttnArgs a) {
 
 template <int HD, bool DROP>
 int launch_fwd(const AttnArgs& a, int64_t batch_heads) {
-  const dim3 grid((unsigned)((a.S + kGroupRows - 1) / kGroupRows), (unsigned)batch_heads);
+  const dim3 grid((unsigned)((a.S + kGroupRows - 1) / kGroupRows * batch_heads));
   hipLaunchKernelGGL((attn_fwd_kernel<HD, DROP>), grid, dim3(kThreads), 0, wxx::stream(), a);
   WXX_LAUNCHED();
   return WXX_OK;
@@ -432,7 +504,7 @@ int launch_fwd(const AttnArgs& a, int64_t batch_heads) {
 
 template <int HD, bool DROP>
 int launch_bwd(const AttnArgs& a, int64_t batch_heads) {
-  const dim3 grid((unsigned)((a.S + kGroupRows - 1) / kGroupRows), (unsigned)batch_heads);
+  const dim3 grid((unsigned)((a.S + kGroupRows - 1) / kGroupRows * batch_heads));
   hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, DROP>), grid, dim3(kThreads), 0, wxx::stream(), a);
   hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, DROP>), grid, dim3(kThreads), 0, wxx::stream(), a);
   WXX_LAUNCHED();
@@ -458,7 +530,8 @@ int dispatch(const AttnArgs& a, int64_t batch_heads, int64_t hd, bool drop) {
 int check_common(int64_t batch, int64_t seq, int64_t heads, int64_t hd, float p_drop,
                  std::initializer_list<const void*> ptrs) {
   WXX_REQUIRE(batch >= 0 && seq >= 0 && heads > 0, "bad attention shape");
-  WXX_REQUIRE(batch * heads < 65536, "at most 65535 batch x heads");
+  WXX_REQUIRE((seq + 127) / 128 * batch * heads < (int64_t(1) << 31),
+              "too many attention row blocks");
   WXX_REQUIRE(p_drop >= 0.f && p_drop < 1.f, "dropout probability %g outside [0, 1)", p_drop);
   for (const void* p : ptrs) {
     WXX_REQUIRE(p, "null pointer");
@@ -496,6 +569,7 @@ WXX_API int wxx_attention_fwd(const float* q, const float* k, const float* v, fl
   a.seed = seed;
   a.seed_dev = seed_dev;
   a.causal = causal ? 1 : 0;
+  a.BH = batch * heads;
   return dispatch<false>(a, batch * heads, head_dim, p_drop > 0.f);
 }
 
@@ -532,6 +606,7 @@ WXX_API int wxx_attention_bwd(const float* q, const float* k, const float* v, co
   a.seed = seed;
   a.seed_dev = seed_dev;
   a.causal = causal ? 1 : 0;
+  a.BH = batch * heads;
   rc = dispatch<true>(a, batch * heads, head_dim, p_drop > 0.f);
   wxx::scratch_free(dvec);
   return rc;
