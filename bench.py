@@ -70,6 +70,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--only", default=None, help="run only this component (profiling)")
     p.add_argument("--no-train", action="store_true", help="skip the train-step extras")
+    p.add_argument("--graph-only", action="store_true",
+                   help="with --only TRAIN_CONFIG: time only the step-graph replays")
     return p.parse_args()
 
 
@@ -284,12 +286,13 @@ def _train_setup(wxx, c, r):
     return m, loss, units, unit, desc
 
 
-def train_step(lib, name, steps, warmup, graph_steps=None):
+def train_step(lib, name, steps, warmup, graph_steps=None, eager=True):
     """Full train step: forward, CCELoss, backward, clip_grad_norm_(1.0), AdamW,
     WarmupCosineLR (README.md:50-51 schedule), zero_grad.  Timed with the host
     clock around ``steps`` steps between device synchronisations, first run
     eagerly (every op dispatched from Python), then recorded once as a step
-    graph and replayed ``graph_steps`` times (the same steps continue)."""
+    graph and replayed ``graph_steps`` times (the same steps continue).  With
+    ``eager`` False only the warm-up runs eagerly (profiling the replays)."""
     import wxx_amd as wxx
 
     c = TRAIN_CONFIGS[name]
@@ -306,22 +309,28 @@ def train_step(lib, name, steps, warmup, graph_steps=None):
         opt.zero_grad()
         return loss
 
-    for _ in range(warmup):
-        step()
-    lib.call("wxx_sync")
-    t0 = time.perf_counter()
-    for _ in range(steps):
+    for _ in range(max(warmup, 1)):
         loss = step()
     lib.call("wxx_sync")
-    dt = (time.perf_counter() - t0) / steps
-    out = {f"{unit}_per_s": units / dt, "ms": dt * 1e3, "steps_timed": steps,
-           "loss": float(loss.numpy().reshape(-1)[0]), "model": desc}
-    if "flop" in c:
-        out["tflops"] = c["flop"] / dt / 1e12
-        out["frac_of_peak"] = out["tflops"] / PEAK_FP32_TFLOPS
+    out = {"model": desc}
+    if eager:
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            loss = step()
+        lib.call("wxx_sync")
+        dt = (time.perf_counter() - t0) / steps
+        out.update({f"{unit}_per_s": units / dt, "ms": dt * 1e3, "steps_timed": steps,
+                    "loss": float(loss.numpy().reshape(-1)[0])})
+        if "flop" in c:
+            out["tflops"] = c["flop"] / dt / 1e12
+            out["frac_of_peak"] = out["tflops"] / PEAK_FP32_TFLOPS
     graph_steps = steps if graph_steps is None else graph_steps
     if graph_steps:
-        g = wxx.StepGraph(step).capture()
+        try:
+            g = wxx.StepGraph(step).capture()
+        except Exception as e:  # reported, not fatal: the eager figure stands
+            out["graph"] = {"error": f"{type(e).__name__}: {e}"}
+            return out
         g.replay()  # first launch of a new graph uploads its code objects
         lib.call("wxx_sync")
         t0 = time.perf_counter()
@@ -357,7 +366,8 @@ def main():
     names = STEP + EXTRA
     if args.only in TRAIN_CONFIGS:
         print(json.dumps({"only": args.only,
-                          "component": train_step(lib, args.only, args.steps, args.warmup)}))
+                          "component": train_step(lib, args.only, args.steps, args.warmup,
+                                                  eager=not args.graph_only)}))
         return
     if args.only:
         names = [args.only]
@@ -463,7 +473,11 @@ def main():
             "config": c5["model"] + "; forward, CCELoss, backward, clip_grad_norm_(1.0), "
                       "AdamW, WarmupCosineLR",
             "model_flop_per_step": TRAIN_CONFIGS["gpt2_train_config5"]["flop"],
-            "timing": "host clock around 5 steps between device synchronisations",
+            "graph_tokens_per_s": c5.get("graph", {}).get("tokens_per_s"),
+            "graph_ms_per_step": c5.get("graph", {}).get("ms"),
+            "graph_frac_of_fp32_peak": c5.get("graph", {}).get("frac_of_peak"),
+            "timing": "host clock around 5 steps between device synchronisations; graph_*: "
+                      "the same steps recorded once as a step graph and replayed",
             "profile": "profiles/gpt2_config5_train_step.md"}
     if not args.no_cpu:
         base = cpu_gemm_baseline(args.cpu_seconds)
