@@ -31,6 +31,7 @@
 #define __host__
 #define __forceinline__ inline
 #define __launch_bounds__(...)
+#define WXX_WAVES_PER_EU(n)
 #define __shared__ static
 #define __align__(n) __attribute__((aligned(n)))
 #define HIP_SYMBOL(x) ((const void*)&(x))

@@ -406,8 +406,8 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(AttnArgs a) {
 // Two waves per SIMD where the registers allow it without spilling (the
 // dropout variant at d = 64 would spill, d = 128 does not fit).
 template <int HD, bool DROP>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(
-    HD == 32 || (HD == 64 && !DROP) ? 2 : 1))) void attn_bwd_dkdv_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kThreads) WXX_WAVES_PER_EU(HD == 32 || (HD == 64 && !DROP) ? 2 : 1)
+void attn_bwd_dkdv_kernel(AttnArgs a) {
   constexpr int KP = HD + 4, TP = kBlock + 4;
   __shared__ __align__(16) float q_lds[kBlock * KP];
   __shared__ __align__(16) float qt_lds[HD * TP];

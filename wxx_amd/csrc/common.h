@@ -31,6 +31,12 @@
 #define WXX_S_BARRIER() asm volatile("s_barrier" ::: "memory")
 #endif
 
+// Occupancy hint: at least n waves per SIMD (the register allocator keeps
+// within the matching VGPR budget).
+#ifndef WXX_WAVES_PER_EU
+#define WXX_WAVES_PER_EU(n) __attribute__((amdgpu_waves_per_eu(n)))
+#endif
+
 // One global_load_lds_dword: every lane's 4 bytes at `src` (any address)
 // land at the wave-uniform LDS address `lds_dst` + 4 * lane.  Written as
 // inline asm so that the compiler does not track it as an LDS store: a

@@ -17,65 +17,56 @@
 //   forward: i = co, j = (b, oh, ow), k = (ci, kh, kw); P = W, Q = im2col(X)
 //   dX:      i = ci, j = (b, ih, iw), k = (co, kh, kw); P = W (ci-strided), Q = gather(dY)
 //   dW:      i = co, j = (ci, kh, kw), k = (b, oh, ow); P = dY, Q = im2col(X)^T
-// Q is gathered on the fly into k-major LDS tiles (never materialised in
-// HBM).  Each lane owns one column j for the whole K loop, so its (b, oh, ow)
-// or (ci, kh, kw) decomposition is computed once; the k decomposition is
-// wave-uniform and runs on the scalar unit.  Tiles are BI x BJ with 4 waves
-// of v_mfma_f32_32x32x2f32, gathered straight into a 3-stage LDS ring.
-// When the tile grid is too small to fill 256 CUs (ResNet's deep layers, and
-// every dW whose K = B Ho Wo is long) the K range is split: each split writes
-// a partial tile and a second pass adds the partials in split order, so the
-// result does not depend on scheduling (no float atomics).
+// Neither operand is materialised in HBM: both are gathered on the fly into
+// LDS tiles, each in the layout (k-major or row-major, conv_addr.h) that
+// reads its tensor with fewer cache lines for the launch's shape.  Tiles are
+// 64 x 64 with 4 waves of v_mfma_f32_32x32x2f32; every load is a fixed
+// per-slot offset plus a wave-uniform offset per chunk, four chunks of loads
+// are in flight in registers and two LDS stages alternate.  When the tile
+// grid is too small for 256 CUs (ResNet's deep layers, and every dW whose
+// K = B Ho Wo is long) the K range is split where a cost model says it pays:
+// each split writes a partial tile and a second pass adds the partials in a
+// fixed order, so the result does not depend on scheduling (no float
+// atomics).
 #include "common.h"
+
+#define WXX_HD __host__ __device__ __forceinline__
+#include "conv_addr.h"
+
+#include <map>
+#include <mutex>
+#include <tuple>
+
+// The source of every zero operand element (padding, stride gaps, ragged
+// tiles).  The kernels receive its address as an argument, so nothing in
+// device code names it: external linkage and `used` keep it in the code
+// object for hipGetSymbolAddress.  Nothing writes it.
+__device__ __attribute__((used)) float wxx_conv_zero_word[4];
 
 namespace {
 
+using namespace wxx_conv;
+
 typedef float floatx16 __attribute__((ext_vector_type(16)));
-
-enum { kFwd = 0, kDx = 1, kDw = 2 };
-
-struct ConvArgs {
-  const float* P;
-  const float* Q;
-  const float* bias;
-  float* out;  // final tensor (splits == 1) or partials [splits][I][J]
-  int B, Cin, H, W, Cout, KH, KW, Ho, Wo, sh, sw, ph, pw, dh, dw;
-  int I, J, K;
-  int kps;  // K elements per split (multiple of the K chunk)
-  int splits;
-  int tiles_i, tiles_j;
-};
 
 // ---------------------------------------------------------------------------
 // The implicit-GEMM tile kernel.
 //
-// Out[i][j] = sum_k P[i][k] Q[k][j] over one K range (a split), for a BI x BJ
-// output tile with 4 waves of v_mfma_f32_32x32x2f32 (each wave a BI/2 x BJ/2
-// quarter).  Both operand tiles are gathered straight into LDS with
-// global_load_lds_dword: one wave instruction takes one 4-byte word per lane
-// from any 64 addresses and writes them as 64 consecutive LDS words, so a
-// tile row k (BI or BJ words, k-major layout) is BI/64 or BJ/64
-// instructions, no VGPR holds the data on its way and no ds_write runs.
-// Elements outside the tensor (padding, ragged tile edges, the end of the K
-// range) are taken from a word of zeros.  A ring of three LDS stages keeps
-// two chunks of loads in flight while the matrix cores work on the third: at
-// chunk c a wave waits until only its loads of chunk c + 1 are outstanding
-// (s_waitcnt vmcnt, loads complete in order), one barrier makes every wave's
-// part of chunk c visible and frees the stage of chunk c - 1, which then
-// receives chunk c + 2.
+// Out[i][j] = sum_k P[i][k] Q[k][j] over one K range (a split), for a 64 x 64
+// output tile with 4 waves of v_mfma_f32_32x32x2f32 (each wave a 32 x 32
+// quarter).  Each operand tile reaches LDS in the layout chosen on the host
+// (KX or XK, conv_addr.h) through ordinary global loads into registers and
+// ds_write: one-float global_load_lds DMA instructions, which a gather needs,
+// retire too slowly to feed the matrix cores.  Elements outside the tensor
+// (padding, stride gaps, ragged tile edges, the end of the K range) are
+// loaded from a word of zeros.
 //
-// The k index of a row decomposes as k = (t0 R1 + t1) R2 + t2 with
-// (t0, t1, t2) = (ci, kh, kw) for the forward, (co, kh, kw) for dX and
-// (b, oh, ow) for dW.  A wave loads 8 consecutive rows per chunk, so it
-// carries the decomposition of its first row on the scalar unit and steps it
-// (by 1 per row, by BK per chunk) with carries instead of dividing.
-constexpr int BK = 32;
-constexpr int kStages = 3;
-constexpr int kRowsPerWave = BK / 4;
+// BK = 36 for 3x3 forward / dX chunks (four whole input channels of taps, so
+// every load keeps fixed taps), 32 otherwise.
+constexpr int kLQ = kTile + 2;  // KX row stride: rows k and k + 16 land 32 banks apart
+constexpr int kDepth = 4;       // chunks of loads in flight per wave
 
-__device__ const float g_conv_zero[4] = {0.f, 0.f, 0.f, 0.f};
 
-// (t0, t1, t2) digits of k in radices (R1, R2) and the step arithmetic.
 struct KDigits {
   int t0, t1, t2;
 };
@@ -107,16 +98,32 @@ __device__ __forceinline__ void kd_add(KDigits& d, int n0, int n1, int n2, int R
   d.t0 += n0 + c;
 }
 
-template <int MODE, int BI, int BJ>
-__global__ __launch_bounds__(256) void conv_lds_kernel(ConvArgs a) {
-  constexpr int WI = BI / 2, WJ = BJ / 2;
-  constexpr int TM = WI / 32, TN = WJ / 32;
-  constexpr int LP = BI + 2, LQ = BJ + 2;  // rows k and k + 16 land 32 banks apart
-  constexpr int HP = BI / 64, HQ = BJ / 64;  // instructions per tile row
-  // separate objects per stage, so the compiler can tell the loads into one
-  // stage from the reads of another
-  __shared__ float P0[BK * LP], P1[BK * LP], P2[BK * LP];
-  __shared__ float Q0[BK * LQ], Q1[BK * LQ], Q2[BK * LQ];
+template <int BK, bool XK>
+struct OpWords {
+  static constexpr int kWords = XK ? Xk<BK>::kWords : BK * kLQ;
+  static constexpr int kPerWave = XK ? Xk<BK>::kPerWave : BK / 4;  // loads per wave per chunk
+};
+
+// SLOTS: every operand is a set of slots (a fixed offset per load plus a
+// wave-uniform offset per chunk; case 1 or 2 of conv_addr.h, and always the
+// forward's P).  Otherwise (case 0: a kernel whose tap count does not divide
+// the chunk) the non-slot operands are KX rows whose k digits are stepped on
+// the scalar unit per row.
+template <int MODE, int BK, bool PXK, bool QXK, bool SLOTS>
+__global__ __launch_bounds__(256, 2) void conv_lds_kernel(ConvArgs a) {
+  using OP = OpWords<BK, PXK>;
+  using OQ = OpWords<BK, QXK>;
+  constexpr int kRowsPerWave = BK / 4;
+  constexpr bool PS = SLOTS || MODE == kFwd;  // P as slots
+  constexpr bool QS = SLOTS;                  // Q as slots
+  static_assert(PS || !PXK, "an XK operand is always slots");
+  static_assert(QS || !QXK, "an XK operand is always slots");
+  // separate objects per stage, so the compiler can tell the writes into one
+  // stage from the reads of the other
+  __shared__ float P0[OP::kWords], P1[OP::kWords];
+  __shared__ float Q0[OQ::kWords], Q1[OQ::kWords];
+  __shared__ SlotX xtab[2][kTile];
+  __shared__ SlotC ctab[2][BK];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -125,256 +132,270 @@ __global__ __launch_bounds__(256) void conv_lds_kernel(ConvArgs a) {
 
   const int tile = blockIdx.x;
   const int ti = tile / a.tiles_j, tj = tile - (tile / a.tiles_j) * a.tiles_j;
-  const int i0 = ti * BI, j0 = tj * BJ;
+  const int i0 = ti * kTile, j0 = tj * kTile;
   const int z = blockIdx.y;
   const int kbeg = z * a.kps;
   const int kend = min(a.K, kbeg + a.kps);
   const int nk = (kend - kbeg + BK - 1) / BK;
 
-  const int HW = a.H * a.W, HoWo = a.Ho * a.Wo, KK = a.KH * a.KW;
-  // radices of k's digits
-  const int R1 = MODE == kDw ? a.Ho : a.KH;
-  const int R2 = MODE == kDw ? a.Wo : a.KW;
+  const int R1 = conv_r1(MODE, a), R2 = conv_r2(MODE, a);
   const int R12 = R1 * R2;
-  const float* __restrict__ zero = g_conv_zero;
+  const float* __restrict__ zero = a.zero;
 
-  // ---- per-lane column data (constant over K) ------------------------------
-  // P: lane's row i of each instruction half; Q: lane's column j.
-  int p_i[HP];
-  int64_t p_off[HP];
-#pragma unroll
-  for (int h = 0; h < HP; ++h) {
-    p_i[h] = i0 + 64 * h + lane;
-    const int64_t stride = MODE == kFwd ? a.K : (MODE == kDx ? KK : HoWo);
-    p_off[h] = (int64_t)p_i[h] * stride;
+  // ---- slots: row entries of the tile and column entries of a chunk, then
+  //      each of the wave's loads from one of each -----------------------------
+  if (wave == 0) {
+    xtab[0][lane] = slot_x<MODE, true>(a, i0 + lane);
+    xtab[1][lane] = slot_x<MODE, false>(a, j0 + lane);
+  } else if (wave == 1 && lane < BK) {
+    ctab[0][lane] = slot_c<MODE, true>(a, lane, BK);
+    ctab[1][lane] = slot_c<MODE, false>(a, lane, BK);
   }
-  // Q column: forward (b, oh, ow) -> base offset and input corner;
-  //           dX (b, y, x) of dX;  dW (ci, kh, kw).
-  int q_ok[HQ], q_b[HQ], q_y[HQ], q_x[HQ];
-  int64_t q_off[HQ];
-#pragma unroll
-  for (int h = 0; h < HQ; ++h) {
-    const int j = j0 + 64 * h + lane;
-    q_ok[h] = j < a.J;
-    const int jj = q_ok[h] ? j : 0;
-    if (MODE == kDw) {
-      const int ci = jj / KK, kk = jj - (jj / KK) * KK;
-      const int kh = kk / a.KW, kw = kk - (kk / a.KW) * a.KW;
-      q_b[h] = 0;
-      q_y[h] = kh * a.dh;  // added to the row's oh sh - ph
-      q_x[h] = kw * a.dw;
-      q_off[h] = (int64_t)ci * HW;
+  __syncthreads();
+  XkSlot psl[PS ? OP::kPerWave : 1], qsl[QS ? OQ::kPerWave : 1];
+  auto make = [&](int op, bool xk, int n) __attribute__((always_inline)) {
+    int xl, c;
+    if (xk) {
+      const int w = 64 * (wave + 4 * n) + lane;
+      xl = w / (BK + 1);
+      c = w - xl * (BK + 1);
     } else {
-      const int S = MODE == kFwd ? HoWo : HW;
-      const int SW = MODE == kFwd ? a.Wo : a.W;
-      const int b = jj / S, r = jj - (jj / S) * S;
-      const int y = r / SW, x = r - (r / SW) * SW;
-      q_b[h] = b;
-      if (MODE == kFwd) {
-        q_y[h] = y * a.sh - a.ph;
-        q_x[h] = x * a.sw - a.pw;
-        q_off[h] = (int64_t)b * a.Cin * HW;
-      } else {
-        q_y[h] = y + a.ph;
-        q_x[h] = x + a.pw;
-        q_off[h] = (int64_t)b * a.Cout * HoWo;
-      }
+      xl = lane;
+      c = kRowsPerWave * wave + n;
     }
+    XkSlot sl;
+    sl.off = sl.iy = 0;
+    sl.c = kDeadSlot;
+    if (xl < kTile && c < BK)
+      sl = op == 0 ? slot_make<MODE, true>(a, xtab[0][xl], ctab[0][c], c)
+                   : slot_make<MODE, false>(a, xtab[1][xl], ctab[1][c], c);
+    return sl;
+  };
+  if constexpr (PS) {
+#pragma unroll
+    for (int n = 0; n < OP::kPerWave; ++n) psl[n] = make(0, PXK, n);
   }
+  if constexpr (QS) {
+#pragma unroll
+    for (int n = 0; n < OQ::kPerWave; ++n) qsl[n] = make(1, QXK, n);
+  }
+  XkUniform xu = xk_uniform(MODE, a, kbeg);
 
-  // ---- the wave's first row of the first chunk, as digits ------------------
+  // ---- case 0: KX rows with scalar digits -----------------------------------
+  const KxCol pcol = kx_col<MODE, true>(a, i0 + lane);
+  const KxCol qcol = kx_col<MODE, false>(a, j0 + lane);
+  const bool dx_strided = MODE == kDx && (a.sh != 1 || a.sw != 1);
   KDigits base;
-  {
+  int n0 = 0, n1 = 0, n2 = 0;
+  if constexpr (!PS || !QS) {
     const int k = kbeg + kRowsPerWave * wave;
-    base.t0 = k / R12;
+    base.t0 = fdiv(k, a.dR12);
     const int r = k - base.t0 * R12;
-    base.t1 = r / R2;
+    base.t1 = fdiv(r, a.dR2);
     base.t2 = r - base.t1 * R2;
+    // BK as digits, for the per-chunk advance
+    n0 = BK / R12;
+    n1 = (BK - n0 * R12) / R2;
+    n2 = BK - n0 * R12 - n1 * R2;
   }
-  // BK as digits, for the per-chunk advance
-  const int n0 = BK / R12, n1 = (BK - n0 * R12) / R2, n2 = BK - n0 * R12 - n1 * R2;
 
-  auto issue = [&](int c, float* ps, float* qs) __attribute__((always_inline)) {
-    KDigits d = base;
-    const int krow0 = kbeg + c * BK + kRowsPerWave * wave;
+  // Every source is the operand's base plus a wave-uniform chunk / row offset
+  // plus the load's fixed offset, or the zero word.  One chunk of loads is in
+  // flight in registers: the n-th load of a wave goes to its LDS word (see
+  // commit).
+  float pr[kDepth][OP::kPerWave], qr[kDepth][OQ::kPerWave];
+  auto issue = [&](int c, float* prs, float* qrs) __attribute__((always_inline)) {
+    const int kbase = kbeg + c * BK;
+    const int rem = kend - kbase;
+    const int lim = rem >= BK ? kDeadSlot : rem;  // only a split's last chunk is partial
+    if constexpr (PS) {
+      const float* pb = a.P + xk_uoff<MODE, true>(a, xu, kbase);
 #pragma unroll
-    for (int m = 0; m < kRowsPerWave; ++m) {
-      const int k = krow0 + m;
-      const bool kin = k < kend;
-      const int row = kRowsPerWave * wave + m;
-      // P row k
-#pragma unroll
-      for (int h = 0; h < HP; ++h) {
-        const float* src = zero;
-        if (kin && p_i[h] < a.I) {
-          int64_t off;
-          if (MODE == kFwd) off = k;
-          else if (MODE == kDx) off = (int64_t)d.t0 * a.Cin * KK + d.t1 * a.KW + d.t2;
-          else off = (int64_t)d.t0 * a.Cout * HoWo + d.t1 * a.Wo + d.t2;
-          src = a.P + p_off[h] + off;
-        }
-        WXX_LDS_DMA_DWORD(src, ps + row * LP + 64 * h);
-      }
-      // Q row k
-#pragma unroll
-      for (int h = 0; h < HQ; ++h) {
-        const float* src = zero;
-        if (kin && q_ok[h]) {
-          if (MODE == kFwd) {
-            const int iy = q_y[h] + d.t1 * a.dh, ix = q_x[h] + d.t2 * a.dw;
-            if ((unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W)
-              src = a.Q + q_off[h] + (int64_t)d.t0 * HW + iy * a.W + ix;
-          } else if (MODE == kDx) {
-            const int th = q_y[h] - d.t1 * a.dh, tw = q_x[h] - d.t2 * a.dw;
-            if (th >= 0 && tw >= 0) {
-              const int oh = th / a.sh, ow = tw / a.sw;
-              if (oh * a.sh == th && ow * a.sw == tw && oh < a.Ho && ow < a.Wo)
-                src = a.Q + q_off[h] + (int64_t)d.t0 * HoWo + oh * a.Wo + ow;
-            }
-          } else {
-            const int iy = d.t1 * a.sh - a.ph + q_y[h], ix = d.t2 * a.sw - a.pw + q_x[h];
-            if ((unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W)
-              src = a.Q + (int64_t)d.t0 * a.Cin * HW + q_off[h] + iy * a.W + ix;
-          }
-        }
-        WXX_LDS_DMA_DWORD(src, qs + row * LQ + 64 * h);
-      }
-      kd_step1(d, R1, R2);
+      for (int n = 0; n < OP::kPerWave; ++n)
+        prs[n] = *(xk_valid<MODE, true>(a, psl[n], xu, lim) ? pb + psl[n].off : zero);
     }
-    kd_add(base, n0, n1, n2, R1, R2);
+    if constexpr (QS) {
+      const float* qb = a.Q + xk_uoff<MODE, false>(a, xu, kbase);
+#pragma unroll
+      for (int n = 0; n < OQ::kPerWave; ++n)
+        qrs[n] = *(xk_valid<MODE, false>(a, qsl[n], xu, lim) ? qb + qsl[n].off : zero);
+    }
+    if constexpr (!PS || !QS) {
+      KDigits d = base;
+#pragma unroll
+      for (int m = 0; m < kRowsPerWave; ++m) {
+        const int k = kbase + kRowsPerWave * wave + m;
+        const bool kin = k < kend;
+        if constexpr (!PS) {
+          const float* rb = a.P + kx_uoff<MODE, true>(a, k, d.t0, d.t1, d.t2);
+          prs[m] = *(kin && pcol.ok ? rb + pcol.lo : zero);
+        }
+        if constexpr (!QS) {
+          const float* src = zero;
+          if (dx_strided) {
+            int off = 0;
+            if (kin && kx_src_strided(a, qcol, d.t0, d.t1, d.t2, off)) src = a.Q + off;
+          } else {
+            const float* rb = a.Q + kx_uoff<MODE, false>(a, k, d.t0, d.t1, d.t2);
+            if (kin && kx_valid<MODE, false>(a, qcol, d.t1, d.t2)) src = rb + qcol.lo;
+          }
+          qrs[m] = *src;
+        }
+        kd_step1(d, R1, R2);
+      }
+      kd_add(base, n0, n1, n2, R1, R2);
+    }
+    if constexpr (PS || QS) xk_advance(MODE, a, xu, BK);
   };
 
-  floatx16 acc[TM][TN];
+  floatx16 acc;
 #pragma unroll
-  for (int x = 0; x < TM; ++x)
-#pragma unroll
-    for (int y = 0; y < TN; ++y)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[x][y][r] = 0.f;
+  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
 
   const int half = lane >> 5;
   const int l32 = lane & 31;
-  const int pa = wi * WI + l32;
-  const int qa = wj * WJ + l32;
+  const int pa = wi * 32 + l32;
+  const int qa = wj * 32 + l32;
 
   auto compute = [&](const float* ps, const float* qs) __attribute__((always_inline)) {
 #pragma unroll
     for (int s = 0; s < BK / 2; ++s) {
       const int kk = s + half * (BK / 2);
-      float af[TM], bf[TN];
-#pragma unroll
-      for (int x = 0; x < TM; ++x) af[x] = ps[kk * LP + pa + 32 * x];
-#pragma unroll
-      for (int y = 0; y < TN; ++y) bf[y] = qs[kk * LQ + qa + 32 * y];
-#pragma unroll
-      for (int x = 0; x < TM; ++x)
-#pragma unroll
-        for (int y = 0; y < TN; ++y)
-          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[x], bf[y], acc[x][y], 0, 0, 0);
+      const float af = PXK ? ps[pa * (BK + 1) + kk] : ps[kk * kLQ + pa];
+      const float bf = QXK ? qs[qa * (BK + 1) + kk] : qs[kk * kLQ + qa];
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af, bf, acc, 0, 0, 0);
     }
   };
 
-  // s_waitcnt with vmcnt = n (expcnt and lgkmcnt left alone): on gfx9 the
-  // vmcnt field is bits 0-3 and 14-15
-  constexpr int kPerChunk = kRowsPerWave * (HP + HQ);  // loads per wave per chunk
-  static_assert(kPerChunk < 64, "vmcnt holds at most 63");
-  constexpr int kWaitOne = 0x0F70 | (kPerChunk & 15) | ((kPerChunk >> 4) << 14);
-
-  // Three stages: chunk c lives in stage c % 3.  The loop is unrolled by 3
-  // so that every stage is a named LDS object.
-  auto step = [&](int c, float* ps, float* qs, float* ps2, float* qs2)
+  // the registers of one issue() into a stage: the same LDS words the loads'
+  // slots (XK) or rows (KX) name
+  auto commit = [&](const float* prs, const float* qrs, float* ps, float* qs)
       __attribute__((always_inline)) {
-    if (c + 1 < nk)
-      __builtin_amdgcn_s_waitcnt(kWaitOne);
-    else
-      __builtin_amdgcn_s_waitcnt(0x0F70);
-    // a bare barrier: __syncthreads() is also a release fence, which would
-    // wait for every outstanding load (vmcnt(0)) and serialise the ring.
-    // Each wave's words of chunk c are in LDS by the wait above; its reads
-    // of chunk c - 1 have all returned (the MFMAs consumed them).
-    WXX_S_BARRIER();
-    if (c + 2 < nk) issue(c + 2, ps2, qs2);
-    compute(ps, qs);
+#pragma unroll
+    for (int n = 0; n < OP::kPerWave; ++n)
+      ps[(PXK ? 64 * (wave + 4 * n) : (kRowsPerWave * wave + n) * kLQ) + lane] = prs[n];
+#pragma unroll
+    for (int n = 0; n < OQ::kPerWave; ++n)
+      qs[(QXK ? 64 * (wave + 4 * n) : (kRowsPerWave * wave + n) * kLQ) + lane] = qrs[n];
   };
-  if (nk > 0) issue(0, P0, Q0);
-  if (nk > 1) issue(1, P1, Q1);
-  for (int c = 0; c < nk; c += 3) {
-    step(c, P0, Q0, P2, Q2);
-    if (c + 1 < nk) step(c + 1, P1, Q1, P0, Q0);
-    if (c + 2 < nk) step(c + 2, P2, Q2, P1, Q1);
+
+  // Two LDS stages (chunk c in stage c % 2) and kDepth chunks of loads in
+  // flight in registers (chunk c in register set c % kDepth).  Step c:
+  //   wait for this wave's LDS writes, barrier: stage c % 2 (written at step
+  //   c - 1) is complete and everyone has finished reading the other stage;
+  //   issue chunk c + kDepth into the register set chunk c has left;
+  //   multiply chunk c; write chunk c + 1 from its registers into the other
+  //   stage (the compiler's vmcnt wait covers only those loads).
+  // The barrier is bare (s_barrier after an lgkmcnt wait): __syncthreads()
+  // would also wait for every outstanding load and drain the pipeline.
+  constexpr int kLgkmOnly = 0xC07F;  // s_waitcnt lgkmcnt(0), vmcnt and expcnt at their maxima
+  auto step = [&](int c, int rs, int rs1, float* ps, float* qs, float* ps1, float* qs1)
+      __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(kLgkmOnly);
+    WXX_S_BARRIER();
+    if (c + kDepth < nk) issue(c + kDepth, pr[rs], qr[rs]);
+    compute(ps, qs);
+    if (c + 1 < nk) commit(pr[rs1], qr[rs1], ps1, qs1);
+  };
+#pragma unroll
+  for (int c = 0; c < kDepth; ++c)
+    if (c < nk) issue(c, pr[c], qr[c]);
+  if (nk > 0) commit(pr[0], qr[0], P0, Q0);
+  static_assert(kDepth == 4, "the step loop below is unrolled for 4 register sets");
+  for (int c = 0; c < nk; c += 4) {
+    step(c, 0, 1, P0, Q0, P1, Q1);
+    if (c + 1 < nk) step(c + 1, 1, 2, P1, Q1, P0, Q0);
+    if (c + 2 < nk) step(c + 2, 2, 3, P0, Q0, P1, Q1);
+    if (c + 3 < nk) step(c + 3, 3, 0, P1, Q1, P0, Q0);
   }
 
   // ---- epilogue: D[i][j] of a 32x32 tile is in lane j + 32 ((i/4)%2),
   //      register (i%4) + 4 (i/8) ------------------------------------------
+  const int j = j0 + wj * 32 + l32;
+  if (j >= a.J) return;
+  const int HoWo = a.Ho * a.Wo, HW = a.H * a.W;
+  int64_t obase = 0, istride = 0;
+  if (a.splits > 1) {
+    obase = (int64_t)z * a.I * a.J + j;
+    istride = a.J;
+  } else if (MODE == kDw) {
+    obase = j;
+    istride = a.J;
+  } else {
+    const int S = MODE == kFwd ? HoWo : HW;
+    const int C = MODE == kFwd ? a.Cout : a.Cin;
+    const int b = j / S, pos = j - b * S;
+    obase = (int64_t)b * C * S + pos;
+    istride = S;
+  }
 #pragma unroll
-  for (int y = 0; y < TN; ++y) {
-    const int j = j0 + wj * WJ + 32 * y + l32;
-    if (j >= a.J) continue;
-    int64_t obase = 0, istride = 0;
-    if (a.splits > 1) {
-      obase = (int64_t)z * a.I * a.J + j;
-      istride = a.J;
-    } else if (MODE == kDw) {
-      obase = j;
-      istride = a.J;
-    } else {
-      const int S = MODE == kFwd ? HoWo : HW;
-      const int C = MODE == kFwd ? a.Cout : a.Cin;
-      const int b = j / S, pos = j - b * S;
-      obase = (int64_t)b * C * S + pos;
-      istride = S;
-    }
-#pragma unroll
-    for (int x = 0; x < TM; ++x) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int i = i0 + wi * WI + 32 * x + 8 * (r >> 2) + 4 * half + (r & 3);
-        if (i < a.I) {
-          float v = acc[x][y][r];
-          if (MODE != kDw && a.splits == 1 && a.bias) v += a.bias[i];
-          a.out[obase + (int64_t)i * istride] = v;
-        }
-      }
+  for (int r = 0; r < 16; ++r) {
+    const int i = i0 + wi * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+    if (i < a.I) {
+      float v = acc[r];
+      if (MODE != kDw && a.splits == 1 && a.bias) v += a.bias[i];
+      a.out[obase + (int64_t)i * istride] = v;
     }
   }
 }
 
-// Adds the split partials in split order and writes the final layout.
+// Adds the split partials in a fixed order and writes the final layout.  A
+// workgroup takes 64 consecutive elements; wave w sums splits w, w + 4, ...
+// in order, and the four sums are added in wave order.
 template <int MODE>
 __global__ __launch_bounds__(256) void conv_splitk_reduce_kernel(ConvArgs a,
                                                                   const float* __restrict__ part,
                                                                   float* __restrict__ out) {
+  __shared__ float red[4][64];
   const int64_t n = (int64_t)a.I * a.J;
-  const int HoWo = a.Ho * a.Wo, HW = a.H * a.W;
-  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n;
-       e += (int64_t)gridDim.x * 256) {
-    const int i = (int)(e / a.J), j = (int)(e - (int64_t)i * a.J);
-    float v = 0.f;
-    for (int s = 0; s < a.splits; ++s) v += part[(int64_t)s * n + e];
-    if (MODE == kDw) {
-      out[e] = v;
-    } else {
-      const int S = MODE == kFwd ? HoWo : HW;
-      const int C = MODE == kFwd ? a.Cout : a.Cin;
-      const int b = j / S, pos = j - b * S;
-      if (a.bias) v += a.bias[i];
-      out[((int64_t)b * C + i) * S + pos] = v;
-    }
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t e = (int64_t)blockIdx.x * 64 + lane;
+  float v = 0.f;
+  if (e < n) {
+#pragma unroll 4
+    for (int s = w; s < a.splits; s += 4) v += part[(int64_t)s * n + e];
+  }
+  red[w][lane] = v;
+  __syncthreads();
+  if (w != 0 || e >= n) return;
+  v = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+  const int i = (int)(e / a.J), j = (int)(e - (int64_t)i * a.J);
+  if (MODE == kDw) {
+    out[e] = v;
+  } else {
+    const int S = MODE == kFwd ? a.Ho * a.Wo : a.H * a.W;
+    const int C = MODE == kFwd ? a.Cout : a.Cin;
+    const int b = j / S, pos = j - b * S;
+    if (a.bias) v += a.bias[i];
+    out[((int64_t)b * C + i) * S + pos] = v;
   }
 }
 
-template <int MODE, int BI, int BJ>
+template <int MODE, int BK, bool PXK, bool QXK, bool SLOTS>
 int launch(ConvArgs& a, float* final_out) {
-  a.tiles_i = (a.I + BI - 1) / BI;
-  a.tiles_j = (a.J + BJ - 1) / BJ;
+  a.tiles_i = (a.I + kTile - 1) / kTile;
+  a.tiles_j = (a.J + kTile - 1) / kTile;
   const int64_t tiles = (int64_t)a.tiles_i * a.tiles_j;
   const int64_t cus = wxx::num_cus() > 0 ? wxx::num_cus() : 256;
-  // Split K when the tile grid leaves CUs idle; keep >= 4 chunks per split.
+  // K splits from a cost model fitted to measured launches on MI355X: a
+  // launch costs ~5 us of fixed latency (dispatch, prologue, first loads,
+  // store drain), a chunk ~0.7 us for one workgroup per CU (more workgroups
+  // per CU share its matrix cores), and a split adds the reduce pass (~3 us
+  // plus the partials written and read back at ~3 TB/s).
   int splits = 1;
-  if (tiles < 2 * cus) {
-    const int64_t want = (2 * cus + tiles - 1) / tiles;
-    const int64_t maxs = std::max<int64_t>(1, a.K / (4 * BK));
-    splits = (int)std::min<int64_t>(std::min<int64_t>(want, maxs), 64);
+  {
+    const int64_t chunks = (a.K + BK - 1) / BK;
+    double best = 1e30;
+    for (int sp = 1; sp <= 64 && sp <= chunks; ++sp) {
+      const int64_t per = (chunks + sp - 1) / sp;
+      const double load = std::max(1.0, (double)(tiles * sp) / (double)cus);
+      double t = 5.0 + 0.7 * (double)per * load;
+      if (sp > 1) t += 3.0 + (double)sp * a.I * a.J * 8.0 / 3.0e6;
+      if (t < best - 1e-9) {
+        best = t;
+        splits = sp;
+      }
+    }
   }
   int kps = (a.K + splits - 1) / splits;
   kps = (kps + BK - 1) / BK * BK;
@@ -391,12 +412,12 @@ int launch(ConvArgs& a, float* final_out) {
   } else {
     a.out = final_out;
   }
-  hipLaunchKernelGGL((conv_lds_kernel<MODE, BI, BJ>), dim3((unsigned)tiles, (unsigned)splits),
+  hipLaunchKernelGGL((conv_lds_kernel<MODE, BK, PXK, QXK, SLOTS>), dim3((unsigned)tiles, (unsigned)splits),
                      dim3(256), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e == hipSuccess && splits > 1) {
     const int64_t n = (int64_t)a.I * a.J;
-    hipLaunchKernelGGL((conv_splitk_reduce_kernel<MODE>), dim3(wxx::grid_1d(n, 256, 8192)),
+    hipLaunchKernelGGL((conv_splitk_reduce_kernel<MODE>), dim3((unsigned)((n + 63) / 64)),
                        dim3(256), 0, s, a, (const float*)part, final_out);
     e = hipGetLastError();
   }
@@ -405,9 +426,80 @@ int launch(ConvArgs& a, float* final_out) {
   return WXX_OK;
 }
 
+// Which layout each operand takes for a shape: the one whose wave loads
+// touch fewer 128-byte lines over one chunk of a middle tile.  Cached per
+// shape (the count costs ~1 ms of host time).
+template <int MODE, int BK>
+std::pair<bool, bool> choose_layouts(const ConvArgs& a) {
+  using Key = std::tuple<int, int, int, int, int, int, int, int, int, int, int, int, int, int, int,
+                         int, int>;
+  static std::mutex mu;
+  static std::map<Key, std::pair<bool, bool>> cache;
+  const Key key{MODE, BK, a.B, a.Cin, a.H, a.W, a.Cout, a.KH, a.KW, a.Ho, a.Wo, a.sh, a.sw, a.ph,
+                a.pw, a.dh, a.dw};
+  {
+    std::lock_guard<std::mutex> g(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+  }
+  ConvArgs t = a;
+  t.tiles_i = (a.I + kTile - 1) / kTile;
+  t.tiles_j = (a.J + kTile - 1) / kTile;
+  const int i0 = (t.tiles_i / 2) * kTile, j0 = (t.tiles_j / 2) * kTile;
+  const int kbase = (a.K / 2) / BK * BK;
+  bool pxk = false, qxk = false;
+  if (MODE == kFwd || a.kcase != 0)
+    pxk = conv_lines<MODE, true, BK>(t, true, i0, kbase) <
+          conv_lines<MODE, true, BK>(t, false, i0, kbase);
+  if (a.kcase != 0)
+    qxk = conv_lines<MODE, false, BK>(t, true, j0, kbase) <
+          conv_lines<MODE, false, BK>(t, false, j0, kbase);
+  std::lock_guard<std::mutex> g(mu);
+  cache[key] = {pxk, qxk};
+  return {pxk, qxk};
+}
+
+template <int MODE, int BK>
+int dispatch_bk(ConvArgs& a, float* final_out) {
+  if (a.kcase == 0) {
+    // forward: W as row-major slots, im2col rows with scalar digits; dX / dW:
+    // both operands as rows
+    if constexpr (MODE == kFwd) return launch<MODE, BK, true, false, false>(a, final_out);
+    return launch<MODE, BK, false, false, false>(a, final_out);
+  }
+  const std::pair<bool, bool> l = choose_layouts<MODE, BK>(a);
+  if (l.first && l.second) return launch<MODE, BK, true, true, true>(a, final_out);
+  if (l.first) return launch<MODE, BK, true, false, true>(a, final_out);
+  if (l.second) return launch<MODE, BK, false, true, true>(a, final_out);
+  return launch<MODE, BK, false, false, true>(a, final_out);
+}
+
+// Device address of wxx_conv_zero_word (looked up once per device).
+const float* zero_word() {
+  static const float* ptr[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  if (!ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(wxx_conv_zero_word)) != hipSuccess) return nullptr;
+    ptr[dev] = (const float*)p;
+  }
+  return ptr[dev];
+}
+
 template <int MODE>
 int dispatch(ConvArgs& a, float* final_out) {
-  return launch<MODE, 64, 64>(a, final_out);
+  const int R2 = conv_r2(MODE, a), R12 = conv_r1(MODE, a) * R2;
+  // chunks of whole input channels of 3x3 taps for the forward and dX
+  const int bk = (MODE != kDw && R12 == 9) ? 36 : 32;
+  a.kcase = bk % R12 == 0 ? 1 : (MODE == kDw && R12 % bk == 0 && bk % R2 == 0) ? 2 : 0;
+  a.zero = zero_word();
+  if (!a.zero) return wxx::set_error(WXX_E_HIP, "conv: zero word address");
+  conv_prepare(MODE, a);
+  if constexpr (MODE != kDw) {
+    if (bk == 36) return dispatch_bk<MODE, 36>(a, final_out);
+  }
+  return dispatch_bk<MODE, 32>(a, final_out);
 }
 
 // Shapes of a convolution with input (B, Cin, H, W), weight (Cout, Cin, KH, KW)
