@@ -144,6 +144,7 @@ inline void __builtin_amdgcn_global_load_lds(const void* src, void* lds, unsigne
 inline void __builtin_amdgcn_s_waitcnt(int) {}
 // the inline-asm form of a dword global_load_lds (wxx_amd/csrc/common.h)
 #define WXX_LDS_DMA_DWORD(src, dst) __builtin_amdgcn_global_load_lds((src), (dst), 4, 0, 0)
+#define WXX_LDS_DMA_DWORDX4(src, dst) __builtin_amdgcn_global_load_lds((src), (dst), 16, 0, 0)
 #define WXX_S_BARRIER() __syncthreads()
 
 inline float __int_as_float(int v) { float f; std::memcpy(&f, &v, 4); return f; }

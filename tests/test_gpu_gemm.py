@@ -155,7 +155,7 @@ def test_matmul_every_tile_code(device, code, splits, ta, tb):
         check(out.numpy(), A, B, bias, ta, tb)
 
 
-@pytest.mark.parametrize("code", [11, 12, 13])
+@pytest.mark.parametrize("code", [11, 12, 13, 14])
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
 @pytest.mark.parametrize("batch,M,N,K,splits,bias_mode", [
     (1, 128, 256, 96, 1, 1),
@@ -164,7 +164,8 @@ def test_matmul_every_tile_code(device, code, splits, ta, tb):
 ])
 def test_matmul_direct_to_lds(device, code, ta, tb, batch, M, N, K, splits, bias_mode):
     # tiles 11 / 12 / 13: 128 x 128 / 128 x 192 / 128 x 64 operand tiles
-    # loaded straight into LDS in swizzled layouts; only for M a multiple of
+    # loaded straight into LDS in swizzled layouts (14: 128 x 64 with three
+    # buffers, two chunks of loads in flight); only for M a multiple of
     # 128, N of the tile width, and whole 32-deep K chunks (N scaled to 192 /
     # 384 for tile 12)
     import ctypes as C
@@ -221,6 +222,30 @@ def test_matmul_direct_to_lds_rejects_edge_tiles(device):
     with pytest.raises(lib.HIPError, match="tile 13"):
         lib.call("wxx_matmul_add", P(A.data_ptr()), P(B.data_ptr()), None, P(out.data_ptr()),
                  130, 128, 64, 1, 0, 0, 0, 0, 0, 0, 13)
+    with pytest.raises(lib.HIPError, match="tile 14"):
+        lib.call("wxx_matmul_add", P(A.data_ptr()), P(B.data_ptr()), None, P(out.data_ptr()),
+                 130, 128, 64, 1, 0, 0, 0, 0, 0, 0, 14)
+
+
+def test_matmul_three_buffer_tiles_equal_two_buffer_tiles(device):
+    # tile 14 runs tile 13's arithmetic with a deeper load pipeline: the same
+    # products added in the same order, so the results are equal bit for bit
+    import ctypes as C
+
+    from wxx_amd.backend import lib
+    from wxx_amd.functional._common import empty
+
+    P = C.c_void_p
+    for (M, N, K, splits) in [(1024, 1024, 1024, 2), (256, 192, 800, 1), (384, 128, 96, 3)]:
+        r = rng(M + K)
+        A, B = up(r.standard_normal((M, K)).astype(np.float32)), up(r.standard_normal((K, N)).astype(np.float32))
+        outs = []
+        for code in (13, 14):
+            out = empty([M, N])
+            lib.call("wxx_matmul_add", P(A.data_ptr()), P(B.data_ptr()), None, P(out.data_ptr()),
+                     M, N, K, 1, 0, 0, 0, 0, 0, 0, code + 256 * splits)
+            outs.append(out.numpy())
+        np.testing.assert_array_equal(outs[0], outs[1])
 
 
 @pytest.mark.parametrize("S,d", [(64, 64), (130, 64), (256, 32), (300, 64), (640, 64),

@@ -58,6 +58,21 @@ __device__ __forceinline__ void wxx_lds_dma_dword(const float* src, float* lds_d
 #pragma clang diagnostic pop
 #endif
 
+// The same for global_load_lds_dwordx4: every lane's 16 bytes at `src` land
+// at `lds_dst` + 16 * lane.
+#ifndef WXX_LDS_DMA_DWORDX4
+#define WXX_LDS_DMA_DWORDX4 wxx_lds_dma_dwordx4
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved; see above
+__device__ __forceinline__ void wxx_lds_dma_dwordx4(const float* src, float* lds_dst) {
+  const unsigned lds = __builtin_amdgcn_readfirstlane(
+      (unsigned)(uintptr_t)(__attribute__((address_space(3))) float*)lds_dst);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+#endif
+
 WXX_API int wxx_fill_u32(void* dst, int64_t n, uint32_t bits);
 WXX_API int wxx_h2d(void* dst, const void* src, size_t bytes);
 WXX_API void* wxx_alloc(size_t bytes);

@@ -449,15 +449,18 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
 // Step s = 4t + r of a chunk feeds the MFMA's K lanes k = 8t + r (lanes
 // 0-31) and k = 8t + 4 + r (lanes 32-63), so a k-contiguous fragment is one
 // ds_read_b128 per 4 steps.
-template <bool TA, bool TB, int BN>
+template <bool TA, bool TB, int BN, int NB = 2>
 __global__ __launch_bounds__(256, 2) void gemm_f32_dtl_kernel(GemmArgs g) {
   static_assert(BN == 64 || BN == 128 || BN == 192, "direct-to-LDS tiles are 128 x 64/128/192");
+  static_assert(NB == 2 || NB == 3, "two or three LDS buffers");
   constexpr int BM = 128, BK = 32, WM = 64, WN = BN / 2, TM = 2, TN = WN / 32;
   constexpr int RB = BN * BK / 256 / 4;  // 1 KiB regions of the B tile per wave
   __shared__ __attribute__((aligned(16))) float As0[BM * BK];
   __shared__ __attribute__((aligned(16))) float As1[BM * BK];
   __shared__ __attribute__((aligned(16))) float Bs0[BN * BK];
   __shared__ __attribute__((aligned(16))) float Bs1[BN * BK];
+  __shared__ __attribute__((aligned(16))) float As2[NB == 3 ? BM * BK : 4];
+  __shared__ __attribute__((aligned(16))) float Bs2[NB == 3 ? BN * BK : 4];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -503,15 +506,29 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_dtl_kernel(GemmArgs g) {
   const int64_t a_step = TA ? BK * g.lda : BK;
   const int64_t b_step = TB ? BK : BK * g.ldb;
 
+  // Two buffers: the compiler-tracked DMA builtin (it waits for all of a
+  // chunk's loads before the barrier anyway).  Three buffers: the same
+  // instruction as inline asm, which the compiler does not track, so that
+  // one chunk's loads stay in flight across the barrier (the tracked form
+  // gets a vmcnt(0) before every LDS read it cannot prove disjoint).
   auto issue = [&](int64_t kc, auto buf_tag) {
-    float* as = decltype(buf_tag)::value ? As1 : As0;
-    float* bs = decltype(buf_tag)::value ? Bs1 : Bs0;
+    constexpr int bt = decltype(buf_tag)::value;
+    float* as = bt == 2 ? As2 : (bt == 1 ? As1 : As0);
+    float* bs = bt == 2 ? Bs2 : (bt == 1 ? Bs1 : Bs0);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      __builtin_amdgcn_global_load_lds(pa[j] + kc * a_step, as + (4 * wave + j) * 256, 16, 0, 0);
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (NB == 3)
+        WXX_LDS_DMA_DWORDX4(pa[j] + kc * a_step, as + (4 * wave + j) * 256);
+      else
+        __builtin_amdgcn_global_load_lds(pa[j] + kc * a_step, as + (4 * wave + j) * 256, 16, 0, 0);
+    }
 #pragma unroll
-    for (int j = 0; j < RB; ++j)
-      __builtin_amdgcn_global_load_lds(pb[j] + kc * b_step, bs + (RB * wave + j) * 256, 16, 0, 0);
+    for (int j = 0; j < RB; ++j) {
+      if constexpr (NB == 3)
+        WXX_LDS_DMA_DWORDX4(pb[j] + kc * b_step, bs + (RB * wave + j) * 256);
+      else
+        __builtin_amdgcn_global_load_lds(pb[j] + kc * b_step, bs + (RB * wave + j) * 256, 16, 0, 0);
+    }
   };
 
   // fragment addresses (floats): k-contiguous row x = w * 64 + l32 (+ 32 a)
@@ -533,8 +550,9 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_dtl_kernel(GemmArgs g) {
       for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
   auto compute = [&](auto buf_tag) {
-    const float* as = decltype(buf_tag)::value ? As1 : As0;
-    const float* bs = decltype(buf_tag)::value ? Bs1 : Bs0;
+    constexpr int bt = decltype(buf_tag)::value;
+    const float* as = bt == 2 ? As2 : (bt == 1 ? As1 : As0);
+    const float* bs = bt == 2 ? Bs2 : (bt == 1 ? Bs1 : Bs0);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       float av[TM][4], bv[TN][4];
@@ -576,7 +594,31 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_dtl_kernel(GemmArgs g) {
 
   using B0 = std::integral_constant<int, 0>;
   using B1 = std::integral_constant<int, 1>;
-  if (nk > 0) {
+  using B2 = std::integral_constant<int, 2>;
+  if constexpr (NB == 3) {
+    // chunk c in buffer c % 3: at step c a wave waits until only its loads
+    // of chunk c + 1 are outstanding (loads complete in order), a bare
+    // barrier publishes chunk c and frees the buffer of chunk c - 1, which
+    // then receives chunk c + 2
+    constexpr int kPer = 4 + RB;  // loads per wave per chunk
+    constexpr int kWaitNext = 0x0F70 | (kPer & 15) | ((kPer >> 4) << 14);
+    auto step = [&](int64_t kc, auto cur, auto nxt2) {
+      if (kc + 1 < nk)
+        __builtin_amdgcn_s_waitcnt(kWaitNext);
+      else
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+      WXX_S_BARRIER();
+      if (kc + 2 < nk) issue(kc + 2, nxt2);
+      compute(cur);
+    };
+    if (nk > 0) issue(0, B0{});
+    if (nk > 1) issue(1, B1{});
+    for (int64_t kc = 0; kc < nk; kc += 3) {
+      step(kc, B0{}, B2{});
+      if (kc + 1 < nk) step(kc + 1, B1{}, B0{});
+      if (kc + 2 < nk) step(kc + 2, B2{}, B1{});
+    }
+  } else if (nk > 0) {
     issue(0, B0{});
     landed();
     for (int64_t kc = 0; kc < nk; kc += 2) {
@@ -615,6 +657,41 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmArgs g,
     else if (g.bias_mode == 3)
       v += g.bias[b * g.sBias + r];
     g.C[b * g.sC + row * g.ldc + col] = v;
+  }
+}
+
+// The same for a contiguous C (ldc == N) with N % 4 == 0, 16-byte aligned
+// partials and C, and fewer than 2^31 elements: four columns per thread,
+// 32-bit row arithmetic once per four elements.
+__global__ __launch_bounds__(256) void gemm_splitk_reduce4_kernel(GemmArgs g,
+                                                                   const float4* __restrict__ part,
+                                                                   int splits, int64_t batch) {
+  const int n4 = (int)(g.M * g.N * batch / 4), mn4 = (int)(g.M * g.N / 4), N4 = (int)(g.N / 4);
+  for (int e = blockIdx.x * 256 + threadIdx.x; e < n4; e += gridDim.x * 256) {
+    float4 v = part[e];
+    for (int z = 1; z < splits; ++z) {
+      const float4 q = part[(int64_t)z * n4 + e];
+      v.x += q.x;
+      v.y += q.y;
+      v.z += q.z;
+      v.w += q.w;
+    }
+    const int b = e / mn4, r4 = e - b * mn4;
+    const int row = r4 / N4, col = 4 * (r4 - row * N4);
+    const float* bias = nullptr;
+    if (g.bias_mode == 1)
+      bias = g.bias + col;
+    else if (g.bias_mode == 2)
+      bias = g.bias + (int64_t)(row % g.bias_rows) * g.N + col;
+    else if (g.bias_mode == 3)
+      bias = g.bias + (int64_t)b * g.sBias + (int64_t)row * g.N + col;
+    if (bias) {
+      v.x += bias[0];
+      v.y += bias[1];
+      v.z += bias[2];
+      v.w += bias[3];
+    }
+    *(float4*)(g.C + (int64_t)b * g.sC + (int64_t)row * g.N + col) = v;
   }
 }
 
@@ -664,8 +741,15 @@ int launch_cfg(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits = 1) {
   p.bias_mode = 0;
   int rc = launch_tiles<BM, BN, BK, WM, WN, NBUF, TRI, DTL>(p, batch, ta, tb, splits);
   if (rc == WXX_OK) {
-    hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3(wxx::grid_1d(n, 256, 8192)), dim3(256), 0,
-                       wxx::stream(), g, (const float*)part, splits, batch);
+    const bool vec4 = g.ldc == g.N && g.N % 4 == 0 && n < (int64_t(1) << 31) &&
+                      (batch == 1 || g.sC % 4 == 0) && (g.bias_mode != 3 || g.sBias % 4 == 0) &&
+                      ((uintptr_t)g.C & 15) == 0 && ((uintptr_t)part & 15) == 0;
+    if (vec4)
+      hipLaunchKernelGGL(gemm_splitk_reduce4_kernel, dim3(wxx::grid_1d(n / 4, 256, 8192)),
+                         dim3(256), 0, wxx::stream(), g, (const float4*)part, splits, batch);
+    else
+      hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3(wxx::grid_1d(n, 256, 8192)), dim3(256),
+                         0, wxx::stream(), g, (const float*)part, splits, batch);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) rc = wxx::set_error(WXX_E_HIP, "split-K reduce: %s", hipGetErrorString(e));
   }
@@ -684,14 +768,15 @@ int launch_tiles(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits) {
     // 128 x 192: 4 KiB of dynamic LDS on top of the tiles' 80 KiB, so that
     // one workgroup occupies a CU (the grids it is chosen for are <= 1 per CU)
     const unsigned dyn = BN == 192 ? 4096u : 0u;
+    constexpr int NB = NBUF == 3 ? 3 : 2;
     if (!ta && !tb)
-      hipLaunchKernelGGL((gemm_f32_dtl_kernel<false, false, BN>), grid, dim3(256), dyn, s, g);
+      hipLaunchKernelGGL((gemm_f32_dtl_kernel<false, false, BN, NB>), grid, dim3(256), dyn, s, g);
     else if (!ta && tb)
-      hipLaunchKernelGGL((gemm_f32_dtl_kernel<false, true, BN>), grid, dim3(256), dyn, s, g);
+      hipLaunchKernelGGL((gemm_f32_dtl_kernel<false, true, BN, NB>), grid, dim3(256), dyn, s, g);
     else if (ta && !tb)
-      hipLaunchKernelGGL((gemm_f32_dtl_kernel<true, false, BN>), grid, dim3(256), dyn, s, g);
+      hipLaunchKernelGGL((gemm_f32_dtl_kernel<true, false, BN, NB>), grid, dim3(256), dyn, s, g);
     else
-      hipLaunchKernelGGL((gemm_f32_dtl_kernel<true, true, BN>), grid, dim3(256), dyn, s, g);
+      hipLaunchKernelGGL((gemm_f32_dtl_kernel<true, true, BN, NB>), grid, dim3(256), dyn, s, g);
   } else {
     if (!ta && !tb)
       hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, false, NBUF, TRI>),
@@ -718,7 +803,8 @@ inline bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 // Strides are in elements; sA / sB == 0 marks an unbatched operand.
 // tile: 0 = choose automatically, 1 = 64x64, 2 = 128x128, 3 = 256x128; 4-10 select
 // alternative tile / K-chunk / buffering shapes of the same kernel; 11 / 12 / 13 the
-// direct-to-LDS 128x128 / 128x192 / 128x64 kernel.  With an
+// direct-to-LDS 128x128 / 128x192 / 128x64 kernel, 14 its 128x64 tiles with
+// three LDS buffers.  With an
 // explicit tile code, bits 8-15 give the number of K splits (0 or 1: none).
 namespace {
 int matmul_impl(const float* A, const float* B, const float* bias, float* C, int64_t M, int64_t N,
@@ -944,12 +1030,34 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
     const int64_t t64d = dtl64_ok && !thin ? (g.M / 128) * (g.N / 64) * nb : 0;
     const double bal64 =
         t64d > 0 ? (double)t64d / (double)(((t64d + cus - 1) / cus) * cus) : 0.0;
+    // 128 x 64 direct-to-LDS tiles split in K when they number fewer than
+    // the CUs, by the same balance and partial-pass cost (1024^3: 128 tiles
+    // x 2 splits, 25.3 + 3 us against 35.1 us on unsplit 64 x 64 tiles).
+    int s64 = 0;
+    double bal64s = 0.0;
+    if (t64d > 0 && t64d < cus) {
+      for (int sp = 2; sp <= 4; ++sp) {
+        if (g.K / sp < 256) break;
+        const int64_t units = t64d * sp;
+        const double bal = (double)units / (double)(((units + cus - 1) / cus) * cus) /
+                           (1.0 + (double)(sp + 1) * 52.0 / (double)g.K);
+        if (bal > bal64s + 1e-9) {
+          bal64s = bal;
+          s64 = sp;
+        }
+      }
+    }
     if (t192 > 0 && t192 <= cus && bal192 >= 0.9 && bal192 > best) {
       tile = 12;
       splits = 1;
     } else if (t64d >= cus && t64d <= 4 * cus && bal64 >= 0.95 && bal64 > best) {
       tile = 13;
       splits = 1;
+    } else if (s64 > 0 && bal64s >= 0.8 && bal64s > best) {
+      // three buffers: one round of one workgroup per CU has nothing else
+      // to hide its load latency behind (1024^3: 29.5 against 30.2 us)
+      tile = 14;
+      splits = s64;
     } else if (dtl_ok && t128 * smax >= cus && best >= 0.8) {
       tile = 11;
       splits = best_splits;
@@ -1040,6 +1148,11 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
       WXX_REQUIRE(dtl64_ok, "tile 13 needs M a multiple of 128, N of 64, K of 32 and "
                   "16-byte aligned operands");
       return launch_cfg<128, 64, 32, 64, 32, 2, false, true>(g, nb, transpose_A, transpose_B,
+                                                             splits);
+    case 14:
+      WXX_REQUIRE(dtl64_ok, "tile 14 needs M a multiple of 128, N of 64, K of 32 and "
+                  "16-byte aligned operands");
+      return launch_cfg<128, 64, 32, 64, 32, 3, false, true>(g, nb, transpose_A, transpose_B,
                                                              splits);
     default: return wxx::set_error(WXX_E_ARG, "bad tile %d", tile);
   }
