@@ -63,6 +63,53 @@ def test_pointwise_strided_views(device):
                  np.transpose(x, (0, 2, 1))[:, :, :1] + np.transpose(y, (0, 2, 1)))
 
 
+@pytest.mark.parametrize("op", [0, 2, 3])
+@pytest.mark.parametrize("cols,off", [(16, 0), (682, 0), (682, 682), (33, 0), (12, 1)])
+def test_pointwise_row_views_every_access_width(device, op, cols, off):
+    # rank-2 views of unit column stride (the halves of a chunked (rows, 2
+    # cols + 8) tensor, a row broadcast, in place): rows whose bases allow
+    # 16-byte (cols 16), 8-byte (cols 682, also the second half first) or
+    # 4-byte (cols 33; offset 1) accesses, bit-exact against float32
+    rows, width = 300, 2 * cols + 8
+    h = rng(60 + cols + off).standard_normal((rows, width)).astype(np.float32)
+    v = rng(70 + cols).standard_normal((cols,)).astype(np.float32) + (3.0 if op == 3 else 0.0)
+    o2 = 0 if off == cols else cols + 4
+    h1, h2 = h[:, off:off + cols], h[:, o2:o2 + cols] + (3.0 if op == 3 else 0.0)
+    th = up(h)
+    x1 = th.narrow(1, off, cols)
+    x2 = th.narrow(1, o2, cols)
+    if op == 3:
+        x2 = F().scalarpointwise(x2, 3.0, 0)
+    assert np.array_equal(F().pointwise(x1, x2, op).numpy(), oe.pointwise(h1, h2, op))
+    assert np.array_equal(F().pointwise(x1, up(v), op).numpy(), oe.pointwise(h1, v, op))
+    tc = up(np.ascontiguousarray(h1))
+    F()._pointwise(tc, up(v), op)
+    assert np.array_equal(tc.numpy(), oe.pointwise(h1, v, op))
+
+
+@pytest.mark.parametrize("op", [0, 1, 2, 3])
+@pytest.mark.parametrize("shape", [(3, 70, 130), (130, 70), (2, 256, 512)])
+@pytest.mark.parametrize("which", ["a", "b"])
+def test_pointwise_one_operand_transposed(device, op, shape, which):
+    # one operand a transposed view (unit stride along the second-last dim),
+    # the other and the output row-major: the LDS-tiled path, ragged 64 x 64
+    # tiles, bit-exact against float32
+    t_shape = shape[:-2] + (shape[-1], shape[-2])
+    src = rng(80 + op).standard_normal(t_shape).astype(np.float32)
+    other = rng(90 + op).standard_normal(shape).astype(np.float32)
+    if op == 3:
+        src, other = src + 3.0, other + 3.0
+    perm = tuple(range(len(shape) - 2)) + (len(shape) - 1, len(shape) - 2)
+    tv = F().permute(up(src), *perm)
+    sv = np.transpose(src, perm)
+    assert not tv.is_contiguous()
+    if which == "a":
+        got, want = F().pointwise(tv, up(other), op), oe.pointwise(sv, other, op)
+    else:
+        got, want = F().pointwise(up(other), tv, op), oe.pointwise(other, sv, op)
+    assert np.array_equal(got.numpy(), want)
+
+
 def test_pointwise_inplace_and_alias(device):
     a = rng(6).standard_normal((3, 4)).astype(np.float32)
     b = rng(7).standard_normal((4,)).astype(np.float32)

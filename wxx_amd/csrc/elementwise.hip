@@ -22,6 +22,7 @@
 #include "nd.h"
 
 #include <cmath>
+#include <type_traits>
 
 namespace {
 
@@ -69,6 +70,84 @@ __global__ __launch_bounds__(kBlock) void binary_flat4_kernel(float4* __restrict
     float4 x = a[i], y = b[i];
     out[i] = make_float4(binop(op, x.x, y.x), binop(op, x.y, y.y), binop(op, x.z, y.z),
                          binop(op, x.w, y.w));
+  }
+}
+
+// Rank 2 (rows x cols) with unit column stride in every operand (b's row
+// stride may be 0: a row broadcast): V consecutive columns per thread item
+// through V-wide accesses (the host picks the widest that every row base
+// allows), four items in flight per thread, 32-bit index arithmetic.
+template <int V>
+__global__ __launch_bounds__(kBlock) void binary_rows_kernel(float* __restrict__ out,
+                                                             const float* __restrict__ a,
+                                                             const float* __restrict__ b, int rows,
+                                                             int cols, int so, int sa, int sb,
+                                                             int op) {
+  using T = typename std::conditional<V == 4, float4, typename std::conditional<V == 2, float2,
+                                                                                float>::type>::type;
+  const int cg = cols / V;  // items per row
+  const int total = rows * cg, step = gridDim.x * kBlock;
+  for (int t0 = blockIdx.x * kBlock + threadIdx.x; t0 < total; t0 += 4 * step) {
+    T x[4], y[4];
+    int oo[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = t0 + u * step;
+      if (t < total) {
+        const int r = t / cg, c = (t - r * cg) * V;
+        x[u] = *reinterpret_cast<const T*>(a + r * sa + c);
+        y[u] = *reinterpret_cast<const T*>(b + r * sb + c);
+        oo[u] = r * so + c;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (t0 + u * step < total) {
+        if constexpr (V == 4)
+          *reinterpret_cast<float4*>(out + oo[u]) =
+              make_float4(binop(op, x[u].x, y[u].x), binop(op, x[u].y, y[u].y),
+                          binop(op, x[u].z, y[u].z), binop(op, x[u].w, y[u].w));
+        else if constexpr (V == 2)
+          *reinterpret_cast<float2*>(out + oo[u]) =
+              make_float2(binop(op, x[u].x, y[u].x), binop(op, x[u].y, y[u].y));
+        else
+          out[oo[u]] = binop(op, x[u], y[u]);
+      }
+    }
+  }
+}
+
+// (batch, M, N) with out and one operand row-major (unit stride along N) and
+// the other column-major (unit stride along M, a transposed view): 64 x 64
+// tiles, the column-major operand read along M into LDS and read back along N,
+// so every global access runs along an operand's unit stride.  tr = 1: a is
+// the column-major operand, 2: b.
+__global__ __launch_bounds__(kBlock) void binary_transposed_kernel(
+    float* __restrict__ out, const float* __restrict__ a, const float* __restrict__ b, int M,
+    int N, int tiles_n, int64_t so0, int64_t so1, int64_t sa0, int64_t sa1, int64_t sa2,
+    int64_t sb0, int64_t sb1, int64_t sb2, int tr, int op) {
+  __shared__ float t[64][65];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
+  const int m0 = tm * 64, n0 = tn * 64;
+  const int64_t bt = blockIdx.y;
+  const float* T = tr == 1 ? a + bt * sa0 : b + bt * sb0;  // column-major: unit stride along M
+  const int64_t tsn = tr == 1 ? sa2 : sb2;
+  const float* R = tr == 1 ? b + bt * sb0 : a + bt * sa0;  // row-major: unit stride along N
+  const int64_t rsm = tr == 1 ? sb1 : sa1;
+#pragma unroll
+  for (int r = ty; r < 64; r += 4) {
+    const int n = n0 + r, m = m0 + tx;
+    if (n < N && m < M) t[r][tx] = T[(int64_t)n * tsn + m];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = ty; r < 64; r += 4) {
+    const int m = m0 + r, n = n0 + tx;
+    if (m < M && n < N) {
+      const float tv = t[tx][r], rv = R[(int64_t)m * rsm + n];
+      out[bt * so0 + (int64_t)m * so1 + n] = tr == 1 ? binop(op, tv, rv) : binop(op, rv, tv);
+    }
   }
 }
 
@@ -410,6 +489,34 @@ bool fits32(const ND& nd, int64_t n) {
   return true;
 }
 
+// Rank 2 or 3 (batch, M, N) with out row-major along N (unit stride), one of
+// a / b row-major along N and the other with unit stride along M: returns
+// 1 (a column-major) or 2 (b column-major), else 0.  Batches fit grid y and
+// M, N fit 32 bits.
+int transposed_pair(const ND& nd) {
+  if (nd.rank != 2 && nd.rank != 3) return 0;
+  const int r3 = nd.rank == 3;
+  const int im = r3, in = r3 + 1;
+  if (nd.shape[im] < 2 || nd.shape[in] < 2 || nd.shape[im] >= (int64_t(1) << 31) ||
+      nd.shape[in] >= (int64_t(1) << 31) || (r3 && nd.shape[0] > 65535))
+    return 0;
+  if (nd.stride[0][in] != 1) return 0;
+  const bool a_row = nd.stride[1][in] == 1, b_row = nd.stride[2][in] == 1;
+  const bool a_col = nd.stride[1][im] == 1, b_col = nd.stride[2][im] == 1;
+  if (b_row && a_col && !a_row) return 1;
+  if (a_row && b_col && !b_row) return 2;
+  return 0;
+}
+
+// Every offset r * row_stride + c of a rank-2 view stays below 2^31.
+bool rows_fit32(const ND& nd) {
+  for (int k = 0; k < 3; ++k) {
+    const int64_t st = nd.stride[k][0];
+    if (st < 0 || (nd.shape[0] - 1) * st + nd.shape[1] >= (int64_t(1) << 31)) return false;
+  }
+  return true;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -436,6 +543,37 @@ WXX_API int wxx_pointwise(float* out, const float* a, const float* b, int rank,
       n % 4 == 0 && ((uintptr_t)out | (uintptr_t)a | (uintptr_t)b) % 16 == 0) {
     hipLaunchKernelGGL(binary_flat4_kernel, dim3(grid_for(n / 4)), dim3(kBlock), 0, s,
                        (float4*)out, (const float4*)a, (const float4*)b, n / 4, op);
+  } else if (transposed_pair(nd) != 0) {
+    // one operand a transposed view of the others' layout
+    const int tr = transposed_pair(nd);
+    const int r3 = nd.rank == 3;
+    const int64_t B = r3 ? nd.shape[0] : 1, M = nd.shape[r3], N = nd.shape[r3 + 1];
+    const int tiles_n = (int)((N + 63) / 64);
+    const dim3 grid((unsigned)(((M + 63) / 64) * tiles_n), (unsigned)B);
+    hipLaunchKernelGGL(binary_transposed_kernel, grid, dim3(kBlock), 0, s, out, a, b, (int)M,
+                       (int)N, tiles_n, r3 ? nd.stride[0][0] : 0, nd.stride[0][r3],
+                       r3 ? nd.stride[1][0] : 0, nd.stride[1][r3], nd.stride[1][r3 + 1],
+                       r3 ? nd.stride[2][0] : 0, nd.stride[2][r3], nd.stride[2][r3 + 1], tr, op);
+  } else if (nd.rank == 2 && nd.stride[0][1] == 1 && nd.stride[1][1] == 1 &&
+             nd.stride[2][1] == 1 && fits32(nd, n) && rows_fit32(nd)) {
+    // rows of unit stride (a strided view's rows, a row broadcast): the
+    // widest access every row base and the row length allow
+    const int rows = (int)nd.shape[0], cols = (int)nd.shape[1];
+    const int64_t so = nd.stride[0][0], sa = nd.stride[1][0], sb = nd.stride[2][0];
+    auto fits = [&](int v) {
+      const uintptr_t bytes = 4 * (uintptr_t)v;
+      return cols % v == 0 && so % v == 0 && sa % v == 0 && sb % v == 0 &&
+             ((uintptr_t)out | (uintptr_t)a | (uintptr_t)b) % bytes == 0;
+    };
+    if (fits(4))
+      hipLaunchKernelGGL(binary_rows_kernel<4>, dim3(grid_for(n / 16)), dim3(kBlock), 0, s, out,
+                         a, b, rows, cols, (int)so, (int)sa, (int)sb, op);
+    else if (fits(2))
+      hipLaunchKernelGGL(binary_rows_kernel<2>, dim3(grid_for(n / 8)), dim3(kBlock), 0, s, out,
+                         a, b, rows, cols, (int)so, (int)sa, (int)sb, op);
+    else
+      hipLaunchKernelGGL(binary_rows_kernel<1>, dim3(grid_for(n / 4)), dim3(kBlock), 0, s, out,
+                         a, b, rows, cols, (int)so, (int)sa, (int)sb, op);
   } else if (fits32(nd, n)) {
     hipLaunchKernelGGL(binary_kernel<false>, dim3(grid_for(n)), dim3(kBlock), 0, s, out, a, b,
                        nd, n, op);

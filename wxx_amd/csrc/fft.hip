@@ -913,6 +913,46 @@ __global__ __launch_bounds__(256) void complex_binary_kernel(float2* __restrict_
   }
 }
 
+// a and out contiguous over all n elements, b contiguous too (BROW false) or
+// one row of `cols` elements repeated for every row (BROW true: a spectrum
+// times a filter or a weight vector broadcast over its rows): two elements
+// per thread through 16-byte loads and stores, four pairs in flight per
+// thread, 32-bit index arithmetic (2 n < 2^31).
+template <bool BROW>
+__global__ __launch_bounds__(256) void complex_binary_pairs_kernel(
+    float4* __restrict__ out, const float4* __restrict__ a, const float2* __restrict__ b,
+    int n2, int cols, int op, int conj_a, int conj_b) {
+  const int step = gridDim.x * 256;
+  for (int t0 = blockIdx.x * 256 + threadIdx.x; t0 < n2; t0 += 4 * step) {
+    float4 av[4], bv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = t0 + u * step;
+      if (t < n2) {
+        av[u] = a[t];
+        if (!BROW) {
+          bv[u] = reinterpret_cast<const float4*>(b)[t];
+        } else {
+          const int c = (2 * t) % cols;  // the pair's first column; the second may wrap
+          const float2 b0 = b[c], b1 = b[c + 1 == cols ? 0 : c + 1];
+          bv[u] = make_float4(b0.x, b0.y, b1.x, b1.y);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = t0 + u * step;
+      if (t < n2) {
+        const float2 r0 = complex_op(make_float2(av[u].x, av[u].y), make_float2(bv[u].x, bv[u].y),
+                                     op, conj_a, conj_b);
+        const float2 r1 = complex_op(make_float2(av[u].z, av[u].w), make_float2(bv[u].z, bv[u].w),
+                                     op, conj_a, conj_b);
+        out[t] = make_float4(r0.x, r0.y, r1.x, r1.y);
+      }
+    }
+  }
+}
+
 // Rank <= 2 after collapsing (rows x columns, e.g. a (B, D, F) spectrum times
 // a (D, F) filter): rows on grid y, columns on grid x, no index division.
 __global__ __launch_bounds__(256) void complex_binary_rows_kernel(
@@ -1039,6 +1079,29 @@ WXX_API int wxx_complex_binary(void* out, const void* a, const void* b, int rank
   const int ca = conj_a ? 1 : 0, cb = conj_b ? 1 : 0;
   if (nd.rank <= 2) {
     const int64_t cols = nd.shape[nd.rank - 1], rows = n / cols;
+    // out and a one contiguous run of n, b the same run or one row broadcast
+    const int c0 = nd.rank - 1;
+    const bool flat_oa = nd.stride[0][c0] == 1 && nd.stride[1][c0] == 1 &&
+                         (nd.rank == 1 || (nd.stride[0][0] == cols && nd.stride[1][0] == cols));
+    const bool b_flat = nd.stride[2][c0] == 1 && (nd.rank == 1 || nd.stride[2][0] == cols);
+    const bool b_row = nd.stride[2][c0] == 1 && nd.rank == 2 && nd.stride[2][0] == 0;
+    const bool b_one = nd.stride[2][c0] == 0 && (nd.rank == 1 || nd.stride[2][0] == 0);
+    auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    if (flat_oa && n % 2 == 0 && n < (int64_t(1) << 30) && al16(o) && al16(pa) &&
+        ((b_flat && al16(pb)) || b_row || b_one)) {
+      const int64_t n2 = n / 2;
+      const dim3 grid((unsigned)std::max<int64_t>(1, std::min<int64_t>((n2 + 1023) / 1024, 16384)));
+      if (b_flat)
+        hipLaunchKernelGGL(complex_binary_pairs_kernel<false>, grid, dim3(256), 0, wxx::stream(),
+                           reinterpret_cast<float4*>(o), reinterpret_cast<const float4*>(pa), pb,
+                           (int)n2, 1, op, ca, cb);
+      else
+        hipLaunchKernelGGL(complex_binary_pairs_kernel<true>, grid, dim3(256), 0, wxx::stream(),
+                           reinterpret_cast<float4*>(o), reinterpret_cast<const float4*>(pa), pb,
+                           (int)n2, b_one ? 1 : (int)cols, op, ca, cb);
+      WXX_LAUNCHED();
+      return WXX_OK;
+    }
     const int64_t gy = std::min<int64_t>(rows, 65535);
     const int64_t gx = std::min<int64_t>((cols + 255) / 256, std::max<int64_t>(64, 16384 / gy));
     const dim3 grid((unsigned)gx, (unsigned)gy);
