@@ -239,6 +239,12 @@ int wxx_batchnormdg(const float* dy, const float* x, const float* saved_mean,
 int wxx_batchnormdx(const float* dy, const float* x, const float* gamma, const float* dgamma,
                     const float* dbeta, const float* saved_mean, const float* inv_std,
                     float* dx, int64_t B, int64_t C, int64_t HW);
+/* functional.batchnormdg then functional.batchnormdx (functional/normalization.py:209-305),
+ * as autograd's batchnorm backward calls them (autograd/normalization.py): dgamma, dbeta
+ * and dx in one call (one launch while B*HW <= 32768) */
+int wxx_batchnorm_backward(const float* dy, const float* x, const float* gamma,
+                           const float* saved_mean, const float* inv_std, float* dgamma,
+                           float* dbeta, float* dx, int64_t B, int64_t C, int64_t HW);
 
 /* ---- E: elementwise / layout -------------------------------------------- */
 /* functional.pointwise (functional/pointwise.py:29-98) and, with out == a,

@@ -105,8 +105,9 @@ def test_rmsnorm_fwd_bwd(device, shape, axis):
                        on.rmsnormdg(dy, x, er, axis=axis, dtype=F32), msg="dgamma")
 
 
+# B*H*W <= 32768 take the one-launch kernels; (64, 3, 48, 48) the split path
 @pytest.mark.parametrize("shape", [(4, 3, 2, 2), (128, 64, 16, 16), (128, 512, 1, 1),
-                                   (2, 5, 7, 3)])
+                                   (2, 5, 7, 3), (64, 3, 48, 48)])
 @pytest.mark.parametrize("training", [True, False])
 def test_batchnorm(device, shape, training):
     r = rng(60)
@@ -133,6 +134,13 @@ def test_batchnorm(device, shape, training):
     dx = F().batchnormdx(up(dy), up(x), up(g), dg, db, mu, inv)
     assert_error_floor(dx.numpy(), on.batchnormdx(dy, x, g, edg, edb, emu, einv),
                        on.batchnormdx(dy, x, g, edg, edb, emu, einv, dtype=F32), msg="dx")
+    # the autograd backward's one call: the same three results
+    dx2, dg2, db2 = F().batchnorm_backward(up(dy), up(x), up(g), mu, inv)
+    assert_error_floor(dg2.numpy(), edg, fdg, msg="batchnorm_backward dgamma")
+    assert_error_floor(db2.numpy(), edb, fdb, msg="batchnorm_backward dbeta")
+    assert_error_floor(dx2.numpy(), on.batchnormdx(dy, x, g, edg, edb, emu, einv),
+                       on.batchnormdx(dy, x, g, edg, edb, emu, einv, dtype=F32),
+                       msg="batchnorm_backward dx")
 
 
 def test_norm_parameter_size_is_validated(device):

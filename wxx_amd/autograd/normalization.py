@@ -48,7 +48,6 @@ class batchnorm(Function):
     def backward(self, g):
         x, gamma, mean, istd = self.tensor1, self.gamma, self.mean, self.istd
         self.tensor1 = self.gamma = self.mean = self.istd = None
-        gg, gb = functional.batchnormdg(g, x, mean, istd)
-        gx = functional.batchnormdx(g, x, gamma, gg, gb, mean, istd)
+        gx, gg, gb = functional.batchnorm_backward(g, x, gamma, mean, istd)
         grads = [gx, gg, gb]
         return grads + [None] * (len(self.inputs) - 3)

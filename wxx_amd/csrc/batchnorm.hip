@@ -131,6 +131,114 @@ __global__ __launch_bounds__(kBlock) void bn_dx_kernel(
   }
 }
 
+// Channels of at most kFusedMaxM elements (every BatchNorm of ResNet18 at
+// batch 128 on 32x32 images) run as one workgroup of up to 1024 threads per
+// channel that holds the channel in registers (E elements per thread, all
+// loads issued at once), takes the statistics and writes the output in one
+// launch: the split path's three launches (partials, finalize, apply) cost
+// more in latency than their extra parallelism gains on these sizes.  Same
+// formulas, the sums in another (fixed) order.
+constexpr int64_t kFusedMaxM = 32768;
+
+__device__ __forceinline__ int64_t bn_index(int m, int HW, int Cc, int c) {
+  const int bb = m / HW, sp = m - bb * HW;
+  return ((int64_t)bb * Cc + c) * HW + sp;
+}
+
+template <int E>
+__global__ __launch_bounds__(1024) void bn_fused_fwd_kernel(
+    const float* __restrict__ x, const float* __restrict__ g, const float* __restrict__ b,
+    float* __restrict__ running_mean, float* __restrict__ running_var, float* __restrict__ y,
+    float* __restrict__ saved_mean, float* __restrict__ inv_std, int B, int Cc, int HW, float eps,
+    float momentum) {
+  __shared__ float red[16];
+  const int c = blockIdx.x, T = blockDim.x;
+  const int M = B * HW;
+  float v[E];
+  float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int m = threadIdx.x + e * T;
+    v[e] = m < M ? x[bn_index(m, HW, Cc, c)] : 0.f;
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    s1 += v[e];
+    s2 += v[e] * v[e];
+  }
+  const float S = wxx::block_sum(s1, red);
+  const float Q = wxx::block_sum(s2, red);
+  const float mf = (float)M;
+  const float mu = S / mf;
+  const float var = fmaxf(0.f, Q / mf - mu * mu);
+  const float is = rsqrtf(var + eps);
+  if (threadIdx.x == 0) {
+    saved_mean[c] = mu;
+    inv_std[c] = is;
+    running_mean[c] = (1.f - momentum) * running_mean[c] + momentum * mu;
+    const float unbiased = M > 1 ? var * (mf / (mf - 1.f)) : var;
+    running_var[c] = (1.f - momentum) * running_var[c] + momentum * unbiased;
+  }
+  const float gc = g[c], bc = b[c];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int m = threadIdx.x + e * T;
+    if (m < M) y[bn_index(m, HW, Cc, c)] = (v[e] - mu) * is * gc + bc;
+  }
+}
+
+// dgamma, dbeta and dx of one channel per workgroup (sizes as above).
+template <int E>
+__global__ __launch_bounds__(1024) void bn_fused_bwd_kernel(
+    const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ g,
+    const float* __restrict__ mean, const float* __restrict__ inv, float* __restrict__ dg,
+    float* __restrict__ db, float* __restrict__ dx, int B, int Cc, int HW) {
+  __shared__ float red[16];
+  const int c = blockIdx.x, T = blockDim.x;
+  const int M = B * HW;
+  const float mu = mean[c], is = inv[c];
+  float d[E], xh[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int m = threadIdx.x + e * T;
+    const bool in = m < M;
+    const int64_t i = in ? bn_index(m, HW, Cc, c) : 0;
+    d[e] = in ? dy[i] : 0.f;
+    xh[e] = in ? (x[i] - mu) * is : 0.f;
+  }
+  float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    s1 += d[e] * xh[e];
+    s2 += d[e];
+  }
+  const float A = wxx::block_sum(s1, red);
+  const float Bs = wxx::block_sum(s2, red);
+  if (threadIdx.x == 0) {
+    dg[c] = A;
+    db[c] = Bs;
+  }
+  const float mf = (float)M;
+  const float k = g[c] * is / mf;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int m = threadIdx.x + e * T;
+    if (m < M) dx[bn_index(m, HW, Cc, c)] = k * (mf * d[e] - Bs - xh[e] * A);
+  }
+}
+
+// Threads per channel (a multiple of 64, at most 1024) and elements per
+// thread E for a channel of M <= kFusedMaxM elements.
+struct FusedGeo {
+  int threads, E;
+};
+FusedGeo fused_geo(int64_t M) {
+  int E = 1;
+  while ((int64_t)E * 1024 < M) E *= 2;
+  const int64_t t = (M + E - 1) / E;
+  return {(int)std::min<int64_t>(1024, (t + 63) / 64 * 64), E};
+}
+
 int pick_splits(int64_t Cc, int64_t M) {
   const int64_t target = (int64_t)wxx::num_cus() * 8;
   int64_t s = (target + Cc - 1) / Cc;
@@ -151,6 +259,24 @@ WXX_API int wxx_batchnorm(const float* x, const float* gamma, const float* beta,
   WXX_REQUIRE(B >= 0 && C >= 1 && HW >= 0, "bad batchnorm dims");
   hipStream_t s = wxx::stream();
   const int64_t M = B * HW;
+  if (training && M > 0 && M <= kFusedMaxM && C <= 0x7fffffff && B * C * HW < (int64_t(1) << 31)) {
+    const FusedGeo fg = fused_geo(M);
+    const dim3 grid((unsigned)C), block((unsigned)fg.threads);
+#define WXX_BN_FWD(EE)                                                                         \
+  hipLaunchKernelGGL(bn_fused_fwd_kernel<EE>, grid, block, 0, s, x, gamma, beta, running_mean, \
+                     running_var, y, saved_mean, inv_std, (int)B, (int)C, (int)HW, eps, momentum)
+    switch (fg.E) {
+      case 1: WXX_BN_FWD(1); break;
+      case 2: WXX_BN_FWD(2); break;
+      case 4: WXX_BN_FWD(4); break;
+      case 8: WXX_BN_FWD(8); break;
+      case 16: WXX_BN_FWD(16); break;
+      default: WXX_BN_FWD(32); break;
+    }
+#undef WXX_BN_FWD
+    WXX_LAUNCHED();
+    return WXX_OK;
+  }
   int splits = 1;
   float* part = nullptr;
   if (training) {
@@ -210,4 +336,37 @@ WXX_API int wxx_batchnormdx(const float* dy, const float* x, const float* gamma,
                      HW, (float)(B * HW));
   WXX_LAUNCHED();
   return WXX_OK;
+}
+
+// functional.batchnormdg followed by functional.batchnormdx (reference
+// normalization.py:209-305) in one call: the autograd backward of batchnorm.
+WXX_API int wxx_batchnorm_backward(const float* dy, const float* x, const float* gamma,
+                                   const float* saved_mean, const float* inv_std, float* dgamma,
+                                   float* dbeta, float* dx, int64_t B, int64_t C, int64_t HW) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(dy && x && gamma && saved_mean && inv_std && dgamma && dbeta && dx, "null pointer");
+  WXX_REQUIRE(B >= 0 && C >= 1 && HW >= 0, "bad batchnorm dims");
+  const int64_t M = B * HW;
+  if (M > 0 && M <= kFusedMaxM && B * C * HW < (int64_t(1) << 31)) {
+    const FusedGeo fg = fused_geo(M);
+    const dim3 grid((unsigned)C), block((unsigned)fg.threads);
+    hipStream_t s = wxx::stream();
+#define WXX_BN_BWD(EE)                                                                        \
+  hipLaunchKernelGGL(bn_fused_bwd_kernel<EE>, grid, block, 0, s, dy, x, gamma, saved_mean, inv_std, \
+                     dgamma, dbeta, dx, (int)B, (int)C, (int)HW)
+    switch (fg.E) {
+      case 1: WXX_BN_BWD(1); break;
+      case 2: WXX_BN_BWD(2); break;
+      case 4: WXX_BN_BWD(4); break;
+      case 8: WXX_BN_BWD(8); break;
+      case 16: WXX_BN_BWD(16); break;
+      default: WXX_BN_BWD(32); break;
+    }
+#undef WXX_BN_BWD
+    WXX_LAUNCHED();
+    return WXX_OK;
+  }
+  int rc = wxx_batchnormdg(dy, x, saved_mean, inv_std, dgamma, dbeta, B, C, HW);
+  if (rc) return rc;
+  return wxx_batchnormdx(dy, x, gamma, dgamma, dbeta, saved_mean, inv_std, dx, B, C, HW);
 }

@@ -156,6 +156,24 @@ def batchnormdx(grad, tensor1, gamma, dgamma, dbeta, saved_mean, saved_std):
     return dx
 
 
+def batchnorm_backward(grad, tensor1, gamma, saved_mean, saved_std):
+    """``(dx, dgamma, dbeta)``: :func:`batchnormdg` then :func:`batchnormdx` in one call."""
+    tensor1 = contiguous_f32(tensor1)
+    gamma = contiguous_f32(gamma, "gamma")
+    grad = contiguous_f32(grad, "grad")
+    validation.check_rank(tensor1.shape, min_rank=4, max_rank=4, name="batchnorm input")
+    B, Cc, H, W = tensor1.shape
+    validation.check_same_shape(grad.shape, tensor1.shape, name="grad and input")
+    for t, name in ((gamma, "gamma"), (saved_mean, "saved_mean"), (saved_std, "saved_std")):
+        _check_param(t, Cc, name)
+    dx = empty(tensor1.shape)
+    dg = empty((Cc,))
+    db = empty((Cc,))
+    call("wxx_batchnorm_backward", ptr(grad), ptr(tensor1), ptr(gamma), ptr(saved_mean),
+         ptr(saved_std), ptr(dg), ptr(db), ptr(dx), B, Cc, H * W)
+    return dx, dg, db
+
+
 def batchnormdg(grad, tensor1, saved_mean, saved_std):
     tensor1 = contiguous_f32(tensor1)
     grad = contiguous_f32(grad, "grad")
