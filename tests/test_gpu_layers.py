@@ -148,6 +148,21 @@ def test_embed_bit_exact_and_embeddx(device, V, D, B, L):
     assert_close(got, ol.embeddx(g, ids, V), rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("V,D,ntok", [(1024, 8, 65536), (50304, 4, 8192), (3, 5, 10000),
+                                      (1024, 256, 65536)])
+def test_embeddx_token_order_bit_exact(device, V, D, ntok):
+    # the gradient row of id v adds its tokens' rows in token order, which
+    # a float32 np.add.at reproduces bit for bit (Hyena's 1024 x 65536
+    # tokens, GPT-2's vocabulary, a few ids with long runs; the placement
+    # cuts the token list into segments for these sizes)
+    ids = rng(V + ntok).integers(0, V, ntok).astype(np.uint32)
+    g = rng(D).standard_normal((ntok, D)).astype(np.float32)
+    want = np.zeros((V, D), np.float32)
+    np.add.at(want, ids.astype(np.int64), g)
+    got = F().embeddx(up(g), up_u32(ids), ntok, D, V).numpy()
+    assert np.array_equal(got, want)
+
+
 def test_embeddx_repeated_and_out_of_range_ids(device):
     V, D = 5, 6
     ids = np.array([[1, 1, 1, 9, 0, 1]], np.uint32)

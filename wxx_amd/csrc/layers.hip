@@ -117,6 +117,56 @@ __global__ __launch_bounds__(kBlock) void embed_place_kernel(const uint32_t* __r
   }
 }
 
+// The same placement with the token list cut into nseg segments of seglen
+// tokens, so that V x nseg threads share the V x ntok compares: count each
+// (segment, id), turn the counts into each segment's write offset per id
+// (an exclusive scan over segments from offsets[v]), then place each
+// segment's tokens in token order.  The result equals embed_place_kernel's.
+__global__ __launch_bounds__(kBlock) void embed_seg_count_kernel(const uint32_t* __restrict__ ids,
+                                                                 uint32_t* __restrict__ cnt,
+                                                                 int64_t ntok, int64_t V,
+                                                                 int seglen) {
+  __shared__ uint32_t sid[kPlaceChunk];
+  const int64_t v = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.y * seglen;
+  const int len = (int)min((int64_t)seglen, ntok - base);
+  for (int i = threadIdx.x; i < len; i += kBlock) sid[i] = ids[base + i];
+  __syncthreads();
+  if (v >= V) return;
+  uint32_t c = 0;
+  for (int i = 0; i < len; ++i) c += sid[i] == (uint32_t)v;
+  cnt[(int64_t)blockIdx.y * V + v] = c;
+}
+
+__global__ __launch_bounds__(kBlock) void embed_seg_base_kernel(const uint32_t* __restrict__ offsets,
+                                                                uint32_t* __restrict__ cnt,
+                                                                int64_t V, int nseg) {
+  const int64_t v = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (v >= V) return;
+  uint32_t acc = offsets[v];
+  for (int sg = 0; sg < nseg; ++sg) {
+    const uint32_t c = cnt[(int64_t)sg * V + v];
+    cnt[(int64_t)sg * V + v] = acc;
+    acc += c;
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void embed_seg_place_kernel(const uint32_t* __restrict__ ids,
+                                                                 const uint32_t* __restrict__ segbase,
+                                                                 uint32_t* __restrict__ sorted_tok,
+                                                                 int64_t ntok, int64_t V, int seglen) {
+  __shared__ uint32_t sid[kPlaceChunk];
+  const int64_t v = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.y * seglen;
+  const int len = (int)min((int64_t)seglen, ntok - base);
+  for (int i = threadIdx.x; i < len; i += kBlock) sid[i] = ids[base + i];
+  __syncthreads();
+  if (v >= V) return;
+  uint32_t pos = segbase[(int64_t)blockIdx.y * V + v];
+  for (int i = 0; i < len; ++i)
+    if (sid[i] == (uint32_t)v) sorted_tok[pos++] = (uint32_t)(base + i);
+}
+
 // grad[v, :] = sum over the v-segment of the sorted token list, in token order.
 __global__ __launch_bounds__(kBlock) void embed_segsum_kernel(
     const float* __restrict__ g, const uint32_t* __restrict__ sorted_tok,
@@ -243,8 +293,27 @@ WXX_API int wxx_embeddx(const float* g, const uint32_t* ids, float* grad, int64_
                      s, ids, counts, ntok, V);
   hipLaunchKernelGGL(exclusive_scan_u32_kernel, dim3(1), dim3(kScanBlock), 0, s, counts, offsets,
                      V);
-  hipLaunchKernelGGL(embed_place_kernel, dim3((unsigned)((V + kBlock - 1) / kBlock)),
-                     dim3(kBlock), 0, s, ids, offsets, sorted_tok, ntok, V);
+  // Segments: enough (segment, id) threads to fill the chip (~64k), each
+  // segment at most kPlaceChunk tokens (one LDS stage).
+  int64_t nseg = std::max<int64_t>((ntok + kPlaceChunk - 1) / kPlaceChunk, (65536 + V - 1) / V);
+  nseg = std::min<int64_t>(std::min<int64_t>(nseg, ntok), 65535);
+  const int seglen = (int)((ntok + nseg - 1) / nseg);
+  nseg = (ntok + seglen - 1) / seglen;
+  uint32_t* segcnt = nullptr;
+  if (nseg > 1) segcnt = (uint32_t*)wxx::scratch_alloc(sizeof(uint32_t) * (size_t)(nseg * V));
+  const dim3 vblocks((unsigned)((V + kBlock - 1) / kBlock));
+  if (segcnt) {
+    const dim3 grid2(vblocks.x, (unsigned)nseg);
+    hipLaunchKernelGGL(embed_seg_count_kernel, grid2, dim3(kBlock), 0, s, ids, segcnt, ntok, V,
+                       seglen);
+    hipLaunchKernelGGL(embed_seg_base_kernel, vblocks, dim3(kBlock), 0, s, offsets, segcnt, V,
+                       (int)nseg);
+    hipLaunchKernelGGL(embed_seg_place_kernel, grid2, dim3(kBlock), 0, s, ids, segcnt, sorted_tok,
+                       ntok, V, seglen);
+  } else {
+    hipLaunchKernelGGL(embed_place_kernel, vblocks, dim3(kBlock), 0, s, ids, offsets, sorted_tok,
+                       ntok, V);
+  }
   WXX_LAUNCHED();
   const int vec = (D % 4 == 0) && ((((uintptr_t)g) | ((uintptr_t)grad)) % 16 == 0);
   const int64_t dwork = vec ? D / 4 : D;
@@ -252,6 +321,7 @@ WXX_API int wxx_embeddx(const float* g, const uint32_t* ids, float* grad, int64_
   hipLaunchKernelGGL(embed_segsum_kernel, dim3((unsigned)V, gy), dim3(kBlock), 0, s, g,
                      sorted_tok, offsets, counts, grad, D, V, vec);
   WXX_LAUNCHED();
+  if (segcnt) wxx::scratch_free(segcnt);
   wxx::scratch_free(buf);
   return WXX_OK;
 }
