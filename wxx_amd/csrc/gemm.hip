@@ -1087,8 +1087,22 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
     } else if (g.M <= 64 || g.N <= 64 || g.K <= 128) {
       // N = 64 over long M (attention's P V, dS K, P^T dO): 128 x 64 tiles
       tile = (g.N <= 64 && g.M >= 128 && g.K > 128) ? (transpose_A ? 10 : 9) : 1;
-      if (tile == 1 && t64 < 2 * cus)
+      if (nb == 1 && kmax == 1 && g.K >= 256 && 4 * t64 <= cus) {
+        // An unbatched product over at most a quarter of the CUs' worth of
+        // 64 x 64 tiles with K in [256, 2048) is latency-bound (one
+        // workgroup takes about 1.4 us per 16-deep K step): 64 x 64 tiles
+        // and up to 8 power-of-two splits of >= 64 of K, as below (measured
+        // on MI355X, ResNet18's classifier 128 x 10 x 512: 11.1 us against
+        // 44.7 us on one 128 x 64 tile; at K = 128 splitting measured
+        // slower).  Batched N <= 64 products (attention's) keep the tiles
+        // whose causal variants reproduce them bit for bit.
+        tile = 1;
+        int s = 1;
+        while (s < 8 && t64 * s * 2 <= cus && g.K / (s * 2) >= 64) s *= 2;
+        splits = s;
+      } else if (tile == 1 && t64 < 2 * cus) {
         splits = (int)std::min<int64_t>((8 * cus + t64 - 1) / t64, kmax);
+      }
     } else if (t128 >= cus) {
       tile = g.K >= 4096 ? 4 : 2;
       if (t128 < 2 * cus && g.K >= 2048) {
