@@ -245,6 +245,22 @@ int wxx_batchnormdx(const float* dy, const float* x, const float* gamma, const f
 int wxx_batchnorm_backward(const float* dy, const float* x, const float* gamma,
                            const float* saved_mean, const float* inv_std, float* dgamma,
                            float* dbeta, float* dx, int64_t B, int64_t C, int64_t HW);
+/* functional.batchnorm in training (functional/normalization.py:148-206) followed by the
+ * residual add and relu of ResNet's blocks (nn/resnet.py:31-37, 65-66): y = relu(bn(x) +
+ * residual), residual null for none, relu 0/1, one launch; the running statistics take
+ * `updates` (1 or 2) EMA updates, 2 being resnet.py:33's double bn1 evaluation.  Channels of
+ * 1..32768 elements (B*HW), else WXX_E_UNSUPPORTED. */
+int wxx_batchnorm_act(const float* x, const float* gamma, const float* beta,
+                      const float* residual, float* running_mean, float* running_var, float* y,
+                      float* saved_mean, float* inv_std, int64_t B, int64_t C, int64_t HW,
+                      float eps, float momentum, int updates, int relu);
+/* The backward of wxx_batchnorm_act (autograd/normalization.py batchnorm backward after the
+ * relu's and the add's, autograd/pointwise.py): dgamma, dbeta, dx and, exactly when the
+ * forward had a residual, dresidual; relu' is taken from the recomputed pre-activation. */
+int wxx_batchnorm_act_backward(const float* dy, const float* x, const float* gamma,
+                               const float* beta, const float* residual, const float* saved_mean,
+                               const float* inv_std, float* dgamma, float* dbeta, float* dx,
+                               float* dresidual, int64_t B, int64_t C, int64_t HW, int relu);
 
 /* ---- E: elementwise / layout -------------------------------------------- */
 /* functional.pointwise (functional/pointwise.py:29-98) and, with out == a,

@@ -493,16 +493,26 @@ def test_resnet18_config3_train_step_matches_oracle(device, monkeypatch):
     # decisions are checked on their own: each one that differs from the
     # oracle's own float64 choice must be a near-tie.
     from oracle import resnet as orn
+    from wxx_amd import functional as wf
     from wxx_amd.autograd import convolution as ac
+    from wxx_amd.autograd import normalization as an
     from wxx_amd.autograd import pointwise as ap
 
     wxx = W()
     relu_in, pool = [], {}
     relu_fwd = ap.relu.forward
+    bn_act_fwd = an.batchnorm_act.forward
 
     def recording_relu(self, t):
         relu_in.append(t.numpy())
         return relu_fwd(self, t)
+
+    def recording_bn_act(self, t, gamma, beta, res, rm, rv, updates=1, relu=True):
+        if relu:  # the same kernel without the ReLU (on copies of the running statistics)
+            pre, _, _ = wf.batchnorm_act(t, gamma, beta, res, wf.from_numpy(rm.numpy()),
+                                         wf.from_numpy(rv.numpy()), 1, False)
+            relu_in.append(pre.numpy())
+        return bn_act_fwd(self, t, gamma, beta, res, rm, rv, updates, relu)
 
     pool_fwd = ac.maxpooling2d._fwd
 
@@ -512,6 +522,7 @@ def test_resnet18_config3_train_step_matches_oracle(device, monkeypatch):
         return out, idx
 
     monkeypatch.setattr(ap.relu, "forward", recording_relu)
+    monkeypatch.setattr(an.batchnorm_act, "forward", recording_bn_act)
     monkeypatch.setattr(ac.maxpooling2d, "_fwd", staticmethod(recording_pool))
 
     model = wxx.nn.ResNet18(num_classes=10)

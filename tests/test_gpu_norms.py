@@ -143,6 +143,69 @@ def test_batchnorm(device, shape, training):
                        msg="batchnorm_backward dx")
 
 
+@pytest.mark.parametrize("shape", [(4, 3, 2, 2), (128, 64, 8, 8), (128, 512, 1, 1),
+                                   (128, 64, 16, 16), (2, 5, 7, 3)])
+@pytest.mark.parametrize("residual,relu", [(True, True), (False, True), (True, False)])
+def test_batchnorm_act_equals_composed_ops(device, shape, residual, relu):
+    # relu(batchnorm(x) + r) as one kernel, and its backward, equal the
+    # composed ops (batchnorm twice for the two running-statistic updates,
+    # the add, the ReLU, and their autograd backwards) bit for bit
+    import wxx_amd as wxx
+    from wxx_amd.nn import BatchNorm
+
+    r = rng(sum(shape) + 7 * residual + relu)
+    C = shape[1]
+    x = r.standard_normal(shape).astype(np.float32)
+    res = r.standard_normal(shape).astype(np.float32) if residual else None
+    dz = r.standard_normal(shape).astype(np.float32)
+    g = r.standard_normal(C).astype(np.float32)
+    b = r.standard_normal(C).astype(np.float32)
+    rm0 = r.standard_normal(C).astype(np.float32)
+    rv0 = (r.random(C) + 0.5).astype(np.float32)
+    outs = []
+    for fused in (True, False):
+        bn = BatchNorm(C)
+        bn.weight = wxx.Parameter(up(g))
+        bn.bias = wxx.Parameter(up(b))
+        bn.running_mean, bn.running_std = up(rm0), up(rv0)
+        tx = up(x)
+        tx.requires_grad = True
+        tr = None
+        if residual:
+            tr = up(res)
+            tr.requires_grad = True
+        if fused:
+            assert F().batchnorm_act_supported(tx)
+            z = bn.act(tx, residual=tr, relu=relu, updates=2)
+        else:
+            bn(tx)
+            z = bn(tx)
+            if residual:
+                z = z + tr
+            if relu:
+                z = z.relu()
+        (z * up(dz)).sum().backward()  # z's gradient is dz
+        outs.append([z.numpy(), bn.running_mean.numpy(), bn.running_std.numpy(), tx.grad.numpy(),
+                     bn.weight.grad.numpy(), bn.bias.grad.numpy()]
+                    + ([tr.grad.numpy()] if residual else []))
+    names = ["y", "running mean", "running var", "dx", "dgamma", "dbeta", "dresidual"]
+    for name, a, e in zip(names, *outs):
+        assert np.array_equal(a, e), name
+    # and the forward against the float64 oracle: relu(bn(x) + r)
+    ey, _, _, erm, erv = on.batchnorm(x, g, b, rm0, rv0, True)
+    ey = ey + (res if residual else 0)
+    ey = np.maximum(ey, 0) if relu else ey
+    assert_close(outs[0][0], ey, rtol=1e-5, atol=1e-5, msg="y against the oracle")
+
+
+def test_batchnorm_act_rejects_large_channels(device):
+    x = up(np.zeros((64, 3, 48, 48)))  # 147456 elements per channel
+    assert not F().batchnorm_act_supported(x)
+    one = up(np.ones(3))
+    with pytest.raises(Exception):
+        F().batchnorm_act(x, one, one, None, up(np.zeros(3)), up(np.ones(3)))
+
+
 def test_norm_parameter_size_is_validated(device):
     # gamma/beta are indexed by the reduce coordinate: a mismatch must be
     # rejected on the host, never read out of bounds on the device

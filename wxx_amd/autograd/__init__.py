@@ -13,7 +13,7 @@ from .convolution import (
     maxpooling2d,
 )
 from .layers import CrossEntropyLoss, Dropout, Embedding, FusedAttention
-from .normalization import batchnorm, meanvarnorm, rmsnorm
+from .normalization import batchnorm, batchnorm_act, meanvarnorm, rmsnorm
 from .pointwise import (
     abs,
     add,

@@ -51,3 +51,26 @@ class batchnorm(Function):
         gx, gg, gb = functional.batchnorm_backward(g, x, gamma, mean, istd)
         grads = [gx, gg, gb]
         return grads + [None] * (len(self.inputs) - 3)
+
+
+class batchnorm_act(Function):
+    """Training-mode batchnorm, + residual and ReLU as one op (built as
+    ``batchnorm_act(x, gamma, beta[, residual])``); its backward is the
+    composed ops' (batchnorm's, the add's, the ReLU's) in one kernel."""
+
+    def forward(self, tensor1, gamma, beta, residual, running_mean, running_var, updates=1,
+                relu=True):
+        out, mean, istd = functional.batchnorm_act(tensor1, gamma, beta, residual, running_mean,
+                                                   running_var, updates, relu)
+        out.requires_grad = any(t.requires_grad for t in (tensor1, gamma, beta, residual)
+                                if t is not None)
+        return self.attach(out, tensor1=tensor1, gamma=gamma, beta=beta, residual=residual,
+                           mean=mean, istd=istd, relu=relu)
+
+    def backward(self, g):
+        x, gamma, beta, r = self.tensor1, self.gamma, self.beta, self.residual
+        mean, istd = self.mean, self.istd
+        self.tensor1 = self.gamma = self.beta = self.residual = self.mean = self.istd = None
+        gx, gg, gb, gr = functional.batchnorm_act_backward(g, x, gamma, beta, r, mean, istd,
+                                                           self.relu)
+        return [gx, gg, gb, gr][:len(self.inputs)]

@@ -92,6 +92,8 @@ SIGNATURES = {
     "wxx_batchnormdg": (I32, [P, P, P, P, P, P, I64, I64, I64]),
     "wxx_batchnormdx": (I32, [P, P, P, P, P, P, P, P, I64, I64, I64]),
     "wxx_batchnorm_backward": (I32, [P, P, P, P, P, P, P, P, I64, I64, I64]),
+    "wxx_batchnorm_act": (I32, [P, P, P, P, P, P, P, P, P, I64, I64, I64, F32, F32, I32, I32]),
+    "wxx_batchnorm_act_backward": (I32, [P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I32]),
     # elementwise / layout
     "wxx_pointwise": (I32, [P, P, P, I32, P, P, P, P, I32]),
     "wxx_scalarpointwise": (I32, [P, P, I64, I32, F32, I32]),

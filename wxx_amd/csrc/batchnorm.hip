@@ -22,6 +22,19 @@ namespace {
 
 constexpr int kBlock = 256;
 
+// One running-statistic update, r <- (1 - m) r + m v, written once so every
+// kernel rounds it the same way.
+__device__ __forceinline__ float bn_ema(float r, float m, float v) {
+  return (1.f - m) * r + m * v;
+}
+
+// The normalised, scaled and shifted value (v - mu) inv g + b, with its
+// rounding fixed (one product, then one fused multiply-add) so that the
+// backward of the ReLU variant recomputes it bit for bit.
+__device__ __forceinline__ float bn_affine(float v, float mu, float is, float g, float b) {
+  return __builtin_fmaf((v - mu) * is, g, b);
+}
+
 // part[(c * splits + s) * 2 + {0,1}] = sums over this split of (a, b), where
 // (a, b) = (x, x^2) for statistics or (dy * xhat, dy) for the gradient.
 template <bool GRAD>
@@ -84,9 +97,9 @@ __global__ __launch_bounds__(kBlock) void bn_finalize_kernel(
   const float var = fmaxf(0.f, Q / mf - mu * mu);
   saved_mean[c] = mu;
   inv_std[c] = rsqrtf(var + eps);
-  running_mean[c] = (1.f - momentum) * running_mean[c] + momentum * mu;
+  running_mean[c] = bn_ema(running_mean[c], momentum, mu);
   const float unbiased = M > 1 ? var * (mf / (mf - 1.f)) : var;
-  running_var[c] = (1.f - momentum) * running_var[c] + momentum * unbiased;
+  running_var[c] = bn_ema(running_var[c], momentum, unbiased);
 }
 
 __global__ __launch_bounds__(kBlock) void bn_grad_finalize_kernel(const float* __restrict__ part,
@@ -112,7 +125,7 @@ __global__ __launch_bounds__(kBlock) void bn_apply_kernel(
   const int64_t step = (int64_t)gridDim.x * kBlock;
   for (; i < n; i += step) {
     const int64_t c = (i / HW) % Cc;
-    y[i] = (x[i] - mean[c]) * inv[c] * g[c] + b[c];
+    y[i] = bn_affine(x[i], mean[c], inv[c], g[c], b[c]);
   }
 }
 
@@ -145,12 +158,16 @@ __device__ __forceinline__ int64_t bn_index(int m, int HW, int Cc, int c) {
   return ((int64_t)bb * Cc + c) * HW + sp;
 }
 
-template <int E>
+// RES / RELU: the residual block's tail that follows a BatchNorm in
+// ResNet, y = relu(bn(x) + r), in the same launch; `updates` applies the
+// running-statistic update that many times (the reference's blocks evaluate
+// their first BatchNorm twice per forward).
+template <int E, bool RES, bool RELU>
 __global__ __launch_bounds__(1024) void bn_fused_fwd_kernel(
     const float* __restrict__ x, const float* __restrict__ g, const float* __restrict__ b,
-    float* __restrict__ running_mean, float* __restrict__ running_var, float* __restrict__ y,
-    float* __restrict__ saved_mean, float* __restrict__ inv_std, int B, int Cc, int HW, float eps,
-    float momentum) {
+    const float* __restrict__ r, float* __restrict__ running_mean,
+    float* __restrict__ running_var, float* __restrict__ y, float* __restrict__ saved_mean,
+    float* __restrict__ inv_std, int B, int Cc, int HW, float eps, float momentum, int updates) {
   __shared__ float red[16];
   const int c = blockIdx.x, T = blockDim.x;
   const int M = B * HW;
@@ -175,28 +192,44 @@ __global__ __launch_bounds__(1024) void bn_fused_fwd_kernel(
   if (threadIdx.x == 0) {
     saved_mean[c] = mu;
     inv_std[c] = is;
-    running_mean[c] = (1.f - momentum) * running_mean[c] + momentum * mu;
     const float unbiased = M > 1 ? var * (mf / (mf - 1.f)) : var;
-    running_var[c] = (1.f - momentum) * running_var[c] + momentum * unbiased;
+    float rm = running_mean[c], rv = running_var[c];
+    for (int u = 0; u < updates; ++u) {
+      rm = bn_ema(rm, momentum, mu);
+      rv = bn_ema(rv, momentum, unbiased);
+    }
+    running_mean[c] = rm;
+    running_var[c] = rv;
   }
   const float gc = g[c], bc = b[c];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int m = threadIdx.x + e * T;
-    if (m < M) y[bn_index(m, HW, Cc, c)] = (v[e] - mu) * is * gc + bc;
+    if (m < M) {
+      const int64_t i = bn_index(m, HW, Cc, c);
+      float t = bn_affine(v[e], mu, is, gc, bc);
+      if (RES) t += r[i];
+      if (RELU) t = fmaxf(0.f, t);
+      y[i] = t;
+    }
   }
 }
 
-// dgamma, dbeta and dx of one channel per workgroup (sizes as above).
-template <int E>
+// dgamma, dbeta and dx of one channel per workgroup (sizes as above).  With
+// RELU the incoming gradient is first masked by relu' of the forward's
+// pre-activation, recomputed from x (and r) exactly as the forward rounded
+// it; with RES the masked gradient is also the residual's (dr).
+template <int E, bool RES, bool RELU>
 __global__ __launch_bounds__(1024) void bn_fused_bwd_kernel(
     const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ g,
-    const float* __restrict__ mean, const float* __restrict__ inv, float* __restrict__ dg,
-    float* __restrict__ db, float* __restrict__ dx, int B, int Cc, int HW) {
+    const float* __restrict__ b, const float* __restrict__ r, const float* __restrict__ mean,
+    const float* __restrict__ inv, float* __restrict__ dg, float* __restrict__ db,
+    float* __restrict__ dx, float* __restrict__ dr, int B, int Cc, int HW) {
   __shared__ float red[16];
   const int c = blockIdx.x, T = blockDim.x;
   const int M = B * HW;
   const float mu = mean[c], is = inv[c];
+  const float gc = g[c];
   float d[E], xh[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
@@ -204,7 +237,14 @@ __global__ __launch_bounds__(1024) void bn_fused_bwd_kernel(
     const bool in = m < M;
     const int64_t i = in ? bn_index(m, HW, Cc, c) : 0;
     d[e] = in ? dy[i] : 0.f;
-    xh[e] = in ? (x[i] - mu) * is : 0.f;
+    const float xv = in ? x[i] : 0.f;
+    xh[e] = in ? (xv - mu) * is : 0.f;
+    if (RELU && in) {
+      float t = bn_affine(xv, mu, is, gc, b[c]);
+      if (RES) t += r[i];
+      d[e] = d[e] * (t > 0.f ? 1.f : 0.f);  // relu' times the gradient, as the unary backward
+    }
+    if (RES && in) dr[i] = d[e];
   }
   float s1 = 0.f, s2 = 0.f;
 #pragma unroll
@@ -219,7 +259,7 @@ __global__ __launch_bounds__(1024) void bn_fused_bwd_kernel(
     db[c] = Bs;
   }
   const float mf = (float)M;
-  const float k = g[c] * is / mf;
+  const float k = gc * is / mf;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int m = threadIdx.x + e * T;
@@ -237,6 +277,60 @@ FusedGeo fused_geo(int64_t M) {
   while ((int64_t)E * 1024 < M) E *= 2;
   const int64_t t = (M + E - 1) / E;
   return {(int)std::min<int64_t>(1024, (t + 63) / 64 * 64), E};
+}
+
+// Whether a training forward / a backward runs as one fused launch.
+bool fused_ok(int64_t B, int64_t C, int64_t HW) {
+  const int64_t M = B * HW;
+  return M > 0 && M <= kFusedMaxM && C <= 0x7fffffff && B * C * HW < (int64_t(1) << 31);
+}
+
+template <bool RES, bool RELU>
+int launch_fused_fwd(const float* x, const float* gamma, const float* beta, const float* r,
+                     float* running_mean, float* running_var, float* y, float* saved_mean,
+                     float* inv_std, int64_t B, int64_t C, int64_t HW, float eps, float momentum,
+                     int updates) {
+  const FusedGeo fg = fused_geo(B * HW);
+  const dim3 grid((unsigned)C), block((unsigned)fg.threads);
+  hipStream_t s = wxx::stream();
+#define WXX_BN_FWD(EE)                                                                        \
+  hipLaunchKernelGGL((bn_fused_fwd_kernel<EE, RES, RELU>), grid, block, 0, s, x, gamma, beta, r, \
+                     running_mean, running_var, y, saved_mean, inv_std, (int)B, (int)C, (int)HW, \
+                     eps, momentum, updates)
+  switch (fg.E) {
+    case 1: WXX_BN_FWD(1); break;
+    case 2: WXX_BN_FWD(2); break;
+    case 4: WXX_BN_FWD(4); break;
+    case 8: WXX_BN_FWD(8); break;
+    case 16: WXX_BN_FWD(16); break;
+    default: WXX_BN_FWD(32); break;
+  }
+#undef WXX_BN_FWD
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+template <bool RES, bool RELU>
+int launch_fused_bwd(const float* dy, const float* x, const float* gamma, const float* beta,
+                     const float* r, const float* saved_mean, const float* inv_std, float* dgamma,
+                     float* dbeta, float* dx, float* dr, int64_t B, int64_t C, int64_t HW) {
+  const FusedGeo fg = fused_geo(B * HW);
+  const dim3 grid((unsigned)C), block((unsigned)fg.threads);
+  hipStream_t s = wxx::stream();
+#define WXX_BN_BWD(EE)                                                                          \
+  hipLaunchKernelGGL((bn_fused_bwd_kernel<EE, RES, RELU>), grid, block, 0, s, dy, x, gamma, beta, \
+                     r, saved_mean, inv_std, dgamma, dbeta, dx, dr, (int)B, (int)C, (int)HW)
+  switch (fg.E) {
+    case 1: WXX_BN_BWD(1); break;
+    case 2: WXX_BN_BWD(2); break;
+    case 4: WXX_BN_BWD(4); break;
+    case 8: WXX_BN_BWD(8); break;
+    case 16: WXX_BN_BWD(16); break;
+    default: WXX_BN_BWD(32); break;
+  }
+#undef WXX_BN_BWD
+  WXX_LAUNCHED();
+  return WXX_OK;
 }
 
 int pick_splits(int64_t Cc, int64_t M) {
@@ -259,23 +353,9 @@ WXX_API int wxx_batchnorm(const float* x, const float* gamma, const float* beta,
   WXX_REQUIRE(B >= 0 && C >= 1 && HW >= 0, "bad batchnorm dims");
   hipStream_t s = wxx::stream();
   const int64_t M = B * HW;
-  if (training && M > 0 && M <= kFusedMaxM && C <= 0x7fffffff && B * C * HW < (int64_t(1) << 31)) {
-    const FusedGeo fg = fused_geo(M);
-    const dim3 grid((unsigned)C), block((unsigned)fg.threads);
-#define WXX_BN_FWD(EE)                                                                         \
-  hipLaunchKernelGGL(bn_fused_fwd_kernel<EE>, grid, block, 0, s, x, gamma, beta, running_mean, \
-                     running_var, y, saved_mean, inv_std, (int)B, (int)C, (int)HW, eps, momentum)
-    switch (fg.E) {
-      case 1: WXX_BN_FWD(1); break;
-      case 2: WXX_BN_FWD(2); break;
-      case 4: WXX_BN_FWD(4); break;
-      case 8: WXX_BN_FWD(8); break;
-      case 16: WXX_BN_FWD(16); break;
-      default: WXX_BN_FWD(32); break;
-    }
-#undef WXX_BN_FWD
-    WXX_LAUNCHED();
-    return WXX_OK;
+  if (training && fused_ok(B, C, HW)) {
+    return launch_fused_fwd<false, false>(x, gamma, beta, nullptr, running_mean, running_var, y,
+                                          saved_mean, inv_std, B, C, HW, eps, momentum, 1);
   }
   int splits = 1;
   float* part = nullptr;
@@ -346,27 +426,63 @@ WXX_API int wxx_batchnorm_backward(const float* dy, const float* x, const float*
   WXX_CHECK_INIT();
   WXX_REQUIRE(dy && x && gamma && saved_mean && inv_std && dgamma && dbeta && dx, "null pointer");
   WXX_REQUIRE(B >= 0 && C >= 1 && HW >= 0, "bad batchnorm dims");
-  const int64_t M = B * HW;
-  if (M > 0 && M <= kFusedMaxM && B * C * HW < (int64_t(1) << 31)) {
-    const FusedGeo fg = fused_geo(M);
-    const dim3 grid((unsigned)C), block((unsigned)fg.threads);
-    hipStream_t s = wxx::stream();
-#define WXX_BN_BWD(EE)                                                                        \
-  hipLaunchKernelGGL(bn_fused_bwd_kernel<EE>, grid, block, 0, s, dy, x, gamma, saved_mean, inv_std, \
-                     dgamma, dbeta, dx, (int)B, (int)C, (int)HW)
-    switch (fg.E) {
-      case 1: WXX_BN_BWD(1); break;
-      case 2: WXX_BN_BWD(2); break;
-      case 4: WXX_BN_BWD(4); break;
-      case 8: WXX_BN_BWD(8); break;
-      case 16: WXX_BN_BWD(16); break;
-      default: WXX_BN_BWD(32); break;
-    }
-#undef WXX_BN_BWD
-    WXX_LAUNCHED();
-    return WXX_OK;
+  if (fused_ok(B, C, HW)) {
+    return launch_fused_bwd<false, false>(dy, x, gamma, nullptr, nullptr, saved_mean, inv_std,
+                                          dgamma, dbeta, dx, nullptr, B, C, HW);
   }
   int rc = wxx_batchnormdg(dy, x, saved_mean, inv_std, dgamma, dbeta, B, C, HW);
   if (rc) return rc;
   return wxx_batchnormdx(dy, x, gamma, dgamma, dbeta, saved_mean, inv_std, dx, B, C, HW);
+}
+
+// functional.batchnorm in training (reference normalization.py:148-206)
+// followed by the residual add and ReLU of ResNet's blocks (reference
+// src/wxx/nn/resnet.py:31-37, 65-66): y = relu(bn(x) + residual), residual
+// optional, ReLU optional, in one launch, the running statistics updated
+// `updates` times (1 or 2).  Channels of at most 32768 elements (B*HW).
+WXX_API int wxx_batchnorm_act(const float* x, const float* gamma, const float* beta,
+                              const float* residual, float* running_mean, float* running_var,
+                              float* y, float* saved_mean, float* inv_std, int64_t B, int64_t C,
+                              int64_t HW, float eps, float momentum, int updates, int relu) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(x && gamma && beta && running_mean && running_var && y && saved_mean && inv_std,
+              "null pointer");
+  WXX_REQUIRE(B >= 0 && C >= 1 && HW >= 0, "bad batchnorm dims");
+  WXX_REQUIRE(updates == 1 || updates == 2, "updates must be 1 or 2, got %d", updates);
+  if (!fused_ok(B, C, HW))
+    return wxx::set_error(WXX_E_UNSUPPORTED,
+                          "batchnorm_act takes channels of 1..%lld elements, got B*HW = %lld",
+                          (long long)kFusedMaxM, (long long)(B * HW));
+#define WXX_BN_ACT(RES, RELU)                                                                 \
+  launch_fused_fwd<RES, RELU>(x, gamma, beta, residual, running_mean, running_var, y, saved_mean, \
+                              inv_std, B, C, HW, eps, momentum, updates)
+  if (residual) return relu ? WXX_BN_ACT(true, true) : WXX_BN_ACT(true, false);
+  return relu ? WXX_BN_ACT(false, true) : WXX_BN_ACT(false, false);
+#undef WXX_BN_ACT
+}
+
+// The backward of wxx_batchnorm_act (autograd's batchnorm backward,
+// reference normalization.py:209-305, after the ReLU's and the add's,
+// autograd/pointwise.py): dgamma, dbeta, dx, and the residual's gradient
+// (dresidual, needed exactly when the forward had a residual).
+WXX_API int wxx_batchnorm_act_backward(const float* dy, const float* x, const float* gamma,
+                                       const float* beta, const float* residual,
+                                       const float* saved_mean, const float* inv_std,
+                                       float* dgamma, float* dbeta, float* dx, float* dresidual,
+                                       int64_t B, int64_t C, int64_t HW, int relu) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(dy && x && gamma && beta && saved_mean && inv_std && dgamma && dbeta && dx,
+              "null pointer");
+  WXX_REQUIRE(!residual == !dresidual, "residual and dresidual go together");
+  WXX_REQUIRE(B >= 0 && C >= 1 && HW >= 0, "bad batchnorm dims");
+  if (!fused_ok(B, C, HW))
+    return wxx::set_error(WXX_E_UNSUPPORTED,
+                          "batchnorm_act takes channels of 1..%lld elements, got B*HW = %lld",
+                          (long long)kFusedMaxM, (long long)(B * HW));
+#define WXX_BN_ACT_BWD(RES, RELU)                                                             \
+  launch_fused_bwd<RES, RELU>(dy, x, gamma, beta, residual, saved_mean, inv_std, dgamma, dbeta, \
+                              dx, dresidual, B, C, HW)
+  if (residual) return relu ? WXX_BN_ACT_BWD(true, true) : WXX_BN_ACT_BWD(true, false);
+  return relu ? WXX_BN_ACT_BWD(false, true) : WXX_BN_ACT_BWD(false, false);
+#undef WXX_BN_ACT_BWD
 }

@@ -174,6 +174,76 @@ def batchnorm_backward(grad, tensor1, gamma, saved_mean, saved_std):
     return dx, dg, db
 
 
+# Channels (B * H * W elements) that batchnorm_act takes: one workgroup each.
+BN_ACT_MAX = 32768
+
+
+def batchnorm_act_supported(tensor1):
+    """Whether :func:`batchnorm_act` takes this NCHW input."""
+    if len(tensor1.shape) != 4:
+        return False
+    B, Cc, H, W = tensor1.shape
+    return 0 < B * H * W <= BN_ACT_MAX and B * Cc * H * W < 2**31
+
+
+def batchnorm_act(tensor1, gamma, beta, residual, running_mean, running_std, updates=1,
+                  relu=True):
+    """Training-mode :func:`batchnorm`, then ``+ residual`` (``None``: no add) and ReLU
+    (``relu``), in one kernel; returns ``(y, mean, inv_std)``.
+
+    The running statistics take ``updates`` (1 or 2) EMA updates, the second one
+    being the reference ResNet block's repeated ``bn1`` evaluation
+    (src/wxx/nn/resnet.py:33).  Inputs outside :func:`batchnorm_act_supported`
+    raise (callers compose batchnorm, add and relu there).
+    """
+    tensor1 = contiguous_f32(tensor1)
+    gamma = contiguous_f32(gamma, "gamma")
+    validation.check_rank(tensor1.shape, min_rank=4, max_rank=4, name="batchnorm input")
+    B, Cc, H, W = tensor1.shape
+    for t, name in ((gamma, "gamma"), (beta, "beta"), (running_mean, "running_mean"),
+                    (running_std, "running_std")):
+        _check_param(t, Cc, name)
+    if residual is not None:
+        residual = contiguous_f32(residual, "residual")
+        validation.check_same_shape(residual.shape, tensor1.shape, name="residual and input")
+    y = empty(tensor1.shape)
+    mean = empty((Cc,))
+    istd = empty((Cc,))
+    call("wxx_batchnorm_act", ptr(tensor1), ptr(gamma), ptr(beta),
+         ptr(residual) if residual is not None else None, ptr(running_mean), ptr(running_std),
+         ptr(y), ptr(mean), ptr(istd), B, Cc, H * W, BN_EPS, BN_MOMENTUM, int(updates),
+         1 if relu else 0)
+    return y, mean, istd
+
+
+def batchnorm_act_backward(grad, tensor1, gamma, beta, residual, saved_mean, saved_std,
+                           relu=True):
+    """``(dx, dgamma, dbeta, dresidual)`` of :func:`batchnorm_act` (``dresidual`` is
+    ``None`` without a residual); relu' is taken from the recomputed pre-activation."""
+    tensor1 = contiguous_f32(tensor1)
+    gamma = contiguous_f32(gamma, "gamma")
+    grad = contiguous_f32(grad, "grad")
+    validation.check_rank(tensor1.shape, min_rank=4, max_rank=4, name="batchnorm input")
+    B, Cc, H, W = tensor1.shape
+    validation.check_same_shape(grad.shape, tensor1.shape, name="grad and input")
+    for t, name in ((gamma, "gamma"), (beta, "beta"), (saved_mean, "saved_mean"),
+                    (saved_std, "saved_std")):
+        _check_param(t, Cc, name)
+    dr = None
+    if residual is not None:
+        residual = contiguous_f32(residual, "residual")
+        validation.check_same_shape(residual.shape, tensor1.shape, name="residual and input")
+        dr = empty(tensor1.shape)
+    dx = empty(tensor1.shape)
+    dg = empty((Cc,))
+    db = empty((Cc,))
+    call("wxx_batchnorm_act_backward", ptr(grad), ptr(tensor1), ptr(gamma), ptr(beta),
+         ptr(residual) if residual is not None else None, ptr(saved_mean), ptr(saved_std),
+         ptr(dg), ptr(db), ptr(dx), ptr(dr) if dr is not None else None, B, Cc, H * W,
+         1 if relu else 0)
+    return dx, dg, db, dr
+
+
 def batchnormdg(grad, tensor1, saved_mean, saved_std):
     tensor1 = contiguous_f32(tensor1)
     grad = contiguous_f32(grad, "grad")

@@ -254,6 +254,24 @@ class BatchNorm(Module):
         return op.forward(x, self.weight, self.bias, self.running_mean, self.running_std,
                           context.MODE == 0)
 
+    def act(self, x, residual=None, relu=True, updates=1):
+        """``relu(self(x) + residual)`` (add and ReLU optional) after ``updates``
+        evaluations of ``self(x)``: while recording, one fused kernel where it
+        takes the shape (the running statistics take the ``updates`` EMA steps
+        the repeated calls would), otherwise the calls themselves."""
+        recording = context.MODE == 0
+        if recording and functional.batchnorm_act_supported(x):
+            inputs = (x, self.weight, self.bias) + (() if residual is None else (residual,))
+            return autograd.batchnorm_act(*inputs).forward(
+                x, self.weight, self.bias, residual, self.running_mean, self.running_std,
+                updates, relu)
+        for _ in range(updates - 1 if recording else 0):
+            self(x)
+        out = self(x)
+        if residual is not None:
+            out = out + residual
+        return out.relu() if relu else out
+
 
 def _pair(v):
     return (v, v) if isinstance(v, int) else v

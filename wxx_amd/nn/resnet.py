@@ -27,15 +27,12 @@ class ResBlock(Module):
             self.sh = True
 
     def forward(self, x):
-        out = self.conv1(x)
         # The reference evaluates bn1 twice here (once inside its hasattr
         # test, resnet.py:33): the running statistics take two EMA updates
-        # per forward.  Kept so training matches.
-        probe = self.bn1(out)
-        out = self.bn1(out).relu() if hasattr(probe, "relu") else self.bn1(out)
-        out = self.bn2(self.conv2(out))
-        out = out + self.shortcut(x)
-        return out.relu()
+        # per forward, kept so training matches.  BatchNorm, the residual add
+        # and the ReLUs run as fused BatchNorm ops.
+        out = self.bn1.act(self.conv1(x), relu=True, updates=2)
+        return self.bn2.act(self.conv2(out), residual=self.shortcut(x), relu=True)
 
 
 class ResNet18(Module):
@@ -59,7 +56,7 @@ class ResNet18(Module):
         return Sequential(*layers)
 
     def forward(self, x):
-        out = self.maxpool(self.bn1(self.conv1(x)).relu())
+        out = self.maxpool(self.bn1.act(self.conv1(x), relu=True))
         out = self.layer4(self.layer3(self.layer2(self.layer1(out))))
         out = self.avgpool(out)
         return self.fc(out.reshape((out.shape[0], out.shape[1])))
