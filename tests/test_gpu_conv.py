@@ -81,6 +81,34 @@ def test_conv2d_resnet18_shapes(device, case):
     _run_conv(case, 100 + RESNET18.index(case), True)
 
 
+# Kernels that reach past the input on every output: only their live taps
+# run (the others read nothing but padding); dW is zero at the dead taps.
+DEAD_TAPS = [
+    (3, 6, 1, 1, 5, 3, 3, (1, 1), (1, 1), (1, 1)),    # 1 x 1 map: the centre tap only
+    (2, 4, 2, 2, 3, 3, 3, (2, 2), (1, 1), (1, 1)),    # 2 x 2 -> 1 x 1: taps 1..2
+    (2, 3, 1, 3, 4, 5, 3, (1, 1), (2, 1), (1, 1)),    # rows pruned, columns kept
+    (1, 2, 2, 1, 3, 3, 5, (1, 2), (1, 2), (1, 1)),    # W = 1: column taps 2 only
+    (2, 3, 1, 1, 2, 3, 3, (1, 1), (2, 2), (2, 2)),    # dilation 2, padding 2: tap 1
+    (2, 5, 1, 2, 3, 4, 2, (1, 1), (2, 0), (1, 1)),    # even kernel, taps 2..2
+]
+
+
+@pytest.mark.parametrize("case", DEAD_TAPS)
+def test_conv2d_dead_taps(device, case):
+    _run_conv(case, 200 + DEAD_TAPS.index(case), True)
+    B, Cin, H, W, Cout, KH, KW, s, p, d = case
+    r = rng(300 + DEAD_TAPS.index(case))
+    X = r.standard_normal((B, Cin, H, W)).astype(np.float32)
+    Ho = (H + 2 * p[0] - d[0] * (KH - 1) - 1) // s[0] + 1
+    Wo = (W + 2 * p[1] - d[1] * (KW - 1) - 1) // s[1] + 1
+    g = r.standard_normal((B, Cout, Ho, Wo)).astype(np.float32)
+    dw = F().conv2ddw(up(g), up(X), s, p, d, X.shape, (Cout, Cin, KH, KW)).numpy()
+    ew = oc.conv2ddw(g, X, s, p, d, (Cout, Cin, KH, KW))
+    dead = np.all(ew == 0, axis=(0, 1))  # taps no output reaches the input through
+    assert dead.any()
+    assert np.all(dw[:, :, dead] == 0)
+
+
 def test_conv2d_strided_input_view(device):
     X = rng(3).standard_normal((2, 5, 6, 3)).astype(np.float32)  # NHWC on the host
     Wt = rng(4).standard_normal((4, 3, 3, 3)).astype(np.float32)

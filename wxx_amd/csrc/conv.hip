@@ -109,8 +109,16 @@ struct OpWords {
 // forward's P).  Otherwise (case 0: a kernel whose tap count does not divide
 // the chunk) the non-slot operands are KX rows whose k digits are stepped on
 // the scalar unit per row.
-template <int MODE, int BK, bool PXK, bool QXK, bool SLOTS>
-__global__ __launch_bounds__(256, 2) void conv_lds_kernel(ConvArgs a) {
+//
+// KS: groups of 4 waves per workgroup that share the tile and split its K
+// range chunk by chunk (group g takes chunks g, g + KS, ...; a group past
+// the end multiplies a chunk of zeros, so every group passes the same
+// barriers), each with its own LDS stages; at the end the groups' sums are
+// added in group order.  KS = 2 gives a launch of at most one workgroup per
+// CU two waves per SIMD, so one wave's loads and barrier waits overlap the
+// other's matrix work.
+template <int MODE, int BK, bool PXK, bool QXK, bool SLOTS, int KS>
+__global__ __launch_bounds__(256 * KS, 2) void conv_lds_kernel(ConvArgs a) {
   using OP = OpWords<BK, PXK>;
   using OQ = OpWords<BK, QXK>;
   constexpr int kRowsPerWave = BK / 4;
@@ -120,15 +128,21 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(ConvArgs a) {
   static_assert(QS || !QXK, "an XK operand is always slots");
   // separate objects per stage, so the compiler can tell the writes into one
   // stage from the reads of the other
-  __shared__ float P0[OP::kWords], P1[OP::kWords];
-  __shared__ float Q0[OQ::kWords], Q1[OQ::kWords];
+  __shared__ float P0s[KS][OP::kWords], P1s[KS][OP::kWords];
+  __shared__ float Q0s[KS][OQ::kWords], Q1s[KS][OQ::kWords];
+  __shared__ float xch[KS > 1 ? 16 * 256 : 1];  // the other groups' sums
   __shared__ SlotX xtab[2][kTile];
   __shared__ SlotC ctab[2][BK];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) & 3);  // wave of its group
+  const int grp = KS > 1 ? __builtin_amdgcn_readfirstlane(tid >> 8) : 0;
   const int wi = wave >> 1, wj = wave & 1;
+  float* const P0 = P0s[grp];
+  float* const P1 = P1s[grp];
+  float* const Q0 = Q0s[grp];
+  float* const Q1 = Q1s[grp];
 
   const int tile = blockIdx.x;
   const int ti = tile / a.tiles_j, tj = tile - (tile / a.tiles_j) * a.tiles_j;
@@ -137,6 +151,8 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(ConvArgs a) {
   const int kbeg = z * a.kps;
   const int kend = min(a.K, kbeg + a.kps);
   const int nk = (kend - kbeg + BK - 1) / BK;
+  const int nks = (nk + KS - 1) / KS;  // steps: chunks per group
+  const int kg = kbeg + grp * BK;      // this group's first chunk
 
   const int R1 = conv_r1(MODE, a), R2 = conv_r2(MODE, a);
   const int R12 = R1 * R2;
@@ -144,10 +160,10 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(ConvArgs a) {
 
   // ---- slots: row entries of the tile and column entries of a chunk, then
   //      each of the wave's loads from one of each -----------------------------
-  if (wave == 0) {
+  if (grp == 0 && wave == 0) {
     xtab[0][lane] = slot_x<MODE, true>(a, i0 + lane);
     xtab[1][lane] = slot_x<MODE, false>(a, j0 + lane);
-  } else if (wave == 1 && lane < BK) {
+  } else if (grp == 0 && wave == 1 && lane < BK) {
     ctab[0][lane] = slot_c<MODE, true>(a, lane, BK);
     ctab[1][lane] = slot_c<MODE, false>(a, lane, BK);
   }
@@ -179,7 +195,7 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(ConvArgs a) {
 #pragma unroll
     for (int n = 0; n < OQ::kPerWave; ++n) qsl[n] = make(1, QXK, n);
   }
-  XkUniform xu = xk_uniform(MODE, a, kbeg);
+  XkUniform xu = xk_uniform(MODE, a, kg);
 
   // ---- case 0: KX rows with scalar digits -----------------------------------
   const KxCol pcol = kx_col<MODE, true>(a, i0 + lane);
@@ -188,7 +204,7 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(ConvArgs a) {
   KDigits base;
   int n0 = 0, n1 = 0, n2 = 0;
   if constexpr (!PS || !QS) {
-    const int k = kbeg + kRowsPerWave * wave;
+    const int k = kg + kRowsPerWave * wave;
     base.t0 = fdiv(k, a.dR12);
     const int r = k - base.t0 * R12;
     base.t1 = fdiv(r, a.dR2);
@@ -205,7 +221,7 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(ConvArgs a) {
   // commit).
   float pr[kDepth][OP::kPerWave], qr[kDepth][OQ::kPerWave];
   auto issue = [&](int c, float* prs, float* qrs) __attribute__((always_inline)) {
-    const int kbase = kbeg + c * BK;
+    const int kbase = kbeg + (c * KS + grp) * BK;
     const int rem = kend - kbase;
     const int lim = rem >= BK ? kDeadSlot : rem;  // only a split's last chunk is partial
     if constexpr (PS) {
@@ -243,9 +259,13 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(ConvArgs a) {
         }
         kd_step1(d, R1, R2);
       }
-      kd_add(base, n0, n1, n2, R1, R2);
+#pragma unroll
+      for (int g = 0; g < KS; ++g) kd_add(base, n0, n1, n2, R1, R2);
     }
-    if constexpr (PS || QS) xk_advance(MODE, a, xu, BK);
+    if constexpr (PS || QS) {
+#pragma unroll
+      for (int g = 0; g < KS; ++g) xk_advance(MODE, a, xu, BK);
+    }
   };
 
   floatx16 acc;
@@ -293,20 +313,33 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(ConvArgs a) {
       __attribute__((always_inline)) {
     __builtin_amdgcn_s_waitcnt(kLgkmOnly);
     WXX_S_BARRIER();
-    if (c + kDepth < nk) issue(c + kDepth, pr[rs], qr[rs]);
+    if (c + kDepth < nks) issue(c + kDepth, pr[rs], qr[rs]);
     compute(ps, qs);
-    if (c + 1 < nk) commit(pr[rs1], qr[rs1], ps1, qs1);
+    if (c + 1 < nks) commit(pr[rs1], qr[rs1], ps1, qs1);
   };
 #pragma unroll
   for (int c = 0; c < kDepth; ++c)
-    if (c < nk) issue(c, pr[c], qr[c]);
-  if (nk > 0) commit(pr[0], qr[0], P0, Q0);
+    if (c < nks) issue(c, pr[c], qr[c]);
+  if (nks > 0) commit(pr[0], qr[0], P0, Q0);
   static_assert(kDepth == 4, "the step loop below is unrolled for 4 register sets");
-  for (int c = 0; c < nk; c += 4) {
+  for (int c = 0; c < nks; c += 4) {
     step(c, 0, 1, P0, Q0, P1, Q1);
-    if (c + 1 < nk) step(c + 1, 1, 2, P1, Q1, P0, Q0);
-    if (c + 2 < nk) step(c + 2, 2, 3, P0, Q0, P1, Q1);
-    if (c + 3 < nk) step(c + 3, 3, 0, P1, Q1, P0, Q0);
+    if (c + 1 < nks) step(c + 1, 1, 2, P1, Q1, P0, Q0);
+    if (c + 2 < nks) step(c + 2, 2, 3, P0, Q0, P1, Q1);
+    if (c + 3 < nks) step(c + 3, 3, 0, P1, Q1, P0, Q0);
+  }
+  if constexpr (KS > 1) {
+    // group 1 hands its sums to group 0 (the same lane and register of the
+    // same wave of the tile), which adds them after its own
+    static_assert(KS == 2, "the groups' sums are exchanged pairwise");
+    if (grp == 1) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) xch[r * 256 + wave * 64 + lane] = acc[r];
+    }
+    __syncthreads();
+    if (grp == 1) return;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] += xch[r * 256 + wave * 64 + lane];
   }
 
   // ---- epilogue: D[i][j] of a 32x32 tile is in lane j + 32 ((i/4)%2),
@@ -397,6 +430,12 @@ int launch(ConvArgs& a, float* final_out) {
       }
     }
   }
+  // Two groups of waves per workgroup when the launch leaves CUs without a
+  // second workgroup and each workgroup has a long K range (measured on
+  // MI355X: ResNet18's layer1 forward 25.1 -> 23.8 us, the stem's weight
+  // gradient 28.1 -> 26.1 us; short ranges lose to the groups' exchange).
+  const int64_t chunks_per_split = ((a.K + splits - 1) / splits + BK - 1) / BK;
+  const int ks = tiles * splits <= cus && chunks_per_split >= 8 ? 2 : 1;
   int kps = (a.K + splits - 1) / splits;
   kps = (kps + BK - 1) / BK * BK;
   splits = (a.K + kps - 1) / kps;
@@ -412,8 +451,11 @@ int launch(ConvArgs& a, float* final_out) {
   } else {
     a.out = final_out;
   }
-  hipLaunchKernelGGL((conv_lds_kernel<MODE, BK, PXK, QXK, SLOTS>), dim3((unsigned)tiles, (unsigned)splits),
-                     dim3(256), 0, s, a);
+  const dim3 grid((unsigned)tiles, (unsigned)splits);
+  if (ks == 2)
+    hipLaunchKernelGGL((conv_lds_kernel<MODE, BK, PXK, QXK, SLOTS, 2>), grid, dim3(512), 0, s, a);
+  else
+    hipLaunchKernelGGL((conv_lds_kernel<MODE, BK, PXK, QXK, SLOTS, 1>), grid, dim3(256), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e == hipSuccess && splits > 1) {
     const int64_t n = (int64_t)a.I * a.J;
@@ -487,8 +529,105 @@ const float* zero_word() {
   return ptr[dev];
 }
 
+// Copies between a weight-shaped tensor [outer][KH][KW] and its window of
+// taps [outer][KHe][KWe] starting at (kh0, kw0): into the window
+// (expand == 0), or back out of it with zeros at the other taps.
+__global__ __launch_bounds__(256) void conv_tap_window_kernel(const float* __restrict__ src,
+                                                              float* __restrict__ dst,
+                                                              int64_t outer, int KH, int KW,
+                                                              int kh0, int kw0, int KHe, int KWe,
+                                                              int expand) {
+  const int64_t n = outer * (expand ? KH * KW : KHe * KWe);
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n;
+       e += (int64_t)gridDim.x * 256) {
+    if (expand) {
+      const int64_t o = e / (KH * KW);
+      const int t = (int)(e - o * KH * KW), kh = t / KW - kh0, kw = t % KW - kw0;
+      dst[e] = kh >= 0 && kh < KHe && kw >= 0 && kw < KWe ? src[(o * KHe + kh) * KWe + kw] : 0.f;
+    } else {
+      const int64_t o = e / (KHe * KWe);
+      const int t = (int)(e - o * KHe * KWe), kh = t / KWe + kh0, kw = t % KWe + kw0;
+      dst[e] = src[(o * KH + kh) * KW + kw];
+    }
+  }
+}
+
+// [lo, hi): the taps along one axis that read at least one input element for
+// some output position (input index o s - p + k d in [0, n_in) for some o in
+// [0, n_out)); the taps outside only ever read padding.
+void live_taps(int K, int n_in, int n_out, int s, int p, int d, int& lo, int& hi) {
+  lo = K;
+  hi = 0;
+  for (int k = 0; k < K; ++k) {
+    const int c = k * d - p;  // input index of output 0
+    const int o = c >= 0 ? 0 : (-c + s - 1) / s;
+    if (o < n_out && o * s + c < n_in) {
+      lo = std::min(lo, k);
+      hi = k + 1;
+    }
+  }
+}
+
+template <int MODE>
+int dispatch_all_taps(ConvArgs& a, float* final_out);
+
+// A convolution whose kernel reaches past the input on every output (ResNet's
+// 3x3 convolutions on 1 x 1 and 2 x 2 maps) runs on its live taps only: the
+// others multiply nothing but padding, so dropping them leaves every sum's
+// terms the same but for zeros.  The weight window is copied out for the
+// forward / dX (the padding shrinks by the dropped leading taps), and the
+// weight gradient of the window is expanded back with zeros at the dead taps.
 template <int MODE>
 int dispatch(ConvArgs& a, float* final_out) {
+  int kh0, kh1, kw0, kw1;
+  live_taps(a.KH, a.H, a.Ho, a.sh, a.ph, a.dh, kh0, kh1);
+  live_taps(a.KW, a.W, a.Wo, a.sw, a.pw, a.dw, kw0, kw1);
+  // Worth the window's copy when at most a third of the taps live (a half
+  // for dX, whose strided gathers gain more): measured on MI355X, ResNet18's
+  // 3x3 convolutions on 1 x 1 maps (1 of 9 taps) forward 20.1 -> 14.3 us and
+  // dX 21.6 -> 16.0 us; its stride-2 2 x 2 -> 1 x 1 one (4 of 9) dX 32.5 ->
+  // 25.2 us but forward 15.3 -> 17.4 us.
+  const int live = (kh1 - kh0) * (kw1 - kw0);
+  const bool prune = kh1 > kh0 && kw1 > kw0 && kh0 * a.dh <= a.ph && kw0 * a.dw <= a.pw &&
+                     (MODE == kDx ? 2 * live <= a.KH * a.KW : 3 * live <= a.KH * a.KW);
+  if (!prune) return dispatch_all_taps<MODE>(a, final_out);
+  const int KHe = kh1 - kh0, KWe = kw1 - kw0;
+  const int64_t outer = (int64_t)a.Cout * a.Cin;
+  const int64_t nwin = outer * KHe * KWe;
+  float* win = (float*)wxx::scratch_alloc(sizeof(float) * (size_t)nwin);
+  if (!win) return wxx::set_error(WXX_E_OOM, "conv weight window");
+  ConvArgs b = a;
+  b.KH = KHe;
+  b.KW = KWe;
+  b.ph = a.ph - kh0 * a.dh;
+  b.pw = a.pw - kw0 * a.dw;
+  hipStream_t s = wxx::stream();
+  int rc = WXX_OK;
+  if (MODE != kDw) {
+    hipLaunchKernelGGL(conv_tap_window_kernel, dim3(wxx::grid_1d(nwin, 256, 4096)), dim3(256), 0,
+                       s, a.P, win, outer, a.KH, a.KW, kh0, kw0, KHe, KWe, 0);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) rc = wxx::set_error(WXX_E_HIP, "conv weight window: %s", hipGetErrorString(e));
+    b.P = win;
+    b.K = (MODE == kFwd ? a.Cin : a.Cout) * KHe * KWe;
+    if (rc == WXX_OK) rc = dispatch_all_taps<MODE>(b, final_out);
+  } else {
+    b.J = a.Cin * KHe * KWe;
+    rc = dispatch_all_taps<MODE>(b, win);
+    if (rc == WXX_OK) {
+      const int64_t n = outer * a.KH * a.KW;
+      hipLaunchKernelGGL(conv_tap_window_kernel, dim3(wxx::grid_1d(n, 256, 4096)), dim3(256), 0, s,
+                         win, final_out, outer, a.KH, a.KW, kh0, kw0, KHe, KWe, 1);
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess) rc = wxx::set_error(WXX_E_HIP, "conv weight window: %s", hipGetErrorString(e));
+    }
+  }
+  wxx::scratch_free(win);
+  return rc;
+}
+
+template <int MODE>
+int dispatch_all_taps(ConvArgs& a, float* final_out) {
   const int R2 = conv_r2(MODE, a), R12 = conv_r1(MODE, a) * R2;
   // chunks of whole input channels of 3x3 taps for the forward and dX
   const int bk = (MODE != kDw && R12 == 9) ? 36 : 32;
