@@ -241,15 +241,15 @@ int wxx_batchnormdx(const float* dy, const float* x, const float* gamma, const f
                     float* dx, int64_t B, int64_t C, int64_t HW);
 /* functional.batchnormdg then functional.batchnormdx (functional/normalization.py:209-305),
  * as autograd's batchnorm backward calls them (autograd/normalization.py): dgamma, dbeta
- * and dx in one call (one launch while B*HW <= 32768) */
+ * and dx in one call (one launch while B*HW <= 8192, two above) */
 int wxx_batchnorm_backward(const float* dy, const float* x, const float* gamma,
                            const float* saved_mean, const float* inv_std, float* dgamma,
                            float* dbeta, float* dx, int64_t B, int64_t C, int64_t HW);
 /* functional.batchnorm in training (functional/normalization.py:148-206) followed by the
  * residual add and relu of ResNet's blocks (nn/resnet.py:31-37, 65-66): y = relu(bn(x) +
- * residual), residual null for none, relu 0/1, one launch; the running statistics take
- * `updates` (1 or 2) EMA updates, 2 being resnet.py:33's double bn1 evaluation.  Channels of
- * 1..32768 elements (B*HW), else WXX_E_UNSUPPORTED. */
+ * residual), residual null for none, relu 0/1 (one launch while B*HW <= 8192, two above);
+ * the running statistics take `updates` (1 or 2) EMA updates, 2 being resnet.py:33's double
+ * bn1 evaluation.  B*HW >= 1 and B*C*HW < 2^31, else WXX_E_UNSUPPORTED. */
 int wxx_batchnorm_act(const float* x, const float* gamma, const float* beta,
                       const float* residual, float* running_mean, float* running_var, float* y,
                       float* saved_mean, float* inv_std, int64_t B, int64_t C, int64_t HW,

@@ -144,14 +144,16 @@ __global__ __launch_bounds__(kBlock) void bn_dx_kernel(
   }
 }
 
-// Channels of at most kFusedMaxM elements (every BatchNorm of ResNet18 at
-// batch 128 on 32x32 images) run as one workgroup of up to 1024 threads per
-// channel that holds the channel in registers (E elements per thread, all
-// loads issued at once), takes the statistics and writes the output in one
-// launch: the split path's three launches (partials, finalize, apply) cost
-// more in latency than their extra parallelism gains on these sizes.  Same
-// formulas, the sums in another (fixed) order.
-constexpr int64_t kFusedMaxM = 32768;
+// Channels of at most kFusedMaxM elements (ResNet18's BatchNorms at batch
+// 128 on 32x32 images but the stem's) run as one workgroup of up to 1024
+// threads per channel that holds the channel in registers (E elements per
+// thread, all loads issued at once), takes the statistics and writes the
+// output in one launch: more launches cost more in latency than their extra
+// parallelism gains on these sizes.  Same formulas, the sums in another
+// (fixed) order.  (At 32768 elements, 32 per thread, the ReLU backward ran
+// out of registers and one workgroup per channel left most CUs idle: 136 us
+// against ~10 us for the two-launch split path.)
+constexpr int64_t kFusedMaxM = 8192;
 
 __device__ __forceinline__ int64_t bn_index(int m, int HW, int Cc, int c) {
   const int bb = m / HW, sp = m - bb * HW;
@@ -267,6 +269,160 @@ __global__ __launch_bounds__(1024) void bn_fused_bwd_kernel(
   }
 }
 
+// Larger channels (training): a (channel, split) grid of partial sums, then
+// a second launch over the same grid in which every workgroup adds its
+// channel's partials itself (all in the same fixed order, so they agree bit
+// for bit), the channel's first workgroup stores the statistics, and each
+// normalises its own split: two launches at the whole chip's width where one
+// workgroup per channel would leave most CUs idle (ResNet18's stem: 64
+// channels of 32768) and run out of registers.
+
+// The channel's two sums from its partials: lane l of wave 0 adds splits l,
+// l + 64, ... in order, then a butterfly over the wave; every thread gets
+// the result.
+__device__ __forceinline__ float2 bn_channel_sums(const float* __restrict__ part, int64_t c,
+                                                  int splits, float* red) {
+  if (threadIdx.x < 64) {
+    float a = 0.f, b = 0.f;
+    for (int s = threadIdx.x; s < splits; s += 64) {
+      a += part[(c * splits + s) * 2 + 0];
+      b += part[(c * splits + s) * 2 + 1];
+    }
+    a = wxx::warp_sum(a);
+    b = wxx::warp_sum(b);
+    if (threadIdx.x == 0) {
+      red[0] = a;
+      red[1] = b;
+    }
+  }
+  __syncthreads();
+  return make_float2(red[0], red[1]);
+}
+
+__device__ __forceinline__ void bn_split_range(int64_t M, int splits, int s, int64_t& m0,
+                                               int64_t& m1) {
+  const int64_t seg = (M + splits - 1) / splits;
+  m0 = s * seg;
+  m1 = m0 + seg < M ? m0 + seg : M;
+}
+
+template <bool RES, bool RELU>
+__global__ __launch_bounds__(kBlock) void bn_split_apply_kernel(
+    const float* __restrict__ x, const float* __restrict__ g, const float* __restrict__ b,
+    const float* __restrict__ r, const float* __restrict__ part, float* __restrict__ running_mean,
+    float* __restrict__ running_var, float* __restrict__ y, float* __restrict__ saved_mean,
+    float* __restrict__ inv_std, int64_t B, int64_t Cc, int64_t HW, int splits, float eps,
+    float momentum, int updates) {
+  __shared__ float red[2];
+  const int64_t c = blockIdx.x;
+  const int s = blockIdx.y;
+  const float2 t = bn_channel_sums(part, c, splits, red);
+  const int64_t M = B * HW;
+  const float mf = (float)M;
+  const float mu = t.x / mf;
+  const float var = fmaxf(0.f, t.y / mf - mu * mu);
+  const float is = rsqrtf(var + eps);
+  if (s == 0 && threadIdx.x == 0) {
+    saved_mean[c] = mu;
+    inv_std[c] = is;
+    const float unbiased = M > 1 ? var * (mf / (mf - 1.f)) : var;
+    float rm = running_mean[c], rv = running_var[c];
+    for (int u = 0; u < updates; ++u) {
+      rm = bn_ema(rm, momentum, mu);
+      rv = bn_ema(rv, momentum, unbiased);
+    }
+    running_mean[c] = rm;
+    running_var[c] = rv;
+  }
+  const float gc = g[c], bc = b[c];
+  int64_t m0, m1;
+  bn_split_range(M, splits, s, m0, m1);
+  for (int64_t m = m0 + threadIdx.x; m < m1; m += kBlock) {
+    const int64_t bb = m / HW, sp = m - bb * HW;
+    const int64_t idx = (bb * Cc + c) * HW + sp;
+    float v = bn_affine(x[idx], mu, is, gc, bc);
+    if (RES) v += r[idx];
+    if (RELU) v = fmaxf(0.f, v);
+    y[idx] = v;
+  }
+}
+
+// The gradient's partial sums (dy xhat, dy), dy masked by relu' of the
+// recomputed pre-activation for RELU.
+template <bool RES, bool RELU>
+__global__ __launch_bounds__(kBlock) void bn_split_grad_partial_kernel(
+    const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ g,
+    const float* __restrict__ b, const float* __restrict__ r, const float* __restrict__ mean,
+    const float* __restrict__ inv, float* __restrict__ part, int64_t B, int64_t Cc, int64_t HW,
+    int splits) {
+  __shared__ float red[4];
+  const int64_t c = blockIdx.x;
+  const int s = blockIdx.y;
+  const int64_t M = B * HW;
+  const float mu = mean[c], is = inv[c];
+  const float gc = g[c], bc = RELU ? b[c] : 0.f;
+  int64_t m0, m1;
+  bn_split_range(M, splits, s, m0, m1);
+  float a = 0.f, sd = 0.f;
+  for (int64_t m = m0 + threadIdx.x; m < m1; m += kBlock) {
+    const int64_t bb = m / HW, sp = m - bb * HW;
+    const int64_t idx = (bb * Cc + c) * HW + sp;
+    const float xv = x[idx];
+    float d = dy[idx];
+    if (RELU) {
+      float t = bn_affine(xv, mu, is, gc, bc);
+      if (RES) t += r[idx];
+      d = d * (t > 0.f ? 1.f : 0.f);
+    }
+    a += d * ((xv - mu) * is);
+    sd += d;
+  }
+  a = wxx::block_sum(a, red);
+  sd = wxx::block_sum(sd, red);
+  if (threadIdx.x == 0) {
+    part[(c * splits + s) * 2 + 0] = a;
+    part[(c * splits + s) * 2 + 1] = sd;
+  }
+}
+
+template <bool RES, bool RELU>
+__global__ __launch_bounds__(kBlock) void bn_split_dx_kernel(
+    const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ g,
+    const float* __restrict__ b, const float* __restrict__ r, const float* __restrict__ mean,
+    const float* __restrict__ inv, const float* __restrict__ part, float* __restrict__ dg,
+    float* __restrict__ db, float* __restrict__ dx, float* __restrict__ dr, int64_t B, int64_t Cc,
+    int64_t HW, int splits) {
+  __shared__ float red[2];
+  const int64_t c = blockIdx.x;
+  const int s = blockIdx.y;
+  const float2 t = bn_channel_sums(part, c, splits, red);
+  const float A = t.x, Bs = t.y;
+  if (s == 0 && threadIdx.x == 0) {
+    dg[c] = A;
+    db[c] = Bs;
+  }
+  const int64_t M = B * HW;
+  const float mf = (float)M;
+  const float mu = mean[c], is = inv[c];
+  const float gc = g[c], bc = RELU ? b[c] : 0.f;
+  const float k = gc * is / mf;
+  int64_t m0, m1;
+  bn_split_range(M, splits, s, m0, m1);
+  for (int64_t m = m0 + threadIdx.x; m < m1; m += kBlock) {
+    const int64_t bb = m / HW, sp = m - bb * HW;
+    const int64_t idx = (bb * Cc + c) * HW + sp;
+    const float xv = x[idx];
+    float d = dy[idx];
+    if (RELU) {
+      float tt = bn_affine(xv, mu, is, gc, bc);
+      if (RES) tt += r[idx];
+      d = d * (tt > 0.f ? 1.f : 0.f);
+    }
+    if (RES) dr[idx] = d;
+    dx[idx] = k * (mf * d - Bs - ((xv - mu) * is) * A);
+  }
+}
+
 // Threads per channel (a multiple of 64, at most 1024) and elements per
 // thread E for a channel of M <= kFusedMaxM elements.
 struct FusedGeo {
@@ -340,6 +496,50 @@ int pick_splits(int64_t Cc, int64_t M) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(s, 1024));
 }
 
+// Training forward / backward of channels above kFusedMaxM: two launches
+// each (partial sums, then sums + elementwise pass).
+bool split_ok(int64_t B, int64_t C, int64_t HW) {
+  return B * HW > 0 && C <= 0x7fffffff && B * C * HW < (int64_t(1) << 31);
+}
+
+template <bool RES, bool RELU>
+int launch_split_fwd(const float* x, const float* gamma, const float* beta, const float* r,
+                     float* running_mean, float* running_var, float* y, float* saved_mean,
+                     float* inv_std, int64_t B, int64_t C, int64_t HW, float eps, float momentum,
+                     int updates) {
+  hipStream_t s = wxx::stream();
+  const int splits = pick_splits(C, B * HW);
+  float* part = (float*)wxx::scratch_alloc(sizeof(float) * 2 * C * splits);
+  if (!part) return wxx::set_error(WXX_E_OOM, "batchnorm partials");
+  const dim3 grid((unsigned)C, splits);
+  hipLaunchKernelGGL(bn_partial_kernel<false>, grid, dim3(kBlock), 0, s, x, nullptr, nullptr,
+                     nullptr, part, B, C, HW, splits);
+  hipLaunchKernelGGL((bn_split_apply_kernel<RES, RELU>), grid, dim3(kBlock), 0, s, x, gamma, beta,
+                     r, part, running_mean, running_var, y, saved_mean, inv_std, B, C, HW, splits,
+                     eps, momentum, updates);
+  wxx::scratch_free(part);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+template <bool RES, bool RELU>
+int launch_split_bwd(const float* dy, const float* x, const float* gamma, const float* beta,
+                     const float* r, const float* saved_mean, const float* inv_std, float* dgamma,
+                     float* dbeta, float* dx, float* dr, int64_t B, int64_t C, int64_t HW) {
+  hipStream_t s = wxx::stream();
+  const int splits = pick_splits(C, B * HW);
+  float* part = (float*)wxx::scratch_alloc(sizeof(float) * 2 * C * splits);
+  if (!part) return wxx::set_error(WXX_E_OOM, "batchnorm partials");
+  const dim3 grid((unsigned)C, splits);
+  hipLaunchKernelGGL((bn_split_grad_partial_kernel<RES, RELU>), grid, dim3(kBlock), 0, s, dy, x,
+                     gamma, beta, r, saved_mean, inv_std, part, B, C, HW, splits);
+  hipLaunchKernelGGL((bn_split_dx_kernel<RES, RELU>), grid, dim3(kBlock), 0, s, dy, x, gamma, beta,
+                     r, saved_mean, inv_std, part, dgamma, dbeta, dx, dr, B, C, HW, splits);
+  wxx::scratch_free(part);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
 }  // namespace
 
 // Replaces functional.batchnorm (reference src/wxx/functional/normalization.py:148-206).
@@ -355,6 +555,10 @@ WXX_API int wxx_batchnorm(const float* x, const float* gamma, const float* beta,
   const int64_t M = B * HW;
   if (training && fused_ok(B, C, HW)) {
     return launch_fused_fwd<false, false>(x, gamma, beta, nullptr, running_mean, running_var, y,
+                                          saved_mean, inv_std, B, C, HW, eps, momentum, 1);
+  }
+  if (training && split_ok(B, C, HW)) {
+    return launch_split_fwd<false, false>(x, gamma, beta, nullptr, running_mean, running_var, y,
                                           saved_mean, inv_std, B, C, HW, eps, momentum, 1);
   }
   int splits = 1;
@@ -430,6 +634,10 @@ WXX_API int wxx_batchnorm_backward(const float* dy, const float* x, const float*
     return launch_fused_bwd<false, false>(dy, x, gamma, nullptr, nullptr, saved_mean, inv_std,
                                           dgamma, dbeta, dx, nullptr, B, C, HW);
   }
+  if (split_ok(B, C, HW)) {
+    return launch_split_bwd<false, false>(dy, x, gamma, nullptr, nullptr, saved_mean, inv_std,
+                                          dgamma, dbeta, dx, nullptr, B, C, HW);
+  }
   int rc = wxx_batchnormdg(dy, x, saved_mean, inv_std, dgamma, dbeta, B, C, HW);
   if (rc) return rc;
   return wxx_batchnormdx(dy, x, gamma, dgamma, dbeta, saved_mean, inv_std, dx, B, C, HW);
@@ -438,8 +646,8 @@ WXX_API int wxx_batchnorm_backward(const float* dy, const float* x, const float*
 // functional.batchnorm in training (reference normalization.py:148-206)
 // followed by the residual add and ReLU of ResNet's blocks (reference
 // src/wxx/nn/resnet.py:31-37, 65-66): y = relu(bn(x) + residual), residual
-// optional, ReLU optional, in one launch, the running statistics updated
-// `updates` times (1 or 2).  Channels of at most 32768 elements (B*HW).
+// optional, ReLU optional, the running statistics updated `updates` times (1
+// or 2); one launch for channels of at most kFusedMaxM elements, two above.
 WXX_API int wxx_batchnorm_act(const float* x, const float* gamma, const float* beta,
                               const float* residual, float* running_mean, float* running_var,
                               float* y, float* saved_mean, float* inv_std, int64_t B, int64_t C,
@@ -449,13 +657,16 @@ WXX_API int wxx_batchnorm_act(const float* x, const float* gamma, const float* b
               "null pointer");
   WXX_REQUIRE(B >= 0 && C >= 1 && HW >= 0, "bad batchnorm dims");
   WXX_REQUIRE(updates == 1 || updates == 2, "updates must be 1 or 2, got %d", updates);
-  if (!fused_ok(B, C, HW))
+  if (!split_ok(B, C, HW))
     return wxx::set_error(WXX_E_UNSUPPORTED,
-                          "batchnorm_act takes channels of 1..%lld elements, got B*HW = %lld",
-                          (long long)kFusedMaxM, (long long)(B * HW));
-#define WXX_BN_ACT(RES, RELU)                                                                 \
-  launch_fused_fwd<RES, RELU>(x, gamma, beta, residual, running_mean, running_var, y, saved_mean, \
-                              inv_std, B, C, HW, eps, momentum, updates)
+                          "batchnorm_act needs 1 <= B*HW and B*C*HW < 2^31, got B*HW = %lld, "
+                          "B*C*HW = %lld", (long long)(B * HW), (long long)(B * C * HW));
+  const bool one = fused_ok(B, C, HW);
+#define WXX_BN_ACT(RES, RELU)                                                                  \
+  (one ? launch_fused_fwd<RES, RELU>(x, gamma, beta, residual, running_mean, running_var, y,     \
+                                     saved_mean, inv_std, B, C, HW, eps, momentum, updates)     \
+       : launch_split_fwd<RES, RELU>(x, gamma, beta, residual, running_mean, running_var, y,     \
+                                     saved_mean, inv_std, B, C, HW, eps, momentum, updates))
   if (residual) return relu ? WXX_BN_ACT(true, true) : WXX_BN_ACT(true, false);
   return relu ? WXX_BN_ACT(false, true) : WXX_BN_ACT(false, false);
 #undef WXX_BN_ACT
@@ -475,13 +686,16 @@ WXX_API int wxx_batchnorm_act_backward(const float* dy, const float* x, const fl
               "null pointer");
   WXX_REQUIRE(!residual == !dresidual, "residual and dresidual go together");
   WXX_REQUIRE(B >= 0 && C >= 1 && HW >= 0, "bad batchnorm dims");
-  if (!fused_ok(B, C, HW))
+  if (!split_ok(B, C, HW))
     return wxx::set_error(WXX_E_UNSUPPORTED,
-                          "batchnorm_act takes channels of 1..%lld elements, got B*HW = %lld",
-                          (long long)kFusedMaxM, (long long)(B * HW));
-#define WXX_BN_ACT_BWD(RES, RELU)                                                             \
-  launch_fused_bwd<RES, RELU>(dy, x, gamma, beta, residual, saved_mean, inv_std, dgamma, dbeta, \
-                              dx, dresidual, B, C, HW)
+                          "batchnorm_act needs 1 <= B*HW and B*C*HW < 2^31, got B*HW = %lld, "
+                          "B*C*HW = %lld", (long long)(B * HW), (long long)(B * C * HW));
+  const bool one = fused_ok(B, C, HW);
+#define WXX_BN_ACT_BWD(RES, RELU)                                                              \
+  (one ? launch_fused_bwd<RES, RELU>(dy, x, gamma, beta, residual, saved_mean, inv_std, dgamma, \
+                                     dbeta, dx, dresidual, B, C, HW)                           \
+       : launch_split_bwd<RES, RELU>(dy, x, gamma, beta, residual, saved_mean, inv_std, dgamma, \
+                                     dbeta, dx, dresidual, B, C, HW))
   if (residual) return relu ? WXX_BN_ACT_BWD(true, true) : WXX_BN_ACT_BWD(true, false);
   return relu ? WXX_BN_ACT_BWD(false, true) : WXX_BN_ACT_BWD(false, false);
 #undef WXX_BN_ACT_BWD

@@ -174,16 +174,13 @@ def batchnorm_backward(grad, tensor1, gamma, saved_mean, saved_std):
     return dx, dg, db
 
 
-# Channels (B * H * W elements) that batchnorm_act takes: one workgroup each.
-BN_ACT_MAX = 32768
-
-
 def batchnorm_act_supported(tensor1):
-    """Whether :func:`batchnorm_act` takes this NCHW input."""
+    """Whether :func:`batchnorm_act` takes this NCHW input (non-empty channels,
+    32-bit element indices)."""
     if len(tensor1.shape) != 4:
         return False
     B, Cc, H, W = tensor1.shape
-    return 0 < B * H * W <= BN_ACT_MAX and B * Cc * H * W < 2**31
+    return 0 < B * H * W and B * Cc * H * W < 2**31
 
 
 def batchnorm_act(tensor1, gamma, beta, residual, running_mean, running_std, updates=1,
