@@ -144,10 +144,18 @@ __global__ __launch_bounds__(kBlock) void embed_seg_base_kernel(const uint32_t* 
   const int64_t v = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   if (v >= V) return;
   uint32_t acc = offsets[v];
-  for (int sg = 0; sg < nseg; ++sg) {
-    const uint32_t c = cnt[(int64_t)sg * V + v];
-    cnt[(int64_t)sg * V + v] = acc;
-    acc += c;
+  // eight segments' counts loaded before any is overwritten (one round trip
+  // per eight instead of per segment)
+  constexpr int kU = 8;
+  for (int sg0 = 0; sg0 < nseg; sg0 += kU) {
+    uint32_t c[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) c[u] = sg0 + u < nseg ? cnt[(int64_t)(sg0 + u) * V + v] : 0u;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      if (sg0 + u < nseg) cnt[(int64_t)(sg0 + u) * V + v] = acc;
+      acc += c[u];
+    }
   }
 }
 
@@ -294,8 +302,12 @@ WXX_API int wxx_embeddx(const float* g, const uint32_t* ids, float* grad, int64_
   hipLaunchKernelGGL(exclusive_scan_u32_kernel, dim3(1), dim3(kScanBlock), 0, s, counts, offsets,
                      V);
   // Segments: enough (segment, id) threads to fill the chip (~64k), each
-  // segment at most kPlaceChunk tokens (one LDS stage).
+  // segment at most kPlaceChunk tokens (one LDS stage) and, below that, at
+  // least 256 tokens (GPT-2 config 1's 512 tokens: 2 segments, not 64 / 512
+  // whose serial bases cost 16-29 us).
   int64_t nseg = std::max<int64_t>((ntok + kPlaceChunk - 1) / kPlaceChunk, (65536 + V - 1) / V);
+  nseg = std::min<int64_t>(nseg, std::max<int64_t>((ntok + kPlaceChunk - 1) / kPlaceChunk,
+                                                   ntok / 256));
   nseg = std::min<int64_t>(std::min<int64_t>(nseg, ntok), 65535);
   const int seglen = (int)((ntok + nseg - 1) / nseg);
   nseg = (ntok + seglen - 1) / seglen;
