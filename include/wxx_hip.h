@@ -83,11 +83,11 @@ int wxx_graph_capturing(int* on);
 /* ---- A: GEMM — functional.matmul_add (functional/utils.py:378-499) +
  *      shaders/matmul.wgsl.  sA/sB = batch strides (0 = unbatched);
  *      bias_mode 0 none, 1 (N,), 2 (M,N), 3 (batch,M,N); tile 0 = auto, else a
- *      tile code (1-14) plus 256 x the number of K splits; tiles 11 / 12 /
- *      13 / 14 (128 x 128 / 128 x 192 / 128 x 64 / 128 x 64 with three LDS
- *      buffers; operand tiles loaded straight into LDS) need M a multiple of
- *      128, N of the tile width, K a multiple of 32 and 16-byte aligned
- *      operands, else the call fails. ---- */
+ *      tile code (1-15) plus 256 x the number of K splits; tiles 11 / 12 /
+ *      13 / 14 / 15 (128 x 128 / 128 x 192 / 128 x 64 / 128 x 64 with three
+ *      LDS buffers / 64 x 64 with three buffers; operand tiles loaded straight
+ *      into LDS) need M a multiple of the tile height, N of its width, K a
+ *      multiple of 32 and 16-byte aligned operands, else the call fails. ---- */
 int wxx_matmul_add(const float* A, const float* B, const float* bias, float* C, int64_t M,
                    int64_t N, int64_t K, int64_t batch, int64_t sA, int64_t sB, int64_t sBias,
                    int bias_mode, int transpose_A, int transpose_B, int tile);

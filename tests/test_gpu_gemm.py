@@ -155,7 +155,7 @@ def test_matmul_every_tile_code(device, code, splits, ta, tb):
         check(out.numpy(), A, B, bias, ta, tb)
 
 
-@pytest.mark.parametrize("code", [11, 12, 13, 14])
+@pytest.mark.parametrize("code", [11, 12, 13, 14, 15])
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
 @pytest.mark.parametrize("batch,M,N,K,splits,bias_mode", [
     (1, 128, 256, 96, 1, 1),
@@ -165,9 +165,9 @@ def test_matmul_every_tile_code(device, code, splits, ta, tb):
 def test_matmul_direct_to_lds(device, code, ta, tb, batch, M, N, K, splits, bias_mode):
     # tiles 11 / 12 / 13: 128 x 128 / 128 x 192 / 128 x 64 operand tiles
     # loaded straight into LDS in swizzled layouts (14: 128 x 64 with three
-    # buffers, two chunks of loads in flight); only for M a multiple of
-    # 128, N of the tile width, and whole 32-deep K chunks (N scaled to 192 /
-    # 384 for tile 12)
+    # buffers, two chunks of loads in flight; 15: 64 x 64 with three
+    # buffers); only for M a multiple of the tile height, N of its width,
+    # and whole 32-deep K chunks (N scaled to 192 / 384 for tile 12)
     import ctypes as C
 
     from wxx_amd.backend import lib
@@ -225,6 +225,9 @@ def test_matmul_direct_to_lds_rejects_edge_tiles(device):
     with pytest.raises(lib.HIPError, match="tile 14"):
         lib.call("wxx_matmul_add", P(A.data_ptr()), P(B.data_ptr()), None, P(out.data_ptr()),
                  130, 128, 64, 1, 0, 0, 0, 0, 0, 0, 14)
+    with pytest.raises(lib.HIPError, match="tile 15"):
+        lib.call("wxx_matmul_add", P(A.data_ptr()), P(B.data_ptr()), None, P(out.data_ptr()),
+                 130, 128, 64, 1, 0, 0, 0, 0, 0, 0, 15)
 
 
 def test_matmul_three_buffer_tiles_equal_two_buffer_tiles(device):

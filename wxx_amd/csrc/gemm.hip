@@ -455,11 +455,13 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
 // Step s = 4t + r of a chunk feeds the MFMA's K lanes k = 8t + r (lanes
 // 0-31) and k = 8t + 4 + r (lanes 32-63), so a k-contiguous fragment is one
 // ds_read_b128 per 4 steps.
-template <bool TA, bool TB, int BN, int NB = 2>
+template <bool TA, bool TB, int BN, int NB = 2, int BM = 128>
 __global__ __launch_bounds__(256, 2) void gemm_f32_dtl_kernel(GemmArgs g) {
-  static_assert(BN == 64 || BN == 128 || BN == 192, "direct-to-LDS tiles are 128 x 64/128/192");
+  static_assert(BN == 64 || BN == 128 || BN == 192, "direct-to-LDS tiles are 64/128 x 64/128/192");
+  static_assert(BM == 128 || (BM == 64 && BN == 64), "64-row tiles are 64 x 64");
   static_assert(NB == 2 || NB == 3, "two or three LDS buffers");
-  constexpr int BM = 128, BK = 32, WM = 64, WN = BN / 2, TM = 2, TN = WN / 32;
+  constexpr int BK = 32, WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
+  constexpr int RA = BM * BK / 256 / 4;  // 1 KiB regions of the A tile per wave
   constexpr int RB = BN * BK / 256 / 4;  // 1 KiB regions of the B tile per wave
   __shared__ __attribute__((aligned(16))) float As0[BM * BK];
   __shared__ __attribute__((aligned(16))) float As1[BM * BK];
@@ -490,14 +492,15 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_dtl_kernel(GemmArgs g) {
   // the kernel, whose lambdas capture the array.
   const float* pa[4];
   const float* pb[6];
-  static_assert(RB <= 6, "B regions per wave");
+  static_assert(RA <= 4 && RB <= 6, "A / B regions per wave");
+  constexpr int kRowLanes = BM / 4;  // m-contiguous A: lanes per k row of a region
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int R = 4 * wave + j;
+  for (int j = 0; j < RA; ++j) {
+    const int R = RA * wave + j;
     const int r = 8 * R + (lane >> 3);                // k-contiguous: tile row
     const int q = (lane & 7) ^ ((r >> 1) & 7);        // logical quad of slot lane & 7
-    const int kr = 2 * R + (lane >> 5);               // m-contiguous: k row
-    pa[j] = TA ? A + (kbeg + kr) * g.lda + m0 + 4 * (lane & 31)
+    const int kr = (256 / BM) * R + lane / kRowLanes;  // m-contiguous: k row
+    pa[j] = TA ? A + (kbeg + kr) * g.lda + m0 + 4 * (lane % kRowLanes)
                : A + (m0 + r) * g.lda + kbeg + 4 * q;
   }
 #pragma unroll
@@ -522,11 +525,11 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_dtl_kernel(GemmArgs g) {
     float* as = bt == 2 ? As2 : (bt == 1 ? As1 : As0);
     float* bs = bt == 2 ? Bs2 : (bt == 1 ? Bs1 : Bs0);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < RA; ++j) {
       if constexpr (NB == 3)
-        WXX_LDS_DMA_DWORDX4(pa[j] + kc * a_step, as + (4 * wave + j) * 256);
+        WXX_LDS_DMA_DWORDX4(pa[j] + kc * a_step, as + (RA * wave + j) * 256);
       else
-        __builtin_amdgcn_global_load_lds(pa[j] + kc * a_step, as + (4 * wave + j) * 256, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(pa[j] + kc * a_step, as + (RA * wave + j) * 256, 16, 0, 0);
     }
 #pragma unroll
     for (int j = 0; j < RB; ++j) {
@@ -606,7 +609,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_dtl_kernel(GemmArgs g) {
     // of chunk c + 1 are outstanding (loads complete in order), a bare
     // barrier publishes chunk c and frees the buffer of chunk c - 1, which
     // then receives chunk c + 2
-    constexpr int kPer = 4 + RB;  // loads per wave per chunk
+    constexpr int kPer = RA + RB;  // loads per wave per chunk
     constexpr int kWaitNext = 0x0F70 | (kPer & 15) | ((kPer >> 4) << 14);
     auto step = [&](int64_t kc, auto cur, auto nxt2) {
       if (kc + 1 < nk)
@@ -786,20 +789,21 @@ int launch_tiles(GemmArgs& g, int64_t batch, bool ta, bool tb, int splits) {
   dim3 grid((unsigned)((int64_t)g.tiles_m * g.tiles_n * batch), 1, (unsigned)splits);
   hipStream_t s = wxx::stream();
   if constexpr (DTL) {
-    static_assert(BM == 128 && (BN == 64 || BN == 128 || BN == 192) && BK == 32,
-                  "direct-to-LDS tiles are 128 x 64/128/192 x 32");
+    static_assert((BM == 128 && (BN == 64 || BN == 128 || BN == 192) || BM == 64 && BN == 64) &&
+                      BK == 32,
+                  "direct-to-LDS tiles are 128 x 64/128/192 or 64 x 64, x 32");
     // 128 x 192: 4 KiB of dynamic LDS on top of the tiles' 80 KiB, so that
     // one workgroup occupies a CU (the grids it is chosen for are <= 1 per CU)
     const unsigned dyn = BN == 192 ? 4096u : 0u;
     constexpr int NB = NBUF == 3 ? 3 : 2;
     if (!ta && !tb)
-      hipLaunchKernelGGL((gemm_f32_dtl_kernel<false, false, BN, NB>), grid, dim3(256), dyn, s, g);
+      hipLaunchKernelGGL((gemm_f32_dtl_kernel<false, false, BN, NB, BM>), grid, dim3(256), dyn, s, g);
     else if (!ta && tb)
-      hipLaunchKernelGGL((gemm_f32_dtl_kernel<false, true, BN, NB>), grid, dim3(256), dyn, s, g);
+      hipLaunchKernelGGL((gemm_f32_dtl_kernel<false, true, BN, NB, BM>), grid, dim3(256), dyn, s, g);
     else if (ta && !tb)
-      hipLaunchKernelGGL((gemm_f32_dtl_kernel<true, false, BN, NB>), grid, dim3(256), dyn, s, g);
+      hipLaunchKernelGGL((gemm_f32_dtl_kernel<true, false, BN, NB, BM>), grid, dim3(256), dyn, s, g);
     else
-      hipLaunchKernelGGL((gemm_f32_dtl_kernel<true, true, BN, NB>), grid, dim3(256), dyn, s, g);
+      hipLaunchKernelGGL((gemm_f32_dtl_kernel<true, true, BN, NB, BM>), grid, dim3(256), dyn, s, g);
   } else {
     if (!ta && !tb)
       hipLaunchKernelGGL((gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, false, NBUF, TRI>),
@@ -827,7 +831,7 @@ inline bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 // tile: 0 = choose automatically, 1 = 64x64, 2 = 128x128, 3 = 256x128; 4-10 select
 // alternative tile / K-chunk / buffering shapes of the same kernel; 11 / 12 / 13 the
 // direct-to-LDS 128x128 / 128x192 / 128x64 kernel, 14 its 128x64 tiles with
-// three LDS buffers.  With an
+// three LDS buffers, 15 its 64x64 tiles with three buffers.  With an
 // explicit tile code, bits 8-15 give the number of K splits (0 or 1: none).
 namespace {
 int matmul_impl(const float* A, const float* B, const float* bias, float* C, int64_t M, int64_t N,
@@ -980,6 +984,8 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
                          tri == 0;
   const bool dtl64_ok = g.vec_ok && g.M % 128 == 0 && g.N % 64 == 0 && K > 0 && K % 32 == 0 &&
                         tri == 0;
+  const bool dtl6464_ok = g.vec_ok && g.M % 64 == 0 && g.N % 64 == 0 && K > 0 && K % 32 == 0 &&
+                          tri == 0;
 
   if (K == 0) {
     // Empty contraction: C = bias (or 0).  Reuse the kernel with K = 0: the
@@ -1070,12 +1076,37 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
         }
       }
     }
+    // 64 x 64 direct-to-LDS tiles (three buffers) where the 128 x 64 ones
+    // make less than one round: up to 8 power-of-two K splits of >= 256
+    // within one round, by the same balance (measured on MI355X: 1024^3 on
+    // 256 unsplit tiles 24.6 against 29.8 us on two K splits of 128 x 64;
+    // 1024 x 1024 x 2048 44.0 against 48.4 us; 512 x 512 x 4096 as 64 tiles
+    // x 4 splits 28.6 against 43.2 us).
+    const int64_t t6464 = dtl6464_ok && !thin ? (g.M / 64) * (g.N / 64) * nb : 0;
+    int s6464 = 0;
+    double bal6464 = 0.0;
+    if (t6464 > 0 && t64d < cus) {
+      for (int sp = 1; sp <= 8; sp *= 2) {
+        if (sp > 1 && g.K / sp < 256) break;
+        const int64_t units = t6464 * sp;
+        if (units > cus) break;
+        const double bal = (double)units / (double)cus /
+                           (sp > 1 ? 1.0 + (double)(sp + 1) * 52.0 / (double)g.K : 1.0);
+        if (bal > bal6464 + 1e-9) {
+          bal6464 = bal;
+          s6464 = sp;
+        }
+      }
+    }
     if (t192 > 0 && t192 <= cus && bal192 >= 0.9 && bal192 > best) {
       tile = 12;
       splits = 1;
     } else if (t64d >= cus && t64d <= 4 * cus && bal64 >= 0.95 && bal64 > best) {
       tile = 13;
       splits = 1;
+    } else if (s6464 > 0 && bal6464 >= 0.8 && bal6464 >= bal64s && bal6464 > best) {
+      tile = 15;
+      splits = s6464;
     } else if (s64 > 0 && bal64s >= 0.8 && bal64s > best) {
       // three buffers: one round of one workgroup per CU has nothing else
       // to hide its load latency behind (1024^3: 29.5 against 30.2 us)
@@ -1191,6 +1222,11 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
                   "16-byte aligned operands");
       return launch_cfg<128, 64, 32, 64, 32, 3, false, true>(g, nb, transpose_A, transpose_B,
                                                              splits);
+    case 15:
+      WXX_REQUIRE(dtl6464_ok, "tile 15 needs M, N multiples of 64, K of 32 and 16-byte aligned "
+                  "operands");
+      return launch_cfg<64, 64, 32, 32, 32, 3, false, true>(g, nb, transpose_A, transpose_B,
+                                                            splits);
     default: return wxx::set_error(WXX_E_ARG, "bad tile %d", tile);
   }
 }
