@@ -222,3 +222,37 @@ def test_decay_window(device):
     g = rng(7).standard_normal((64, L)).astype(np.float32)
     d = F().decay_window_backward(up(g), up(decay), 2, L).numpy()
     assert_close(d, ol.decay_window_backward(g, decay, 2, L), rtol=1e-4, atol=1e-4)
+
+
+# ------------------------------------------------------------------- SwiGLU
+
+
+@pytest.mark.parametrize("T,d,hid", [(256, 128, 170), (512, 256, 682), (128, 128, 128 + 1)])
+def test_swiglu_padded_matches_composed(device, T, d, hid):
+    # the SwiGLU op with its hidden width padded to a multiple of 128 (zero
+    # weight columns / rows) against the composed ops (Linear, silu, product,
+    # Linear) on the same weights: output and every gradient
+    import wxx_amd as wxx
+    from wxx_amd import nn
+
+    r = rng(T + hid)
+    x = (r.standard_normal((2, T // 2, d)) * 0.5).astype(np.float32)
+    g = r.standard_normal((2, T // 2, d)).astype(np.float32)
+    m = nn.SwiGLU(d, hidden_dim=hid)
+    outs = []
+    for padded in (True, False):
+        for lin in (m.w1, m.w2, m.w3):
+            lin.weight.grad = None
+        tx = up(x)
+        tx.requires_grad = True
+        if padded:
+            y = m(tx)
+            assert y.creator is not None and type(y.creator).__name__ == "swiglu_padded"
+        else:
+            y = m.w3(m.w1(tx).silu() * m.w2(tx))
+        (y * up(g)).sum().backward()
+        outs.append([y.numpy(), tx.grad.numpy()] + [lin.weight.grad.numpy()
+                                                     for lin in (m.w1, m.w2, m.w3)])
+    for name, a, e in zip(["y", "dx", "dw1", "dw2", "dw3"], *outs):
+        assert a.shape == e.shape, name
+        assert_close(a, e, rtol=1e-4, atol=2e-5 * np.sqrt(max(d, hid)), msg=name)

@@ -12,7 +12,7 @@ from .convolution import (
     maxpooling1d,
     maxpooling2d,
 )
-from .layers import CrossEntropyLoss, Dropout, Embedding, FusedAttention
+from .layers import CrossEntropyLoss, Dropout, Embedding, FusedAttention, swiglu_padded
 from .normalization import batchnorm, batchnorm_act, meanvarnorm, rmsnorm
 from .pointwise import (
     abs,

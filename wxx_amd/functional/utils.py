@@ -212,13 +212,15 @@ def contiguous(tensor1):
     return out
 
 
-def matmul_add(tensor1, tensor2, tensor3, transpose_A=False, transpose_B=False, tri=0):
+def matmul_add(tensor1, tensor2, tensor3, transpose_A=False, transpose_B=False, tri=0,
+               tile=0):
     """Batched ``op(A) @ op(B) (+ bias)`` over the last two dimensions.
 
     ``tri`` (no bias) marks causal-attention structure whose zero triangle
     the kernel skips, with the same result: 1 the square output is only
     needed on and below the diagonal (zeros above), 2 ``op(A)`` is square
-    lower triangular, 3 ``op(A)`` is square upper triangular.
+    lower triangular, 3 ``op(A)`` is square upper triangular.  ``tile`` is
+    the kernel's tile code (0: its own choice; see ``wxx_matmul_add``).
     """
     validation.check_rank(tensor1.shape, min_rank=2, name="matmul left operand")
     validation.check_rank(tensor2.shape, min_rank=2, name="matmul right operand")
@@ -295,7 +297,7 @@ def matmul_add(tensor1, tensor2, tensor3, transpose_A=False, transpose_B=False, 
         bias_mode,
         1 if transpose_A else 0,
         1 if transpose_B else 0,
-        0,
+        int(tile),
     )
     return out
 
