@@ -541,18 +541,19 @@ __global__ __launch_bounds__(256) void conv_tap_window_kernel(const float* __res
                                                               int64_t outer, int KH, int KW,
                                                               int kh0, int kw0, int KHe, int KWe,
                                                               int expand) {
-  const int64_t n = outer * (expand ? KH * KW : KHe * KWe);
-  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n;
-       e += (int64_t)gridDim.x * 256) {
-    if (expand) {
-      const int64_t o = e / (KH * KW);
-      const int t = (int)(e - o * KH * KW), kh = t / KW - kh0, kw = t % KW - kw0;
-      dst[e] = kh >= 0 && kh < KHe && kw >= 0 && kw < KWe ? src[(o * KHe + kh) * KWe + kw] : 0.f;
-    } else {
-      const int64_t o = e / (KHe * KWe);
-      const int t = (int)(e - o * KHe * KWe), kh = t / KWe + kh0, kw = t % KWe + kw0;
-      dst[e] = src[(o * KH + kh) * KW + kw];
-    }
+  // one element per thread, 32-bit index arithmetic (weights are < 2^31
+  // elements, checked by setup())
+  const int n = (int)(outer * (expand ? KH * KW : KHe * KWe));
+  const int e = (int)blockIdx.x * 256 + (int)threadIdx.x;
+  if (e >= n) return;
+  if (expand) {
+    const int o = e / (KH * KW);
+    const int t = e - o * KH * KW, kh = t / KW - kh0, kw = t % KW - kw0;
+    dst[e] = kh >= 0 && kh < KHe && kw >= 0 && kw < KWe ? src[(o * KHe + kh) * KWe + kw] : 0.f;
+  } else {
+    const int o = e / (KHe * KWe);
+    const int t = e - o * KHe * KWe, kh = t / KWe + kh0, kw = t % KWe + kw0;
+    dst[e] = src[(o * KH + kh) * KW + kw];
   }
 }
 
@@ -608,8 +609,8 @@ int dispatch(ConvArgs& a, float* final_out) {
   hipStream_t s = wxx::stream();
   int rc = WXX_OK;
   if (MODE != kDw) {
-    hipLaunchKernelGGL(conv_tap_window_kernel, dim3(wxx::grid_1d(nwin, 256, 4096)), dim3(256), 0,
-                       s, a.P, win, outer, a.KH, a.KW, kh0, kw0, KHe, KWe, 0);
+    hipLaunchKernelGGL(conv_tap_window_kernel, dim3(wxx::grid_1d(nwin, 256, int64_t(1) << 23)),
+                       dim3(256), 0, s, a.P, win, outer, a.KH, a.KW, kh0, kw0, KHe, KWe, 0);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) rc = wxx::set_error(WXX_E_HIP, "conv weight window: %s", hipGetErrorString(e));
     b.P = win;
@@ -620,8 +621,9 @@ int dispatch(ConvArgs& a, float* final_out) {
     rc = dispatch_all_taps<MODE>(b, win);
     if (rc == WXX_OK) {
       const int64_t n = outer * a.KH * a.KW;
-      hipLaunchKernelGGL(conv_tap_window_kernel, dim3(wxx::grid_1d(n, 256, 4096)), dim3(256), 0, s,
-                         win, final_out, outer, a.KH, a.KW, kh0, kw0, KHe, KWe, 1);
+      hipLaunchKernelGGL(conv_tap_window_kernel, dim3(wxx::grid_1d(n, 256, int64_t(1) << 23)),
+                         dim3(256), 0, s, win, final_out, outer, a.KH, a.KW, kh0, kw0, KHe, KWe,
+                         1);
       hipError_t e = hipGetLastError();
       if (e != hipSuccess) rc = wxx::set_error(WXX_E_HIP, "conv weight window: %s", hipGetErrorString(e));
     }
