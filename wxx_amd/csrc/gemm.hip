@@ -1036,16 +1036,14 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
     }
     // 128 x 192 direct-to-LDS tiles, unsplit, when they make one round of at
     // most one tile per CU that balances better (8192 x 768: 256 tiles, where
-    // 128 x 128 makes 384, or needs split-K partials to balance), and only for
-    // the shapes where they measured faster on MI355X (GPT-2 small): a
-    // k-contiguous B (one ds_read_b128 per 4 MFMA steps; an n-contiguous B
-    // reads 4x as many LDS words singly) with K >= 2048 (8192x768x3072:
-    // 321 us against 388 us on two K splits), or K >= 16384, where the
-    // 128 x 128 alternative adds 16 splits' partials (8192x768x50304: 4.99
-    // against 5.19 ms).  At K = 768 the 128 x 64 tiles stay faster
-    // (100-101 us against 107-108 us), as do the split 128 x 128 tiles for
-    // an n-contiguous B at K = 3072 (318 us against 340 us).
-    const int64_t t192 = dtl192_ok && !thin && ((transpose_B && g.K >= 2048) || g.K >= 16384)
+    // 128 x 128 makes 384, or needs split-K partials to balance), and only
+    // where they measured faster on MI355X (GPT-2 small): K >= 16384, where
+    // the 128 x 128 alternative adds 16 splits' partials (8192x768x50304:
+    // 4.99 against 5.19 ms).  Below that the 128 x 64 tiles (three per CU)
+    // are faster, also for a k-contiguous B (8192x768x3072: 303 against 310
+    // us, 8192x768x2304: 230 against 239 us; at K = 768 100-101 against
+    // 107-108 us).
+    const int64_t t192 = dtl192_ok && !thin && g.K >= 16384
                              ? (g.M / 128) * (g.N / 192) * nb
                              : 0;
     const double bal192 = (double)t192 / (double)cus;
@@ -1102,6 +1100,12 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
       tile = 12;
       splits = 1;
     } else if (t64d >= cus && t64d <= 4 * cus && bal64 >= 0.95 && bal64 > best) {
+      tile = 13;
+      splits = 1;
+    } else if (t64d > 4 * cus && g.K <= 1024 && bal64 >= 0.95 && best < 0.95) {
+      // many rounds of short-K products that 128 x 128 tiles balance
+      // poorly (GPT-2 small's q/k/v projection, 8192 x 2304 x 768: 4.5
+      // rounds of 128 x 128, 237 against 255 us on 128 x 64 tiles)
       tile = 13;
       splits = 1;
     } else if (s6464 > 0 && bal6464 >= 0.8 && bal6464 >= bal64s && bal6464 > best) {
