@@ -275,6 +275,14 @@ int wxx_unary(const float* x, float* y, int64_t n, int op);
 /* f'(x) * g for the activation backwards of autograd/pointwise.py:291-388
  * (derivative kernel + pointwise multiply in one pass); op = derivative code */
 int wxx_unary_backward(const float* x, const float* g, float* y, int64_t n, int op);
+/* SwiGLU's gate h = silu(a) * b (nn/module.py:541-552, Tensor.silu = sigmoid(x) * x at
+ * Tensor.py:724-727) in one pass, each operation rounded as the sigmoid and product kernels
+ * it replaces round it */
+int wxx_swiglu_gate(const float* a, const float* b, float* h, int64_t n);
+/* its backward: da, db from dh, a, b in one pass (the mul, mul and sigmoid backwards of
+ * autograd/pointwise.py and the gradient sum they replace, same roundings) */
+int wxx_swiglu_gate_backward(const float* dh, const float* a, const float* b, float* da,
+                             float* db, int64_t n);
 /* dst (dense over shape) = src (strides s_src, 0 = broadcast) * scale: the
  * ones_like * grad products of sum/mean backward (autograd/reductions.py:38-95) */
 int wxx_broadcast_scale(float* dst, const float* src, int rank, const int64_t* shape,

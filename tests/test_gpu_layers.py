@@ -256,3 +256,26 @@ def test_swiglu_padded_matches_composed(device, T, d, hid):
     for name, a, e in zip(["y", "dx", "dw1", "dw2", "dw3"], *outs):
         assert a.shape == e.shape, name
         assert_close(a, e, rtol=1e-4, atol=2e-5 * np.sqrt(max(d, hid)), msg=name)
+
+
+@pytest.mark.parametrize("n", [1, 7, 4096, 65536 * 3 + 5])
+def test_swiglu_gate_bit_exact_against_composed_ops(device, n):
+    # silu(a) * b and its backward in one kernel each: the same roundings as
+    # the sigmoid, product, product-backward and sigmoid-backward kernels
+    r = rng(n)
+    a = (r.standard_normal(n) * 4).astype(np.float32)
+    a[: min(n, 3)] = [100.0, -100.0, 0.0][: min(n, 3)]  # the sigmoid's clamp and zero
+    b = r.standard_normal(n).astype(np.float32)
+    dh = r.standard_normal(n).astype(np.float32)
+    ta, tb, tdh = up(a), up(b), up(dh)
+    s = F().unary(ta, "sigmoid")
+    g = F().pointwise(s, ta, 2)
+    h = F().pointwise(g, tb, 2)
+    assert np.array_equal(F().swiglu_gate(ta, tb).numpy(), h.numpy())
+    db = F().pointwise(tdh, g, 2)
+    dg = F().pointwise(tdh, tb, 2)
+    da = F().pointwise(F().pointwise(dg, s, 2),
+                       F().unary_backward(s, F().pointwise(dg, ta, 2), "sigmoid"), 0)
+    gda, gdb = F().swiglu_gate_backward(tdh, ta, tb)
+    assert np.array_equal(gda.numpy(), da.numpy())
+    assert np.array_equal(gdb.numpy(), db.numpy())

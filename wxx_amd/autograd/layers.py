@@ -96,8 +96,9 @@ class swiglu_padded(Function):
     every product runs on the direct-to-LDS tiles (a width like Hyena's 682
     is neither a multiple of 64 nor 16-byte aligned per row).  Built as
     ``swiglu_padded(x, w1, w2, w3)``; the parameters and their gradients keep
-    their (d, hidden) / (hidden, d) shapes.  silu(a) = sigmoid(a) a, with the
-    gradient the composed ops' (the product rule over sigmoid's output)."""
+    their (d, hidden) / (hidden, d) shapes.  The gate silu(a) b and its
+    backward are one kernel each (``swiglu_gate``), equal bit for bit to the
+    composed sigmoid / product ops and their backwards."""
 
     # tile codes measured on MI355X for T = 65536, d = 256, hp = 768:
     # 128 x 64 direct-to-LDS tiles for the T-row products (x w1: 247 against
@@ -120,19 +121,16 @@ class swiglu_padded(Function):
         t = self.ROWS_TILE if _aligned(x2) else 0
         a = functional.matmul_add(x2, w1p, None, tile=t)
         b = functional.matmul_add(x2, w2p, None, tile=t)
-        s = functional.unary(a, "sigmoid")
-        g = functional.pointwise(s, a, 2)
-        h = functional.pointwise(g, b, 2)
+        h = functional.swiglu_gate(a, b)
         y = functional.matmul_add(h, w3p, None, tile=t)
         out = functional.reshape(y, self.shape[:-1] + [w3.shape[1]])
         out.requires_grad = any(v.requires_grad for v in (x, w1, w2, w3))
-        return self.attach(out, x2=x2, a=a, b=b, s=s, g=g, h=h, w1p=w1p, w2p=w2p, w3p=w3p,
-                           hid=hid)
+        return self.attach(out, x2=x2, a=a, b=b, h=h, w1p=w1p, w2p=w2p, w3p=w3p, hid=hid)
 
     def backward(self, dy):
-        x2, a, b, s, g, h = self.x2, self.a, self.b, self.s, self.g, self.h
+        x2, a, b, h = self.x2, self.a, self.b, self.h
         w1p, w2p, w3p, hid = self.w1p, self.w2p, self.w3p, self.hid
-        self.x2 = self.a = self.b = self.s = self.g = self.h = None
+        self.x2 = self.a = self.b = self.h = None
         self.w1p = self.w2p = self.w3p = None
         dy2 = functional.reshape(dy, [-1, w3p.shape[1]])
         if not dy2.is_contiguous():
@@ -144,12 +142,7 @@ class swiglu_padded(Function):
         if self.needs_input_grad[3]:
             dw3 = functional.contiguous(
                 functional.matmul_add(h, dy2, None, transpose_A=True, tile=tw)[:hid])
-        db = functional.pointwise(dh, g, 2)
-        dg = functional.pointwise(dh, b, 2)
-        # g = s a: da = dg s + sigmoid'(from s) (dg a)
-        ds = functional.pointwise(dg, a, 2)
-        da = functional.pointwise(functional.pointwise(dg, s, 2),
-                                  functional.unary_backward(s, ds, "sigmoid"), 0)
+        da, db = functional.swiglu_gate_backward(dh, a, b)
         dw1 = dw2 = dx = None
         if self.needs_input_grad[1]:
             dw1 = functional.contiguous(

@@ -99,6 +99,8 @@ SIGNATURES = {
     "wxx_scalarpointwise": (I32, [P, P, I64, I32, F32, I32]),
     "wxx_unary": (I32, [P, P, I64, I32]),
     "wxx_unary_backward": (I32, [P, P, P, I64, I32]),
+    "wxx_swiglu_gate": (I32, [P, P, P, I64]),
+    "wxx_swiglu_gate_backward": (I32, [P, P, P, P, P, I64]),
     "wxx_broadcast_scale": (I32, [P, P, I32, P, P, F32]),
     "wxx_clamp": (I32, [P, P, I64, F32, F32, I32]),
     "wxx_equal": (I32, [P, P, P, I64, I32, U32]),

@@ -265,6 +265,68 @@ __global__ __launch_bounds__(kBlock) void unary_bwd_kernel(const float* __restri
   for (int64_t i = (n4 << 2) + t; i < n; i += step) y[i] = unary_op(OP, x[i]) * g[i];
 }
 
+// SwiGLU's gate h = (sigmoid(a) a) b in one pass instead of the sigmoid,
+// a s and g b kernels, every operation rounded as those kernels round it:
+// contraction is off in these helpers (__fmul_rn / __fadd_rn are plain
+// operators here, which the compiler may fuse into an fma), as it is across
+// the separate kernels.
+__device__ __forceinline__ float swiglu_h(float a, float b) {
+#pragma clang fp contract(off)
+  const float s = unary_op(U_SIGMOID, a);
+  return (s * a) * b;
+}
+
+// Its backward from dh: with s and g = s a recomputed, db = dh g, dg = dh b,
+// da = dg s + sigmoid'(s) (dg a) -- the products and the sum of the mul,
+// mul and sigmoid backwards and the gradient accumulation they replace.
+__device__ __forceinline__ void swiglu_dab(float dh, float a, float b, float& da, float& db) {
+#pragma clang fp contract(off)
+  const float s = unary_op(U_SIGMOID, a);
+  const float g = s * a;
+  db = dh * g;
+  const float dg = dh * b;
+  const float ds = dg * a;
+  const float t1 = dg * s, t2 = unary_op(U_SIGMOID_BWD, s) * ds;
+  da = t1 + t2;
+}
+
+__global__ __launch_bounds__(kBlock) void swiglu_gate_kernel(const float* __restrict__ a,
+                                                             const float* __restrict__ b,
+                                                             float* __restrict__ h, int64_t n,
+                                                             int vec) {
+  const int64_t n4 = vec ? n >> 2 : 0;
+  const int64_t step = (int64_t)gridDim.x * kBlock;
+  const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  for (int64_t i = t; i < n4; i += step) {
+    const float4 x = reinterpret_cast<const float4*>(a)[i];
+    const float4 y = reinterpret_cast<const float4*>(b)[i];
+    reinterpret_cast<float4*>(h)[i] = make_float4(swiglu_h(x.x, y.x), swiglu_h(x.y, y.y),
+                                                  swiglu_h(x.z, y.z), swiglu_h(x.w, y.w));
+  }
+  for (int64_t i = (n4 << 2) + t; i < n; i += step) h[i] = swiglu_h(a[i], b[i]);
+}
+
+__global__ __launch_bounds__(kBlock) void swiglu_gate_bwd_kernel(
+    const float* __restrict__ dh, const float* __restrict__ a, const float* __restrict__ b,
+    float* __restrict__ da, float* __restrict__ db, int64_t n, int vec) {
+  const int64_t n4 = vec ? n >> 2 : 0;
+  const int64_t step = (int64_t)gridDim.x * kBlock;
+  const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  for (int64_t i = t; i < n4; i += step) {
+    const float4 g = reinterpret_cast<const float4*>(dh)[i];
+    const float4 x = reinterpret_cast<const float4*>(a)[i];
+    const float4 y = reinterpret_cast<const float4*>(b)[i];
+    float4 ra, rb;
+    swiglu_dab(g.x, x.x, y.x, ra.x, rb.x);
+    swiglu_dab(g.y, x.y, y.y, ra.y, rb.y);
+    swiglu_dab(g.z, x.z, y.z, ra.z, rb.z);
+    swiglu_dab(g.w, x.w, y.w, ra.w, rb.w);
+    reinterpret_cast<float4*>(da)[i] = ra;
+    reinterpret_cast<float4*>(db)[i] = rb;
+  }
+  for (int64_t i = (n4 << 2) + t; i < n; i += step) swiglu_dab(dh[i], a[i], b[i], da[i], db[i]);
+}
+
 // dst[i] = src[offset(i)] * scale for a dense dst over `shape` (broadcast read).
 __global__ __launch_bounds__(kBlock) void broadcast_scale_kernel(float* __restrict__ dst,
                                                                  const float* __restrict__ src,
@@ -859,6 +921,34 @@ WXX_API int wxx_unfolddx(const float* dy, float* dx, int64_t prefix, int64_t len
   if (n <= 0) return WXX_OK;
   hipLaunchKernelGGL(unfolddx_kernel, dim3(grid_for(n)), dim3(kBlock), 0, wxx::stream(), dy, dx,
                      prefix, length, suffix, windows, size, step);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// SwiGLU's gate silu(a) * b (reference src/wxx/nn/module.py:551-552, with
+// Tensor.silu = sigmoid(x) * x at Tensor.py:724-727) in one pass.
+WXX_API int wxx_swiglu_gate(const float* a, const float* b, float* h, int64_t n) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(a && b && h, "null pointer");
+  if (n <= 0) return WXX_OK;
+  const int vec = ((uintptr_t)a | (uintptr_t)b | (uintptr_t)h) % 16 == 0;
+  hipLaunchKernelGGL(swiglu_gate_kernel, dim3(grid_for((n + 3) / 4)), dim3(kBlock), 0,
+                     wxx::stream(), a, b, h, n, vec);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// The backward of wxx_swiglu_gate: da and db from dh, a and b (the composed
+// ops' backwards, autograd/pointwise.py mul and sigmoid, in one pass).
+WXX_API int wxx_swiglu_gate_backward(const float* dh, const float* a, const float* b, float* da,
+                                     float* db, int64_t n) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(dh && a && b && da && db, "null pointer");
+  if (n <= 0) return WXX_OK;
+  const int vec =
+      ((uintptr_t)dh | (uintptr_t)a | (uintptr_t)b | (uintptr_t)da | (uintptr_t)db) % 16 == 0;
+  hipLaunchKernelGGL(swiglu_gate_bwd_kernel, dim3(grid_for((n + 3) / 4)), dim3(kBlock), 0,
+                     wxx::stream(), dh, a, b, da, db, n, vec);
   WXX_LAUNCHED();
   return WXX_OK;
 }

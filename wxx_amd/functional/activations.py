@@ -74,6 +74,36 @@ def unary_backward(src, grad, name):
     return out
 
 
+def swiglu_gate(a, b):
+    """``silu(a) * b`` in one kernel, equal bit for bit to ``sigmoid(a) * a * b``."""
+    a, b = _same_dense(a, b, "swiglu_gate")
+    out = empty(a.shape)
+    call("wxx_swiglu_gate", ptr(a), ptr(b), ptr(out), validation.numel(a.shape))
+    return out
+
+
+def swiglu_gate_backward(grad, a, b):
+    """``(da, db)`` of :func:`swiglu_gate` for the output gradient ``grad``, equal bit
+    for bit to the composed ops' backwards."""
+    a, b = _same_dense(a, b, "swiglu_gate_backward")
+    grad, _ = _same_dense(grad, a, "swiglu_gate_backward")
+    da = empty(a.shape)
+    db = empty(a.shape)
+    call("wxx_swiglu_gate_backward", ptr(grad), ptr(a), ptr(b), ptr(da), ptr(db),
+         validation.numel(a.shape))
+    return da, db
+
+
+def _same_dense(x, y, what):
+    if not x.is_contiguous():
+        x = x.contiguous()
+    if not y.is_contiguous():
+        y = y.contiguous()
+    if tuple(x.shape) != tuple(y.shape):
+        raise ValueError(f"{what} shapes differ: {tuple(x.shape)} vs {tuple(y.shape)}")
+    return x, y
+
+
 def relu(tensor1):
     return unary(tensor1, "relu")
 
