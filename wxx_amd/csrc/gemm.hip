@@ -1021,8 +1021,12 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
     // tiles below are faster there, e.g. attention's 96 x 1024 x 1024 x 64
     // scores at 191 us against 237 us on 128 x 128 direct-to-LDS tiles.)
     const bool thin = g.M <= 64 || g.N <= 64 || g.K <= 128;
+    // (Up to 64 splits where K allows: a few output tiles over a very long K,
+    // Hyena's 256 x 256 weight gradients over K = 65536, take 64 splits of
+    // 1024 on 4 tiles instead of 32 splits on 16 register-staged 64 x 64
+    // tiles.)
     const int64_t smax =
-        dtl_ok && !thin ? std::min<int64_t>(16, std::max<int64_t>(g.K / 512, 1)) : 0;
+        dtl_ok && !thin ? std::min<int64_t>(64, std::max<int64_t>(g.K / 512, 1)) : 0;
     double best = 0.0;
     int best_splits = 1;
     for (int64_t sp = 1; sp <= smax; ++sp) {
@@ -1108,7 +1112,11 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
       // rounds of 128 x 128, 237 against 255 us on 128 x 64 tiles)
       tile = 13;
       splits = 1;
-    } else if (s6464 > 0 && bal6464 >= 0.8 && bal6464 >= bal64s && bal6464 > best) {
+    } else if (s6464 > 0 && bal6464 >= 0.8 && bal6464 >= bal64s && bal6464 > best &&
+               g.K / s6464 <= 2048) {
+      // (only for short K per unit: over long K ranges the 128 x 128 tiles'
+      // higher arithmetic intensity wins, e.g. 256 x 1024 x 65536 at 309 us
+      // on 16 tiles x 16 splits against 352 us on 64 x 64 tiles x 4 splits)
       tile = 15;
       splits = s6464;
     } else if (s64 > 0 && bal64s >= 0.8 && bal64s > best) {
@@ -1136,7 +1144,10 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
         while (s < 8 && t64 * s * 2 <= cus && g.K / (s * 2) >= 64) s *= 2;
         splits = s;
       } else if (tile == 1 && t64 < 2 * cus) {
-        splits = (int)std::min<int64_t>((8 * cus + t64 - 1) / t64, kmax);
+        // few thin tiles over a long K (Hyena's filter-network weight
+        // gradients, 17 x 64 and 64 x 256 over K = 8192): splits of >= 256
+        splits = (int)std::min<int64_t>((8 * cus + t64 - 1) / t64,
+                                        std::max<int64_t>(g.K / 256, 1));
       }
     } else if (t128 >= cus) {
       tile = g.K >= 4096 ? 4 : 2;
@@ -1172,7 +1183,7 @@ int matmul_impl(const float* A, const float* B, const float* bias, float* C, int
         splits = s;
       }
     }
-    splits = std::max(1, std::min(splits, tile == 4 ? 64 : 32));
+    splits = std::max(1, std::min(splits, tile == 4 || tile == 11 ? 64 : 32));
   }
   if (tri) {
     // triangular modes: one K range per row tile (no split), on the tile
