@@ -411,7 +411,10 @@ class irfft(Function):
             return None
         spec, _ = functional.rfft(g, self.N)
         w = functional.complex_weights([x / float(self.N) for x in _irfft_backward_weights(self.N)])
-        return functional.complex_pad(functional.complex_mul(spec, w), self.in_len)
+        gs = functional.complex_mul(spec, w)
+        # the spectrum already has the input's N / 2 + 1 bins when n matched
+        # it: no pad (a copy of the whole spectrum otherwise)
+        return gs if gs.shape[-1] == self.in_len else functional.complex_pad(gs, self.in_len)
 
 
 class complex_mul(Function):
