@@ -281,6 +281,115 @@ def test_fft_convolution_end_to_end_gradient(device):
     np.testing.assert_allclose(h.grad.numpy(), dH, rtol=1e-4, atol=1e-4)
 
 
+# (x shape, filter shape, n): the small-row transforms, the persistent ones
+# at 2^11..2^14 complex points (n = 4096 .. 32768, the Hyena rows at 16384),
+# a ragged odd length, a filter longer than the signal, n below 2 L (crop of
+# a circular product) and one row
+FFT_CONV = [
+    ((2, 3, 32), (3, 32), 64),
+    ((2, 4, 101), (4, 101), 256),
+    ((3, 2, 20), (2, 37), 64),
+    ((2, 3, 48), (3, 48), 64),
+    ((1, 1, 9), (1, 9), 16),
+    ((2, 2, 2048), (2, 2048), 4096),
+    ((2, 3, 3000), (3, 3000), 8192),
+    ((2, 4, 8192), (4, 8192), 16384),
+    ((1, 2, 16384), (2, 16384), 32768),
+]
+
+
+@pytest.mark.parametrize("xs,hs,n", FFT_CONV)
+def test_fft_conv_equals_composed_ops_bit_for_bit(device, xs, hs, n):
+    # the fused long convolution against rfft / complex_mul / irfft composed
+    # through their own Functions: output and both gradients identical bits
+    W = wxx()
+    r = rng(61)
+    X, H, G = (r.standard_normal(xs), r.standard_normal(hs),
+               r.standard_normal(xs[:-1] + (min(xs[-1], n),)))
+    length = min(xs[-1], n)
+    x0, h0 = f32(X, True), f32(H, True)
+    y0 = x0.rfft(n).complex_mul(h0.rfft(n)).irfft(n, length)
+    (y0 * f32(G)).sum().backward()
+    x1, h1 = f32(X, True), f32(H, True)
+    y1 = W.autograd.fft_conv(x1, h1).forward(x1, h1, n, length)
+    (y1 * f32(G)).sum().backward()
+    assert np.array_equal(y1.numpy(), y0.numpy())
+    assert np.array_equal(x1.grad.numpy(), x0.grad.numpy())
+    assert np.array_equal(h1.grad.numpy(), h0.grad.numpy())
+
+
+def test_fft_conv_filter_only_gradient(device):
+    # only the filter trains (a signal without requires_grad): no signal
+    # gradient is formed and the filter's still matches the composed ops
+    W = wxx()
+    r = rng(62)
+    X, H, G = r.standard_normal((3, 2, 40)), r.standard_normal((2, 40)), r.standard_normal((3, 2, 40))
+    h0 = f32(H, True)
+    (f32(X).rfft(128).complex_mul(h0.rfft(128)).irfft(128, 40) * f32(G)).sum().backward()
+    x1, h1 = f32(X), f32(H, True)
+    (W.autograd.fft_conv(x1, h1).forward(x1, h1, 128, 40) * f32(G)).sum().backward()
+    assert x1.grad is None
+    assert np.array_equal(h1.grad.numpy(), h0.grad.numpy())
+
+
+@pytest.mark.parametrize("batch", [1, 3, 4, 5, 8, 9])
+def test_complex_mul_batch_sum_equals_product_then_sum(device, batch):
+    # one pass against complex_mul followed by the sum over the batch: the
+    # same bits, for batches below, at and past multiples of four
+    W = wxx()
+    F = W.functional
+    r = rng(63)
+    A = r.standard_normal((batch, 3, 77)) + 1j * r.standard_normal((batch, 3, 77))
+    Cc = r.standard_normal((batch, 3, 77)) + 1j * r.standard_normal((batch, 3, 77))
+    a, c = c64(A), c64(Cc)
+    for conj in (False, True):
+        got = F.complex_mul_batch_sum(a, c, conj_c=conj, keep=2).numpy()
+        prod = F.complex_mul(a, c, conj_b=conj)
+        from wxx_amd.autograd.utils import _sum_to_shape_complex
+
+        want = _sum_to_shape_complex(prod, (3, 77)).numpy()
+        assert np.array_equal(got, want)
+        ref = (A.astype(np.complex64).astype(np.complex128)
+               * (np.conj(Cc) if conj else Cc).astype(np.complex64)).sum(axis=0)
+        np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("n", [16, 1024, 16384])
+def test_spectrum_products_fused_into_transforms(device, n):
+    # rfft_mul and irfft_mul against rfft / complex_mul / irfft with a filter
+    # broadcast over a leading dim, conjugated or not, and a weight row
+    W = wxx()
+    F = W.functional
+    r = rng(64)
+    bins = n // 2 + 1
+    x = f32(r.standard_normal((2, 3, n)))
+    Hn = r.standard_normal((3, bins)) + 1j * r.standard_normal((3, bins))
+    Wn = r.standard_normal(bins) + 1j * r.standard_normal(bins)
+    h, w = c64(Hn), c64(Wn)
+    spec, _ = F.rfft(x, n)
+    assert np.array_equal(F.rfft_mul(x, n, w).numpy(), F.complex_mul(spec, w).numpy())
+    for conj in (False, True):
+        want = F.irfft(F.complex_mul(F.complex_mul(spec, h, conj_b=conj), w), n,
+                       length=n - 3, scale=2.0).numpy()
+        got = F.irfft_mul(spec, n, h=h, weights=w, conj_h=conj, length=n - 3, scale=2.0).numpy()
+        assert np.array_equal(got, want)
+    assert np.array_equal(F.irfft_mul(spec, n).numpy(), F.irfft(spec, n).numpy())
+
+
+def test_spectrum_products_reject_bad_operands(device):
+    F = wxx().functional
+    x = f32(np.zeros((2, 64)))
+    spec, _ = F.rfft(x, 64)
+    with pytest.raises(ValueError):
+        F.rfft_mul(x, 65536, c64(np.zeros(32769)))
+    with pytest.raises(ValueError):
+        F.rfft_mul(x, 64, c64(np.zeros(32)))  # one bin short
+    with pytest.raises(ValueError):
+        F.irfft_mul(spec, 64, h=c64(np.zeros((3, 33))))  # not a trailing shape
+    with pytest.raises(ValueError):
+        F.complex_mul_batch_sum(spec, spec, keep=2)  # no batch dim left
+
+
 # ---- unfold ---------------------------------------------------------------------
 
 

@@ -433,6 +433,51 @@ class complex_mul(Function):
         return ga, gb
 
 
+class fft_conv(Function):
+    """``irfft(rfft(x, n) * rfft(h, n), n)[..., :length]``: the long
+    convolution of (..., D, Lx) signals with (D, Lh) filters broadcast over
+    the leading dims (reference nn/hyena.py:208-216), with every spectrum
+    product fused into a transform: the forward product into the inverse
+    transform's load, the irfft adjoint's bin weights into the rfft's store,
+    the filter product and the rfft adjoint's bin weights into the inverse
+    transform of the signal gradient, and the filter gradient's product and
+    batch sum into one pass.  Values and gradients equal those of the
+    composed rfft / complex_mul / irfft Functions bit for bit (each fused
+    product rounds as complex_mul does, the batch sum adds in the reduction's
+    order).  Built as ``fft_conv(x, h)``, run as ``.forward(x, h, n, length)``
+    for a power-of-two n <= ``functional.FUSED_MAX_N``."""
+
+    def forward(self, x, h, n, length):
+        n = int(n)
+        self.N, self.x_len, self.h_len = n, x.shape[-1], h.shape[-1]
+        X, _ = functional.rfft(x, n)
+        H, _ = functional.rfft(h, n)
+        out = functional.irfft_mul(X, n, h=H, length=length)
+        out.requires_grad = x.requires_grad or h.requires_grad
+        return self.attach(out, X=X, H=H)
+
+    def backward(self, g):
+        X, H = self.X, self.H
+        self.X = self.H = None
+        n = self.N
+        # the irfft adjoint: rfft(g, n) * w_irfft / n
+        wi = functional.complex_weights([v / float(n) for v in _irfft_backward_weights(n)])
+        gs = functional.rfft_mul(g, n, wi)
+        wr = functional.complex_weights(_rfft_backward_weights(n))
+        gx = gh = None
+        if self.needs_input_grad[0]:
+            # the rfft adjoint of gs * conj(H): irfft(gs conj(H) w_rfft) * n
+            gx = functional.irfft_mul(gs, n, h=H, weights=wr, conj_h=True,
+                                      length=min(self.x_len, n), scale=float(n))
+            gx = _match_last_dim_real(gx, self.x_len)
+        if self.needs_input_grad[1]:
+            gH = functional.complex_mul_batch_sum(gs, X, conj_c=True, keep=len(H.shape))
+            gh = functional.irfft_mul(gH, n, weights=wr, length=min(self.h_len, n),
+                                      scale=float(n))
+            gh = _match_last_dim_real(gh, self.h_len)
+        return gx, gh
+
+
 class complex_conj(Function):
     def forward(self, tensor1):
         out = functional.complex_conj(tensor1)

@@ -80,6 +80,37 @@ __device__ __forceinline__ float2 cmul(float2 a, float2 b) {
   return make_float2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
 }
 
+// a * b with the rounding fixed as written: re = fma(a.x, b.x, -(a.y b.y)),
+// im = fma(a.x, b.y, a.y b.x).  The elementwise complex product and the
+// spectrum products fused into the transforms both use it, so a fused
+// product rounds exactly as the separate one does.
+__device__ __forceinline__ float2 cmul_op(float2 a, float2 b) {
+  return make_float2(fmaf(a.x, b.x, -(a.y * b.y)), fmaf(a.x, b.y, a.y * b.x));
+}
+
+// Spectrum operands multiplied into a transform's input bins (irfft) or
+// output bins (rfft): bin j of row r becomes v * h[r mod hrows][j]
+// (conjugated when conj_h) * w[j], products in that order; a null operand is
+// skipped.  h rows and w have the spectrum's bins per row.
+struct SpecMul {
+  const float2* h;
+  const float2* w;
+  int64_t hrows;
+  int conj_h;
+};
+
+// hr: this row's h row, or null.
+__device__ __forceinline__ float2 spec_mul(float2 v, const SpecMul& m,
+                                           const float2* __restrict__ hr, int64_t j) {
+  if (hr) {
+    float2 b = hr[j];
+    if (m.conj_h) b.y = -b.y;
+    v = cmul_op(v, b);
+  }
+  if (m.w) v = cmul_op(v, m.w[j]);
+  return v;
+}
+
 // cos(pi m / 8), m in [0, 16)
 __device__ constexpr float kCosPi8[16] = {
     1.0f,  0.92387953251128674f,  0.70710678118654752f,  0.38268343236508977f,
@@ -244,11 +275,13 @@ __device__ __forceinline__ void run_passes(float2* v, float2* buf, int t,
 }
 
 // x: rows x in_len f32 (zero-padded / truncated to n = 2M); X: rows x (M+1) c64.
-template <int LOGM, bool VEC>
+// MUL: output bins multiplied by sm's operands (spec_mul).
+template <int LOGM, bool VEC, bool MUL>
 __global__ __launch_bounds__(Geo<LOGM>::NT) void rfft_kernel(const float* __restrict__ x,
                                                              float2* __restrict__ X,
                                                              const float2* __restrict__ tw,
-                                                             int64_t rows, int64_t in_len) {
+                                                             int64_t rows, int64_t in_len,
+                                                             SpecMul sm) {
   using G = Geo<LOGM>;
   constexpr Plan pl{LOGM};
   __shared__ float2 lds[G::RPB * G::PM];
@@ -288,17 +321,19 @@ __global__ __launch_bounds__(Geo<LOGM>::NT) void rfft_kernel(const float* __rest
     const float2 e = make_float2(0.5f * (a.x + b.x), 0.5f * (a.y - b.y));
     const float2 o = make_float2(0.5f * (a.y + b.y), 0.5f * (b.x - a.x));
     const float2 w = wu[k];
-    Xr[k] = make_float2(e.x + (w.x * o.x - w.y * o.y), e.y + (w.x * o.y + w.y * o.x));
+    const float2 z = make_float2(e.x + (w.x * o.x - w.y * o.y), e.y + (w.x * o.y + w.y * o.x));
+    Xr[k] = MUL ? spec_mul(z, sm, nullptr, k) : z;
   }
 }
 
 // X: rows x in_len c64 one-sided spectrum; x: rows x n f32 (n = 2M).
-template <int LOGM, int CROP>
+// MUL: input bins multiplied by sm's operands (spec_mul) as they load.
+template <int LOGM, int CROP, bool MUL>
 __global__ __launch_bounds__(Geo<LOGM>::NT) void irfft_kernel(const float2* __restrict__ X,
                                                               float* __restrict__ x,
                                                               const float2* __restrict__ tw,
                                                               int64_t rows, int64_t in_len,
-                                                              RowOut ro) {
+                                                              RowOut ro, SpecMul sm) {
   using G = Geo<LOGM>;
   constexpr Plan pl{LOGM};
   __shared__ float2 lds[G::RPB * G::PM];
@@ -309,6 +344,7 @@ __global__ __launch_bounds__(Geo<LOGM>::NT) void irfft_kernel(const float2* __re
   float2* buf = lds + rb * G::PM;
   const float2* Xr = X + (live ? row : 0) * in_len;
   const float2* wu = tw + pl.offset(pl.npass());
+  const float2* hr = MUL && sm.h ? sm.h + ((live ? row : 0) % sm.hrows) * in_len : nullptr;
 
   // Pack the Hermitian spectrum into Z = E + i O (E, O: spectra of the even
   // and odd samples).  Bins at or above in_len are zero; the imaginary parts
@@ -323,8 +359,8 @@ __global__ __launch_bounds__(Geo<LOGM>::NT) void irfft_kernel(const float2* __re
       const int jj = G::M - j;
       float2 a = make_float2(0.f, 0.f), b = make_float2(0.f, 0.f);
       if (live) {
-        if (j < in_len) a = Xr[j];
-        if (jj < in_len) b = Xr[jj];
+        if (j < in_len) a = MUL ? spec_mul(Xr[j], sm, hr, j) : Xr[j];
+        if (jj < in_len) b = MUL ? spec_mul(Xr[jj], sm, hr, jj) : Xr[jj];
       }
       if (j == 0) a.y = 0.f;
       if (jj == G::M) b.y = 0.f;
@@ -575,10 +611,10 @@ __device__ __forceinline__ void rfft_big_load(float2* v, const float* __restrict
     }
 }
 
-template <int LOGM, bool VEC>
+template <int LOGM, bool VEC, bool MUL>
 __global__ __launch_bounds__(Big<LOGM>::T, Big<LOGM>::MIN_WAVES) void rfft_big_kernel(
     const float* __restrict__ x, float2* __restrict__ X, const float2* __restrict__ tw,
-    int64_t rows, int64_t in_len) {
+    int64_t rows, int64_t in_len, SpecMul sm) {
   using G = Big<LOGM>;
   __shared__ float2 buf[G::PM];
   float2 twb[G::NTB];
@@ -629,8 +665,10 @@ __global__ __launch_bounds__(Big<LOGM>::T, Big<LOGM>::MIN_WAVES) void rfft_big_k
       const float2 o = make_float2(0.5f * (a.y + b.y), 0.5f * (b.x - a.x));
       const float2 w = cmul(wtr, untangle_tw<G::E, G::T>(wu, i * G::T));
       const float2 wo = cmul(w, o);
-      Xr[k] = make_float2(e.x + wo.x, e.y + wo.y);
-      if (k != G::M / 2) Xr[G::M - k] = make_float2(e.x - wo.x, wo.y - e.y);
+      const float2 lo = make_float2(e.x + wo.x, e.y + wo.y);
+      const float2 hi = make_float2(e.x - wo.x, wo.y - e.y);
+      Xr[k] = MUL ? spec_mul(lo, sm, nullptr, k) : lo;
+      if (k != G::M / 2) Xr[G::M - k] = MUL ? spec_mul(hi, sm, nullptr, G::M - k) : hi;
     }
     __syncthreads();  // the row buffer is free for the next row
   }
@@ -646,21 +684,23 @@ __host__ __device__ constexpr int big_pos0(int e) {
 }
 
 // Spectrum bins of one irfft row at this thread's pass-0 positions.
-template <int LOGM, bool FULL>
+template <int LOGM, bool FULL, bool MUL>
 __device__ __forceinline__ void irfft_big_load(float2* a, const float2* __restrict__ Xr, int t,
-                                               int64_t in_len) {
+                                               int64_t in_len, const SpecMul& sm,
+                                               const float2* __restrict__ hr) {
   using G = Big<LOGM>;
 #pragma unroll
   for (int e = 0; e < G::E; ++e) {
     const int j = t + big_pos0<LOGM>(e);
-    a[e] = (FULL || j < in_len) ? Xr[j] : make_float2(0.f, 0.f);  // FULL: in_len >= M
+    a[e] = (FULL || j < in_len) ? (MUL ? spec_mul(Xr[j], sm, hr, j) : Xr[j])
+                                : make_float2(0.f, 0.f);  // FULL: in_len >= M
   }
 }
 
-template <int LOGM, int CROP>
+template <int LOGM, int CROP, bool MUL>
 __global__ __launch_bounds__(Big<LOGM>::T, Big<LOGM>::MIN_WAVES) void irfft_big_kernel(
     const float2* __restrict__ X, float* __restrict__ x, const float2* __restrict__ tw,
-    int64_t rows, int64_t in_len, RowOut ro) {
+    int64_t rows, int64_t in_len, RowOut ro, SpecMul sm) {
   using G = Big<LOGM>;
   __shared__ float2 buf[G::PM];
   float2 twb[G::NTB];
@@ -676,11 +716,13 @@ __global__ __launch_bounds__(Big<LOGM>::T, Big<LOGM>::MIN_WAVES) void irfft_big_
     WXX_OPAQUE(wtr.x);
     WXX_OPAQUE(wtr.y);
     const float2* Xr = X + row * in_len;
+    const float2* hr = MUL && sm.h ? sm.h + (row % sm.hrows) * in_len : nullptr;
     if (in_len >= G::M)
-      irfft_big_load<LOGM, true>(v, Xr, t, in_len);
+      irfft_big_load<LOGM, true, MUL>(v, Xr, t, in_len, sm, hr);
     else
-      irfft_big_load<LOGM, false>(v, Xr, t, in_len);
-    const float2 nyq = G::M < in_len ? Xr[G::M] : make_float2(0.f, 0.f);
+      irfft_big_load<LOGM, false, MUL>(v, Xr, t, in_len, sm, hr);
+    const float2 nyq = G::M < in_len ? (MUL ? spec_mul(Xr[G::M], sm, hr, G::M) : Xr[G::M])
+                                     : make_float2(0.f, 0.f);
     // exchange the bins through LDS to pair j with M - j
     const int tb = bpad(t), nb = -t + ((-t) >> 5);  // bpad(t), and bpad(a - t) - bpad_c(a)
 #pragma unroll
@@ -805,9 +847,10 @@ int log2_exact(int64_t n) {
   return (int64_t(1) << l) == n ? l : -1;
 }
 
-template <int LOGM>
-void launch_rfft(const float* x, float2* X, const float2* tw, int64_t rows, int64_t in_len,
-                 bool vec) {
+// sm null: the plain transform; else the MUL instantiation with *sm.
+template <int LOGM, bool VEC, bool MUL>
+void launch_rfft_k(const float* x, float2* X, const float2* tw, int64_t rows, int64_t in_len,
+                   const SpecMul& sm) {
   if constexpr (LOGM >= kBigMinLogM) {
     const float2* btw = big_twiddles<LOGM>();
     if (!btw) {
@@ -815,30 +858,36 @@ void launch_rfft(const float* x, float2* X, const float2* tw, int64_t rows, int6
       return;
     }
     constexpr int T = Big<LOGM>::T;
-    if (vec) {
-      const unsigned g = persistent_grid(rfft_big_kernel<LOGM, true>, T, rows);
-      hipLaunchKernelGGL((rfft_big_kernel<LOGM, true>), dim3(g), dim3(T), 0, wxx::stream(), x, X,
-                         btw, rows, in_len);
-    } else {
-      const unsigned g = persistent_grid(rfft_big_kernel<LOGM, false>, T, rows);
-      hipLaunchKernelGGL((rfft_big_kernel<LOGM, false>), dim3(g), dim3(T), 0, wxx::stream(), x, X,
-                         btw, rows, in_len);
-    }
-    return;
+    const unsigned g = persistent_grid(rfft_big_kernel<LOGM, VEC, MUL>, T, rows);
+    hipLaunchKernelGGL((rfft_big_kernel<LOGM, VEC, MUL>), dim3(g), dim3(T), 0, wxx::stream(), x,
+                       X, btw, rows, in_len, sm);
+  } else {
+    using G = Geo<LOGM>;
+    const dim3 grid((unsigned)((rows + G::RPB - 1) / G::RPB));
+    hipLaunchKernelGGL((rfft_kernel<LOGM, VEC, MUL>), grid, dim3(G::NT), 0, wxx::stream(), x, X,
+                       tw, rows, in_len, sm);
   }
-  using G = Geo<LOGM>;
-  const dim3 grid((unsigned)((rows + G::RPB - 1) / G::RPB));
-  if (vec)
-    hipLaunchKernelGGL((rfft_kernel<LOGM, true>), grid, dim3(G::NT), 0, wxx::stream(), x, X, tw,
-                       rows, in_len);
-  else
-    hipLaunchKernelGGL((rfft_kernel<LOGM, false>), grid, dim3(G::NT), 0, wxx::stream(), x, X, tw,
-                       rows, in_len);
 }
 
-template <int LOGM, int CROP>
+template <int LOGM>
+void launch_rfft(const float* x, float2* X, const float2* tw, int64_t rows, int64_t in_len,
+                 bool vec, const SpecMul* sm) {
+  const SpecMul none{};
+  if (sm) {
+    if (vec)
+      launch_rfft_k<LOGM, true, true>(x, X, tw, rows, in_len, *sm);
+    else
+      launch_rfft_k<LOGM, false, true>(x, X, tw, rows, in_len, *sm);
+  } else if (vec) {
+    launch_rfft_k<LOGM, true, false>(x, X, tw, rows, in_len, none);
+  } else {
+    launch_rfft_k<LOGM, false, false>(x, X, tw, rows, in_len, none);
+  }
+}
+
+template <int LOGM, int CROP, bool MUL>
 void launch_irfft_mode(const float2* X, float* x, const float2* tw, int64_t rows, int64_t in_len,
-                       RowOut ro) {
+                       RowOut ro, const SpecMul& sm) {
   ro.scale = 1.0f / (float)(1 << LOGM);
   if constexpr (LOGM >= kBigMinLogM) {
     const float2* btw = big_twiddles<LOGM>();
@@ -847,43 +896,52 @@ void launch_irfft_mode(const float2* X, float* x, const float2* tw, int64_t rows
       return;
     }
     constexpr int T = Big<LOGM>::T;
-    const unsigned g = persistent_grid(irfft_big_kernel<LOGM, CROP>, T, rows);
-    hipLaunchKernelGGL((irfft_big_kernel<LOGM, CROP>), dim3(g), dim3(T), 0, wxx::stream(), X, x,
-                       btw, rows, in_len, ro);
+    const unsigned g = persistent_grid(irfft_big_kernel<LOGM, CROP, MUL>, T, rows);
+    hipLaunchKernelGGL((irfft_big_kernel<LOGM, CROP, MUL>), dim3(g), dim3(T), 0, wxx::stream(), X,
+                       x, btw, rows, in_len, ro, sm);
     return;
   }
   using G = Geo<LOGM>;
   const dim3 grid((unsigned)((rows + G::RPB - 1) / G::RPB));
-  hipLaunchKernelGGL((irfft_kernel<LOGM, CROP>), grid, dim3(G::NT), 0, wxx::stream(), X, x, tw,
-                     rows, in_len, ro);
+  hipLaunchKernelGGL((irfft_kernel<LOGM, CROP, MUL>), grid, dim3(G::NT), 0, wxx::stream(), X, x,
+                     tw, rows, in_len, ro, sm);
+}
+
+template <int LOGM, bool MUL>
+void launch_irfft_m(const float2* X, float* x, const float2* tw, int64_t rows, int64_t in_len,
+                    const RowOut& ro, const SpecMul& sm) {
+  if (ro.mode == 0)
+    launch_irfft_mode<LOGM, 0, MUL>(X, x, tw, rows, in_len, ro, sm);
+  else if (ro.mode == 1)
+    launch_irfft_mode<LOGM, 1, MUL>(X, x, tw, rows, in_len, ro, sm);
+  else
+    launch_irfft_mode<LOGM, 2, MUL>(X, x, tw, rows, in_len, ro, sm);
 }
 
 template <int LOGM>
 void launch_irfft(const float2* X, float* x, const float2* tw, int64_t rows, int64_t in_len,
-                  RowOut ro) {
-  if (ro.mode == 0)
-    launch_irfft_mode<LOGM, 0>(X, x, tw, rows, in_len, ro);
-  else if (ro.mode == 1)
-    launch_irfft_mode<LOGM, 1>(X, x, tw, rows, in_len, ro);
+                  const RowOut& ro, const SpecMul* sm) {
+  if (sm)
+    launch_irfft_m<LOGM, true>(X, x, tw, rows, in_len, ro, *sm);
   else
-    launch_irfft_mode<LOGM, 2>(X, x, tw, rows, in_len, ro);
+    launch_irfft_m<LOGM, false>(X, x, tw, rows, in_len, ro, SpecMul{});
 }
 
 template <int L = 0>
 void dispatch_rfft(int logm, const float* x, float2* X, const float2* tw, int64_t rows,
-                   int64_t in_len, bool vec) {
+                   int64_t in_len, bool vec, const SpecMul* sm = nullptr) {
   if constexpr (L <= kMaxLogM) {
-    if (logm == L) return launch_rfft<L>(x, X, tw, rows, in_len, vec);
-    dispatch_rfft<L + 1>(logm, x, X, tw, rows, in_len, vec);
+    if (logm == L) return launch_rfft<L>(x, X, tw, rows, in_len, vec, sm);
+    dispatch_rfft<L + 1>(logm, x, X, tw, rows, in_len, vec, sm);
   }
 }
 
 template <int L = 0>
 void dispatch_irfft(int logm, const float2* X, float* x, const float2* tw, int64_t rows,
-                    int64_t in_len, const RowOut& ro) {
+                    int64_t in_len, const RowOut& ro, const SpecMul* sm = nullptr) {
   if constexpr (L <= kMaxLogM) {
-    if (logm == L) return launch_irfft<L>(X, x, tw, rows, in_len, ro);
-    dispatch_irfft<L + 1>(logm, X, x, tw, rows, in_len, ro);
+    if (logm == L) return launch_irfft<L>(X, x, tw, rows, in_len, ro, sm);
+    dispatch_irfft<L + 1>(logm, X, x, tw, rows, in_len, ro, sm);
   }
 }
 
@@ -893,7 +951,7 @@ __device__ __forceinline__ float2 complex_op(float2 u, float2 w, int op, int con
                                              int conj_b) {
   if (conj_a) u.y = -u.y;
   if (conj_b) w.y = -w.y;
-  return op == 0 ? cmul(u, w) : make_float2(u.x + w.x, u.y + w.y);
+  return op == 0 ? cmul_op(u, w) : make_float2(u.x + w.x, u.y + w.y);
 }
 
 template <bool WIDE>
@@ -983,6 +1041,43 @@ __global__ __launch_bounds__(256) void complex_conj_kernel(float2* __restrict__ 
   }
 }
 
+// out[i] = sum over b < batch of a[b n + i] * (conj) c[b n + i]: the product
+// of a spectrum gradient with a batch of spectra summed over the batch (the
+// adjoint of a filter broadcast over the batch), one output per thread.  Each
+// part is summed in the column-sum order of the reduction kernels: rows
+// r = 4 q + s into four partial sums s (the rows past the last multiple of
+// four into the first), then (s0 + s1) + (s2 + s3), so the fused sum equals
+// the product followed by that reduction.
+__global__ __launch_bounds__(256) void complex_mul_batch_sum_kernel(
+    float2* __restrict__ out, const float2* __restrict__ a, const float2* __restrict__ c,
+    int64_t batch, int64_t n, int conj_c) {
+  const int64_t step = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += step) {
+    float2 s[4] = {make_float2(0.f, 0.f), make_float2(0.f, 0.f), make_float2(0.f, 0.f),
+                   make_float2(0.f, 0.f)};
+    int64_t b = 0;
+    for (; b + 3 < batch; b += 4) {
+      float2 p[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        float2 w = c[(b + u) * n + i];
+        if (conj_c) w.y = -w.y;
+        p[u] = cmul_op(a[(b + u) * n + i], w);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) s[u] = make_float2(s[u].x + p[u].x, s[u].y + p[u].y);
+    }
+    for (; b < batch; ++b) {
+      float2 w = c[b * n + i];
+      if (conj_c) w.y = -w.y;
+      const float2 p = cmul_op(a[b * n + i], w);
+      s[0] = make_float2(s[0].x + p.x, s[0].y + p.y);
+    }
+    out[i] = make_float2((s[0].x + s[1].x) + (s[2].x + s[3].x),
+                         (s[0].y + s[1].y) + (s[2].y + s[3].y));
+  }
+}
+
 __global__ __launch_bounds__(256) void complex_pad_kernel(const float2* __restrict__ src,
                                                           float2* __restrict__ dst,
                                                           int64_t batch, int64_t in_len,
@@ -1056,6 +1151,84 @@ WXX_API int wxx_irfft_crop(const void* X, float* x, int64_t rows, int64_t in_len
 // functional.irfft without a crop: rows x n.
 WXX_API int wxx_irfft(const void* X, float* x, int64_t rows, int64_t in_len, int64_t n) {
   return wxx_irfft_crop(X, x, rows, in_len, n, n, 1.0f);
+}
+
+// rfft with each output bin k multiplied by w[k] (w: n/2 + 1 bins): the
+// spectrum product of the irfft backward (reference autograd/utils.py:549-718,
+// complex_mul of rfft(g) with the bin weights) fused into the transform's
+// store.  The product rounds as wxx_complex_binary's does, so the result is
+// the bit pattern of wxx_rfft followed by that product.
+WXX_API int wxx_rfft_mul(const float* x, void* X, const void* w, int64_t rows, int64_t in_len,
+                         int64_t n) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(x && X && w, "null pointer");
+  WXX_REQUIRE(rows >= 0 && in_len >= 0, "bad rfft dims");
+  const int logn = log2_exact(n);
+  WXX_REQUIRE(logn >= 1 && logn - 1 <= kMaxLogM,
+              "fused spectrum product needs a power-of-two n in [2, %d], got %lld",
+              2 << kMaxLogM, (long long)n);
+  if (rows == 0) return WXX_OK;
+  const float2* tw = twiddles(logn - 1);
+  if (!tw) return wxx::set_error(WXX_E_OOM, "rfft twiddle table allocation failed");
+  const SpecMul sm{nullptr, static_cast<const float2*>(w), 1, 0};
+  const bool vec = in_len % 2 == 0 && (uintptr_t)x % 8 == 0;
+  dispatch_rfft(logn - 1, x, static_cast<float2*>(X), tw, rows, in_len, vec, &sm);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// wxx_irfft_crop of the product X * h * w, formed as the bins load: row r of
+// X (in_len bins) times row r mod hrows of h (conjugated when conj_h) times
+// w (in_len bins), products in that order and rounded as wxx_complex_binary's;
+// h or w null skips that factor.  Fuses the Hyena long convolution's
+// spectrum product into its inverse transform (reference nn/hyena.py:208-216:
+// irfft(rfft(x) * rfft(h))) and the filter product and bin weights of its
+// backward into the rfft adjoint (autograd/utils.py:549-718).
+WXX_API int wxx_irfft_mul(const void* X, const void* h, const void* w, float* x, int64_t rows,
+                          int64_t in_len, int64_t hrows, int conj_h, int64_t n, int64_t out_len,
+                          float post_scale) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(x && X, "null pointer");
+  WXX_REQUIRE(rows >= 0 && in_len >= 0, "bad irfft dims");
+  WXX_REQUIRE(!h || hrows >= 1, "operand rows must be >= 1, got %lld", (long long)hrows);
+  const int logn = log2_exact(n);
+  WXX_REQUIRE(logn >= 1 && logn - 1 <= kMaxLogM,
+              "fused spectrum product needs a power-of-two n in [2, %d], got %lld",
+              2 << kMaxLogM, (long long)n);
+  WXX_REQUIRE(out_len >= 1 && out_len <= n, "irfft output length %lld not in [1, %lld]",
+              (long long)out_len, (long long)n);
+  if (rows == 0) return WXX_OK;
+  const float2* tw = twiddles(logn - 1);
+  if (!tw) return wxx::set_error(WXX_E_OOM, "irfft twiddle table allocation failed");
+  RowOut ro{};
+  ro.lim = out_len;
+  ro.lim32 = (int)out_len;
+  ro.half = (int)(out_len / 2);
+  ro.post = post_scale;
+  ro.mode = out_len == n ? 0 : (out_len % 2 == 0 ? 1 : 2);
+  const SpecMul sm{static_cast<const float2*>(h), static_cast<const float2*>(w),
+                   h ? hrows : 1, conj_h ? 1 : 0};
+  dispatch_irfft(logn - 1, static_cast<const float2*>(X), x, tw, rows, in_len, ro, &sm);
+  WXX_LAUNCHED();
+  return WXX_OK;
+}
+
+// out[i] = sum over b < batch of a[b n + i] * c[b n + i] (c conjugated when
+// conj_c): the broadcast operand's gradient of complex_mul (reference
+// autograd/utils.py:549-718, the product g * conj(a) summed to the filter's
+// shape) in one pass, with the products and the summation order of
+// wxx_complex_binary followed by wxx_reduce over the batch.
+WXX_API int wxx_complex_mul_batch_sum(void* out, const void* a, const void* c, int64_t batch,
+                                      int64_t n, int conj_c) {
+  WXX_CHECK_INIT();
+  WXX_REQUIRE(out && a && c, "null pointer");
+  WXX_REQUIRE(batch >= 1 && n >= 0, "bad batch-sum dims");
+  if (n == 0) return WXX_OK;
+  hipLaunchKernelGGL(complex_mul_batch_sum_kernel, dim3(wxx::grid_1d(n, 256, 16384)), dim3(256),
+                     0, wxx::stream(), static_cast<float2*>(out), static_cast<const float2*>(a),
+                     static_cast<const float2*>(c), batch, n, conj_c ? 1 : 0);
+  WXX_LAUNCHED();
+  return WXX_OK;
 }
 
 // Replaces functional.complex_mul (fft.py:168-213, op 0, conj flags) and

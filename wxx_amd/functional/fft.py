@@ -215,7 +215,113 @@ def irfft(tensor1, n=None, length=None, scale=1.0):
     return out
 
 
+# the fused spectrum products run inside the LDS-resident transforms
+FUSED_MAX_N = 32768
+
+
+def fused_spectrum_supported(n):
+    """Whether ``rfft_mul`` / ``irfft_mul`` take transform length ``n``."""
+    n = int(n)
+    return 2 <= n <= FUSED_MAX_N and (n & (n - 1)) == 0
+
+
+def _contig_c64(t, name):
+    _require_c64(t, name)
+    return t if t.is_contiguous() else complex_contiguous(t)
+
+
+def rfft_mul(tensor1, n, weights):
+    """``complex_mul(rfft(tensor1, n)[0], weights)`` in one kernel: bin k of
+    every row times ``weights[k]`` (a c64 vector of ``n // 2 + 1`` bins) as
+    the transform stores it, rounded as complex_mul rounds (the irfft
+    backward's spectrum product, reference autograd/utils.py:549-718)."""
+    if tensor1.type == "c64":
+        raise TypeError("rfft_mul expects a real-valued tensor")
+    n = int(n)
+    if not fused_spectrum_supported(n):
+        raise ValueError(f"rfft_mul needs a power-of-two n in [2, {FUSED_MAX_N}], got {n}")
+    weights = _contig_c64(weights, "rfft_mul")
+    if tuple(weights.shape) != (n // 2 + 1,):
+        raise ValueError(f"rfft_mul weights must have shape ({n // 2 + 1},), "
+                         f"got {tuple(weights.shape)}")
+    if not tensor1.is_contiguous():
+        tensor1 = tensor1.contiguous()
+    validation.check_rank(tensor1.shape, min_rank=1, name="rfft_mul input")
+    shape = list(tensor1.shape)
+    rows = validation.numel(shape[:-1])
+    out = empty(shape[:-1] + [n // 2 + 1], dtype="c64")
+    call("wxx_rfft_mul", ptr(tensor1), ptr(out), ptr(weights), rows, shape[-1], n)
+    return out
+
+
+def irfft_mul(tensor1, n, h=None, weights=None, conj_h=False, length=None, scale=1.0):
+    """``irfft(tensor1 * h * weights, n, length, scale)`` with the products
+    formed as the bins load, rounded as complex_mul rounds.  ``h`` (c64, the
+    trailing dims of ``tensor1``'s shape) broadcasts over ``tensor1``'s
+    leading dims and is conjugated when ``conj_h``; ``weights`` is one row of
+    bins; either may be None.  The Hyena long convolution's forward product
+    and its backward's filter product (reference nn/hyena.py:208-216)."""
+    tensor1 = _contig_c64(tensor1, "irfft_mul")
+    validation.check_rank(tensor1.shape, min_rank=1, name="irfft_mul input")
+    n = int(n)
+    if not fused_spectrum_supported(n):
+        raise ValueError(f"irfft_mul needs a power-of-two n in [2, {FUSED_MAX_N}], got {n}")
+    shape = list(tensor1.shape)
+    in_len = shape[-1]
+    rows = validation.numel(shape[:-1])
+    hrows = 1
+    if h is not None:
+        h = _contig_c64(h, "irfft_mul")
+        hs = list(h.shape)
+        if len(hs) == 0 or len(hs) > len(shape) or shape[len(shape) - len(hs):] != hs:
+            raise ValueError(f"irfft_mul operand shape {tuple(hs)} is not a trailing part "
+                             f"of {tuple(shape)}")
+        hrows = validation.numel(hs[:-1])
+    if weights is not None:
+        weights = _contig_c64(weights, "irfft_mul")
+        if tuple(weights.shape) != (in_len,):
+            raise ValueError(f"irfft_mul weights must have shape ({in_len},), "
+                             f"got {tuple(weights.shape)}")
+    length = n if length is None else int(length)
+    if not 1 <= length <= n:
+        raise ValueError(f"irfft length must be in [1, {n}], got {length}")
+    out = empty(shape[:-1] + [length])
+    call("wxx_irfft_mul", ptr(tensor1), ptr(h) if h is not None else None,
+         ptr(weights) if weights is not None else None, ptr(out), rows, in_len, max(hrows, 1),
+         1 if conj_h else 0, n, length, C.c_float(scale))
+    return out
+
+
+def complex_mul_batch_sum(tensor_a, tensor_c, conj_c=False, keep=1):
+    """``sum(tensor_a * tensor_c, leading dims)`` in one pass, keeping the
+    last ``keep`` dims (``tensor_c`` conjugated when ``conj_c``): the
+    broadcast operand's gradient of complex_mul (reference
+    autograd/utils.py:549-718), equal bit for bit to complex_mul followed by
+    the reduction over the leading dims."""
+    tensor_a = _contig_c64(tensor_a, "complex_mul_batch_sum")
+    tensor_c = _contig_c64(tensor_c, "complex_mul_batch_sum")
+    if tuple(tensor_a.shape) != tuple(tensor_c.shape):
+        raise ValueError(f"complex_mul_batch_sum shapes differ: {tuple(tensor_a.shape)} "
+                         f"and {tuple(tensor_c.shape)}")
+    shape = list(tensor_a.shape)
+    if not 1 <= keep < len(shape):
+        raise ValueError(f"complex_mul_batch_sum keeps {keep} of {len(shape)} dims")
+    out_shape = shape[len(shape) - keep:]
+    n = validation.numel(out_shape)
+    batch = validation.numel(shape[:len(shape) - keep])
+    if batch == 0:
+        raise ValueError("complex_mul_batch_sum needs a non-empty batch")
+    out = empty(out_shape, dtype="c64")
+    call("wxx_complex_mul_batch_sum", ptr(out), ptr(tensor_a), ptr(tensor_c), batch, n,
+         1 if conj_c else 0)
+    return out
+
+
 __all__ = [
+    "rfft_mul",
+    "irfft_mul",
+    "complex_mul_batch_sum",
+    "fused_spectrum_supported",
     "rfft",
     "irfft",
     "complex_mul",

@@ -103,9 +103,15 @@ class HyenaOperator(Module):
         return n if n >= length else _pow2_at_least(length)
 
     def fft_conv1d(self, x, h):
-        """Causal convolution of (B, D, L) signals with (D, L) filters, cropped to L."""
+        """Causal convolution of (B, D, L) signals with (D, L) filters, cropped
+        to L: irfft(rfft(x) * rfft(h)), as one fused op (``autograd.fft_conv``,
+        equal bit for bit to the composed ops) where the transform length
+        allows."""
         length = x.shape[-1]
         n = self._fft_size(length)
+        if (functional.fused_spectrum_supported(n) and len(h.shape) == 2
+                and len(x.shape) >= 2 and h.shape[0] == x.shape[-2]):
+            return autograd.fft_conv(x, h).forward(x, h, n, min(length, n))
         spectrum = x.rfft(n).complex_mul(h.rfft(n))
         return spectrum.irfft(n, min(length, n))
 
