@@ -325,17 +325,19 @@ int wxx_irfft_crop(const void* X, float* x, int64_t rows, int64_t in_len, int64_
  * and its backward (the rfft / irfft / complex_mul adjoints, autograd/utils.py:549-718)
  * with the spectrum products fused into the transforms; each equals, bit for bit, the
  * separate ops it fuses.  n = 2^k, 2 <= n <= 32768.
- * wxx_rfft_mul: wxx_rfft, then bin k of every row times w[k] (n/2+1 bins).
+ * Bin weights w_k are real: w_edge at bins 0 and n/2, w_mid between (the adjoints'
+ * weights), multiplied as the complex (w_k, 0).
+ * wxx_rfft_mul: wxx_rfft, then bin k of every row times w_k.
  * wxx_irfft_mul: wxx_irfft_crop of X * h * w: row r of X times row r mod hrows of h
- *   (conjugated when conj_h) times w, every operand in_len bins per row; null h or w
- *   skips that factor.
+ *   (conjugated when conj_h; null h skips it, h rows have in_len bins) times w_k
+ *   when weighted (in_len must then be n/2 + 1).
  * wxx_complex_mul_batch_sum: out[i] = sum_b a[b n + i] * c[b n + i] (conj when conj_c),
  *   the broadcast filter's gradient summed over the batch. */
-int wxx_rfft_mul(const float* x, void* X, const void* w, int64_t rows, int64_t in_len,
-                 int64_t n);
-int wxx_irfft_mul(const void* X, const void* h, const void* w, float* x, int64_t rows,
-                  int64_t in_len, int64_t hrows, int conj_h, int64_t n, int64_t out_len,
-                  float post_scale);
+int wxx_rfft_mul(const float* x, void* X, int64_t rows, int64_t in_len, int64_t n,
+                 float w_edge, float w_mid);
+int wxx_irfft_mul(const void* X, const void* h, float* x, int64_t rows, int64_t in_len,
+                  int64_t hrows, int conj_h, int weighted, float w_edge, float w_mid, int64_t n,
+                  int64_t out_len, float post_scale);
 int wxx_complex_mul_batch_sum(void* out, const void* a, const void* c, int64_t batch, int64_t n,
                               int conj_c);
 /* functional.complex_mul (fft.py:168-213, op 0) and complex_add_inplace

@@ -364,15 +364,19 @@ def test_spectrum_products_fused_into_transforms(device, n):
     bins = n // 2 + 1
     x = f32(r.standard_normal((2, 3, n)))
     Hn = r.standard_normal((3, bins)) + 1j * r.standard_normal((3, bins))
-    Wn = r.standard_normal(bins) + 1j * r.standard_normal(bins)
-    h, w = c64(Hn), c64(Wn)
+    h = c64(Hn)
+    edge, mid = 0.75, -1.3  # any real weights; the adjoints use powers of two
+    w = F.complex_weights([edge] + [mid] * (bins - 2) + [edge])
     spec, _ = F.rfft(x, n)
-    assert np.array_equal(F.rfft_mul(x, n, w).numpy(), F.complex_mul(spec, w).numpy())
+    assert np.array_equal(F.rfft_mul(x, n, (edge, mid)).numpy(), F.complex_mul(spec, w).numpy())
     for conj in (False, True):
         want = F.irfft(F.complex_mul(F.complex_mul(spec, h, conj_b=conj), w), n,
                        length=n - 3, scale=2.0).numpy()
-        got = F.irfft_mul(spec, n, h=h, weights=w, conj_h=conj, length=n - 3, scale=2.0).numpy()
+        got = F.irfft_mul(spec, n, h=h, conj_h=conj, bin_weights=(edge, mid), length=n - 3,
+                          scale=2.0).numpy()
         assert np.array_equal(got, want)
+        want = F.irfft(F.complex_mul(spec, h, conj_b=conj), n).numpy()
+        assert np.array_equal(F.irfft_mul(spec, n, h=h, conj_h=conj).numpy(), want)
     assert np.array_equal(F.irfft_mul(spec, n).numpy(), F.irfft(spec, n).numpy())
 
 
@@ -381,9 +385,9 @@ def test_spectrum_products_reject_bad_operands(device):
     x = f32(np.zeros((2, 64)))
     spec, _ = F.rfft(x, 64)
     with pytest.raises(ValueError):
-        F.rfft_mul(x, 65536, c64(np.zeros(32769)))
+        F.rfft_mul(x, 65536, (1.0, 0.5))
     with pytest.raises(ValueError):
-        F.rfft_mul(x, 64, c64(np.zeros(32)))  # one bin short
+        F.irfft_mul(spec, 128, bin_weights=(1.0, 0.5))  # 33 bins, 65 needed
     with pytest.raises(ValueError):
         F.irfft_mul(spec, 64, h=c64(np.zeros((3, 33))))  # not a trailing shape
     with pytest.raises(ValueError):

@@ -200,6 +200,8 @@ def test_adaptive_avgpool2d(device, shape, out):
                                            (3, 70, 130, 5, True),    # partial channel / position tiles
                                            (2, 65, 200, 8, False),   # largest tiled kernel size
                                            (2, 9, 40, 9, True),      # untiled kernels (K > 8)
+                                           (2, 7, 36, 6, False),     # 16-byte dx, third load
+                                           (3, 4, 12, 7, True),      # taps past the row end
                                            (5, 130, 64, 1, True)])
 def test_causal_conv1d(device, B, D, L, K, view):
     r = rng(D)

@@ -460,19 +460,20 @@ class fft_conv(Function):
         X, H = self.X, self.H
         self.X = self.H = None
         n = self.N
-        # the irfft adjoint: rfft(g, n) * w_irfft / n
-        wi = functional.complex_weights([v / float(n) for v in _irfft_backward_weights(n)])
-        gs = functional.rfft_mul(g, n, wi)
-        wr = functional.complex_weights(_rfft_backward_weights(n))
+        # the irfft adjoint: rfft(g, n) * w_irfft / n, its weights (1, 2, ..., 2, 1)
+        wi = _irfft_backward_weights(n)
+        gs = functional.rfft_mul(g, n, (wi[0] / float(n), wi[1] / float(n)))
+        wr = _rfft_backward_weights(n)
+        wr = (wr[0], wr[1])  # (1, 0.5, ..., 0.5, 1)
         gx = gh = None
         if self.needs_input_grad[0]:
             # the rfft adjoint of gs * conj(H): irfft(gs conj(H) w_rfft) * n
-            gx = functional.irfft_mul(gs, n, h=H, weights=wr, conj_h=True,
+            gx = functional.irfft_mul(gs, n, h=H, conj_h=True, bin_weights=wr,
                                       length=min(self.x_len, n), scale=float(n))
             gx = _match_last_dim_real(gx, self.x_len)
         if self.needs_input_grad[1]:
             gH = functional.complex_mul_batch_sum(gs, X, conj_c=True, keep=len(H.shape))
-            gh = functional.irfft_mul(gH, n, weights=wr, length=min(self.h_len, n),
+            gh = functional.irfft_mul(gH, n, bin_weights=wr, length=min(self.h_len, n),
                                       scale=float(n))
             gh = _match_last_dim_real(gh, self.h_len)
         return gx, gh

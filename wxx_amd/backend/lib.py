@@ -116,8 +116,8 @@ SIGNATURES = {
     "wxx_complex_binary": (I32, [P, P, P, I32, P, P, P, P, I32, I32, I32]),
     "wxx_complex_conj": (I32, [P, P, I32, P, P, P]),
     "wxx_complex_pad": (I32, [P, P, I64, I64, I64]),
-    "wxx_rfft_mul": (I32, [P, P, P, I64, I64, I64]),
-    "wxx_irfft_mul": (I32, [P, P, P, P, I64, I64, I64, I32, I64, I64, F32]),
+    "wxx_rfft_mul": (I32, [P, P, I64, I64, I64, F32, F32]),
+    "wxx_irfft_mul": (I32, [P, P, P, I64, I64, I64, I32, I32, F32, F32, I64, I64, F32]),
     "wxx_complex_mul_batch_sum": (I32, [P, P, P, I64, I64, I32]),
     # loss
     "wxx_cceloss": (I32, [P, P, P, P, I64, I64, P]),

@@ -90,13 +90,18 @@ __device__ __forceinline__ float2 cmul_op(float2 a, float2 b) {
 
 // Spectrum operands multiplied into a transform's input bins (irfft) or
 // output bins (rfft): bin j of row r becomes v * h[r mod hrows][j]
-// (conjugated when conj_h) * w[j], products in that order; a null operand is
-// skipped.  h rows and w have the spectrum's bins per row.
+// (conjugated when conj_h, skipped when h is null) * (w, 0) (when weighted),
+// products in that order.  The real bin weight w is w_edge at the DC and
+// Nyquist bins (j == 0, j == nyq) and w_mid between them, the form of the
+// rfft / irfft adjoints' weights: two scalars instead of a table, so no load
+// has to wait behind a row prefetch.  h rows have the spectrum's bins per row.
 struct SpecMul {
   const float2* h;
-  const float2* w;
   int64_t hrows;
   int conj_h;
+  int weighted;
+  float w_edge, w_mid;
+  int nyq;
 };
 
 // hr: this row's h row, or null.
@@ -107,7 +112,7 @@ __device__ __forceinline__ float2 spec_mul(float2 v, const SpecMul& m,
     if (m.conj_h) b.y = -b.y;
     v = cmul_op(v, b);
   }
-  if (m.w) v = cmul_op(v, m.w[j]);
+  if (m.weighted) v = cmul_op(v, make_float2(j == 0 || j == m.nyq ? m.w_edge : m.w_mid, 0.f));
   return v;
 }
 
@@ -1153,15 +1158,16 @@ WXX_API int wxx_irfft(const void* X, float* x, int64_t rows, int64_t in_len, int
   return wxx_irfft_crop(X, x, rows, in_len, n, n, 1.0f);
 }
 
-// rfft with each output bin k multiplied by w[k] (w: n/2 + 1 bins): the
-// spectrum product of the irfft backward (reference autograd/utils.py:549-718,
-// complex_mul of rfft(g) with the bin weights) fused into the transform's
-// store.  The product rounds as wxx_complex_binary's does, so the result is
+// rfft with each output bin k multiplied by the real weight w_k = w_edge at
+// k = 0 and k = n/2, w_mid between: the spectrum product of the irfft
+// backward (reference autograd/utils.py:549-718, complex_mul of rfft(g) with
+// the bin weights) fused into the transform's store.  The product rounds as
+// wxx_complex_binary's does with the weight vector (w_k, 0), so the result is
 // the bit pattern of wxx_rfft followed by that product.
-WXX_API int wxx_rfft_mul(const float* x, void* X, const void* w, int64_t rows, int64_t in_len,
-                         int64_t n) {
+WXX_API int wxx_rfft_mul(const float* x, void* X, int64_t rows, int64_t in_len, int64_t n,
+                         float w_edge, float w_mid) {
   WXX_CHECK_INIT();
-  WXX_REQUIRE(x && X && w, "null pointer");
+  WXX_REQUIRE(x && X, "null pointer");
   WXX_REQUIRE(rows >= 0 && in_len >= 0, "bad rfft dims");
   const int logn = log2_exact(n);
   WXX_REQUIRE(logn >= 1 && logn - 1 <= kMaxLogM,
@@ -1170,7 +1176,7 @@ WXX_API int wxx_rfft_mul(const float* x, void* X, const void* w, int64_t rows, i
   if (rows == 0) return WXX_OK;
   const float2* tw = twiddles(logn - 1);
   if (!tw) return wxx::set_error(WXX_E_OOM, "rfft twiddle table allocation failed");
-  const SpecMul sm{nullptr, static_cast<const float2*>(w), 1, 0};
+  const SpecMul sm{nullptr, 1, 0, 1, w_edge, w_mid, (int)(n / 2)};
   const bool vec = in_len % 2 == 0 && (uintptr_t)x % 8 == 0;
   dispatch_rfft(logn - 1, x, static_cast<float2*>(X), tw, rows, in_len, vec, &sm);
   WXX_LAUNCHED();
@@ -1178,15 +1184,16 @@ WXX_API int wxx_rfft_mul(const float* x, void* X, const void* w, int64_t rows, i
 }
 
 // wxx_irfft_crop of the product X * h * w, formed as the bins load: row r of
-// X (in_len bins) times row r mod hrows of h (conjugated when conj_h) times
-// w (in_len bins), products in that order and rounded as wxx_complex_binary's;
-// h or w null skips that factor.  Fuses the Hyena long convolution's
+// X (in_len bins) times row r mod hrows of h (conjugated when conj_h; null h
+// skips it) times, when weighted, the real bin weight (w_edge at bins 0 and
+// n/2, w_mid between; in_len must then be n/2 + 1), products in that order
+// and rounded as wxx_complex_binary's with the weight vector (w_k, 0).  Fuses the Hyena long convolution's
 // spectrum product into its inverse transform (reference nn/hyena.py:208-216:
 // irfft(rfft(x) * rfft(h))) and the filter product and bin weights of its
 // backward into the rfft adjoint (autograd/utils.py:549-718).
-WXX_API int wxx_irfft_mul(const void* X, const void* h, const void* w, float* x, int64_t rows,
-                          int64_t in_len, int64_t hrows, int conj_h, int64_t n, int64_t out_len,
-                          float post_scale) {
+WXX_API int wxx_irfft_mul(const void* X, const void* h, float* x, int64_t rows, int64_t in_len,
+                          int64_t hrows, int conj_h, int weighted, float w_edge, float w_mid,
+                          int64_t n, int64_t out_len, float post_scale) {
   WXX_CHECK_INIT();
   WXX_REQUIRE(x && X, "null pointer");
   WXX_REQUIRE(rows >= 0 && in_len >= 0, "bad irfft dims");
@@ -1197,6 +1204,9 @@ WXX_API int wxx_irfft_mul(const void* X, const void* h, const void* w, float* x,
               2 << kMaxLogM, (long long)n);
   WXX_REQUIRE(out_len >= 1 && out_len <= n, "irfft output length %lld not in [1, %lld]",
               (long long)out_len, (long long)n);
+  WXX_REQUIRE(!weighted || in_len == n / 2 + 1,
+              "bin weights need the n/2 + 1 = %lld bins of the spectrum, got %lld",
+              (long long)(n / 2 + 1), (long long)in_len);
   if (rows == 0) return WXX_OK;
   const float2* tw = twiddles(logn - 1);
   if (!tw) return wxx::set_error(WXX_E_OOM, "irfft twiddle table allocation failed");
@@ -1206,8 +1216,8 @@ WXX_API int wxx_irfft_mul(const void* X, const void* h, const void* w, float* x,
   ro.half = (int)(out_len / 2);
   ro.post = post_scale;
   ro.mode = out_len == n ? 0 : (out_len % 2 == 0 ? 1 : 2);
-  const SpecMul sm{static_cast<const float2*>(h), static_cast<const float2*>(w),
-                   h ? hrows : 1, conj_h ? 1 : 0};
+  const SpecMul sm{static_cast<const float2*>(h), h ? hrows : 1, conj_h ? 1 : 0,
+                   weighted ? 1 : 0, w_edge, w_mid, (int)(n / 2)};
   dispatch_irfft(logn - 1, static_cast<const float2*>(X), x, tw, rows, in_len, ro, &sm);
   WXX_LAUNCHED();
   return WXX_OK;

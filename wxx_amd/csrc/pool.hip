@@ -331,6 +331,45 @@ __global__ __launch_bounds__(kBlock) void causal_conv1d_dx_rows_kernel(
   }
 }
 
+// The same dx with four consecutive positions per thread (L a multiple of 4,
+// 16-byte aligned rows, KS <= kCMaxKS): the inputs dy[n .. n + 3 + KS - 1]
+// come through two or three 16-byte loads issued together, then the four
+// sums run the row kernel's FMA sequence (acc from 0, taps in order, taps
+// past the row skipped), so the values are the same bits.  Grid
+// (ceil(L / (4 kBlock)), rows).
+__global__ __launch_bounds__(kBlock) void causal_conv1d_dx_vec_kernel(
+    const float* __restrict__ dy, const float* __restrict__ w, float* __restrict__ dx, int D,
+    int L, int KS, int64_t rows) {
+  const int L4 = L / 4;
+  const int q = blockIdx.x * kBlock + threadIdx.x;  // float4 index within the row
+  if (q >= L4) return;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    const int d = (int)(r % D);
+    const float4* g4 = reinterpret_cast<const float4*>(dy + r * L);
+    float gv[12];
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+      float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+      if ((u < 2 || KS > 5) && q + u < L4) t = g4[q + u];
+      gv[4 * u] = t.x;
+      gv[4 * u + 1] = t.y;
+      gv[4 * u + 2] = t.z;
+      gv[4 * u + 3] = t.w;
+    }
+    float out[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int n = 4 * q + i;
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < kCMaxKS; ++k)
+        if (k < KS && n + k < L) acc = fmaf(w[d * KS + k], gv[i + k], acc);
+      out[i] = acc;
+    }
+    reinterpret_cast<float4*>(dx + r * L)[q] = make_float4(out[0], out[1], out[2], out[3]);
+  }
+}
+
 // Weight / bias gradient partials: workgroup (s, t) sums the (b, position)
 // tiles s, s + S, s + 2S, ... of channel tile t in one pass over dy and x,
 // all KS + 1 sums at once (k == KS: the bias).  Lane = channel, the four
@@ -341,7 +380,10 @@ __global__ __launch_bounds__(kBlock) void causal_conv1d_dw_tiled_kernel(
     float* __restrict__ part, int B, int D, int L, int KS) {
   __shared__ float xs[kCT][kCW];
   __shared__ float gs[kCT][kCT + 1];
-  __shared__ float red[kBlock / kCT][kCT][kCMaxKS + 1];
+  // the waves' final sums reuse the x tile's LDS (35 KB a workgroup, so the
+  // four per CU the launch sizes for are resident together)
+  static_assert((kBlock / kCT) * kCT * (kCMaxKS + 1) <= kCT * kCW, "sums exceed the x tile");
+  auto red = reinterpret_cast<float(*)[kCT][kCMaxKS + 1]>(&xs[0][0]);
   const int d0 = blockIdx.y * kCT;
   const int ntl = (L + kCT - 1) / kCT;
   const int64_t tiles = (int64_t)B * ntl;
@@ -378,6 +420,7 @@ __global__ __launch_bounds__(kBlock) void causal_conv1d_dw_tiled_kernel(
       acc[kCMaxKS] += g;
     }
   }
+  __syncthreads();  // the last tile's reads of xs are done
 #pragma unroll
   for (int k = 0; k <= kCMaxKS; ++k) red[wv][dd][k] = acc[k];
   __syncthreads();
@@ -560,8 +603,13 @@ WXX_API int wxx_causal_conv1d_backward(const float* dy, const float* x, int64_t 
     const int64_t rows = B * D;
     const dim3 grid((unsigned)((L + 4 * kBlock - 1) / (4 * kBlock)),
                     (unsigned)std::min<int64_t>(rows, 65535));
-    hipLaunchKernelGGL(causal_conv1d_dx_rows_kernel, grid, dim3(kBlock), 0, s, dy, w, dx, (int)D,
-                       (int)L, (int)KS, rows);
+    auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    if (KS <= kCMaxKS && L % 4 == 0 && al16(dy) && al16(dx))
+      hipLaunchKernelGGL(causal_conv1d_dx_vec_kernel, grid, dim3(kBlock), 0, s, dy, w, dx,
+                         (int)D, (int)L, (int)KS, rows);
+    else
+      hipLaunchKernelGGL(causal_conv1d_dx_rows_kernel, grid, dim3(kBlock), 0, s, dy, w, dx,
+                         (int)D, (int)L, (int)KS, rows);
   }
   if (dw) {
     View3 v{x_off, sb, sc, sl};

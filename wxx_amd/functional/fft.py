@@ -230,36 +230,41 @@ def _contig_c64(t, name):
     return t if t.is_contiguous() else complex_contiguous(t)
 
 
-def rfft_mul(tensor1, n, weights):
-    """``complex_mul(rfft(tensor1, n)[0], weights)`` in one kernel: bin k of
-    every row times ``weights[k]`` (a c64 vector of ``n // 2 + 1`` bins) as
-    the transform stores it, rounded as complex_mul rounds (the irfft
-    backward's spectrum product, reference autograd/utils.py:549-718)."""
+def _bin_weights(bin_weights):
+    edge, mid = bin_weights
+    return C.c_float(float(edge)), C.c_float(float(mid))
+
+
+def rfft_mul(tensor1, n, bin_weights):
+    """``complex_mul(rfft(tensor1, n)[0], w)`` in one kernel, for the real bin
+    weights ``bin_weights = (edge, mid)``: w_k = edge at k = 0 and n/2, mid
+    between (the weights of the rfft / irfft adjoints), multiplied as the
+    transform stores each bin and rounded as complex_mul rounds with the
+    vector (w_k, 0) (the irfft backward's spectrum product, reference
+    autograd/utils.py:549-718)."""
     if tensor1.type == "c64":
         raise TypeError("rfft_mul expects a real-valued tensor")
     n = int(n)
     if not fused_spectrum_supported(n):
         raise ValueError(f"rfft_mul needs a power-of-two n in [2, {FUSED_MAX_N}], got {n}")
-    weights = _contig_c64(weights, "rfft_mul")
-    if tuple(weights.shape) != (n // 2 + 1,):
-        raise ValueError(f"rfft_mul weights must have shape ({n // 2 + 1},), "
-                         f"got {tuple(weights.shape)}")
+    edge, mid = _bin_weights(bin_weights)
     if not tensor1.is_contiguous():
         tensor1 = tensor1.contiguous()
     validation.check_rank(tensor1.shape, min_rank=1, name="rfft_mul input")
     shape = list(tensor1.shape)
     rows = validation.numel(shape[:-1])
     out = empty(shape[:-1] + [n // 2 + 1], dtype="c64")
-    call("wxx_rfft_mul", ptr(tensor1), ptr(out), ptr(weights), rows, shape[-1], n)
+    call("wxx_rfft_mul", ptr(tensor1), ptr(out), rows, shape[-1], n, edge, mid)
     return out
 
 
-def irfft_mul(tensor1, n, h=None, weights=None, conj_h=False, length=None, scale=1.0):
-    """``irfft(tensor1 * h * weights, n, length, scale)`` with the products
-    formed as the bins load, rounded as complex_mul rounds.  ``h`` (c64, the
-    trailing dims of ``tensor1``'s shape) broadcasts over ``tensor1``'s
-    leading dims and is conjugated when ``conj_h``; ``weights`` is one row of
-    bins; either may be None.  The Hyena long convolution's forward product
+def irfft_mul(tensor1, n, h=None, conj_h=False, bin_weights=None, length=None, scale=1.0):
+    """``irfft(tensor1 * h * w, n, length, scale)`` with the products formed
+    as the bins load, rounded as complex_mul rounds.  ``h`` (c64, the trailing
+    dims of ``tensor1``'s shape) broadcasts over ``tensor1``'s leading dims
+    and is conjugated when ``conj_h``; ``bin_weights = (edge, mid)`` are real
+    bin weights as in ``rfft_mul`` (the spectrum then needs its n/2 + 1
+    bins); either may be None.  The Hyena long convolution's forward product
     and its backward's filter product (reference nn/hyena.py:208-216)."""
     tensor1 = _contig_c64(tensor1, "irfft_mul")
     validation.check_rank(tensor1.shape, min_rank=1, name="irfft_mul input")
@@ -277,18 +282,18 @@ def irfft_mul(tensor1, n, h=None, weights=None, conj_h=False, length=None, scale
             raise ValueError(f"irfft_mul operand shape {tuple(hs)} is not a trailing part "
                              f"of {tuple(shape)}")
         hrows = validation.numel(hs[:-1])
-    if weights is not None:
-        weights = _contig_c64(weights, "irfft_mul")
-        if tuple(weights.shape) != (in_len,):
-            raise ValueError(f"irfft_mul weights must have shape ({in_len},), "
-                             f"got {tuple(weights.shape)}")
+    weighted = bin_weights is not None
+    if weighted and in_len != n // 2 + 1:
+        raise ValueError(f"irfft_mul bin weights need the {n // 2 + 1} bins of the spectrum, "
+                         f"got {in_len}")
+    edge, mid = _bin_weights(bin_weights if weighted else (1.0, 1.0))
     length = n if length is None else int(length)
     if not 1 <= length <= n:
         raise ValueError(f"irfft length must be in [1, {n}], got {length}")
     out = empty(shape[:-1] + [length])
-    call("wxx_irfft_mul", ptr(tensor1), ptr(h) if h is not None else None,
-         ptr(weights) if weights is not None else None, ptr(out), rows, in_len, max(hrows, 1),
-         1 if conj_h else 0, n, length, C.c_float(scale))
+    call("wxx_irfft_mul", ptr(tensor1), ptr(h) if h is not None else None, ptr(out), rows,
+         in_len, max(hrows, 1), 1 if conj_h else 0, 1 if weighted else 0, edge, mid, n, length,
+         C.c_float(scale))
     return out
 
 
