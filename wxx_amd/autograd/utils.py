@@ -460,11 +460,12 @@ class fft_conv(Function):
         X, H = self.X, self.H
         self.X = self.H = None
         n = self.N
-        # the irfft adjoint: rfft(g, n) * w_irfft / n, its weights (1, 2, ..., 2, 1)
-        wi = _irfft_backward_weights(n)
-        gs = functional.rfft_mul(g, n, (wi[0] / float(n), wi[1] / float(n)))
-        wr = _rfft_backward_weights(n)
-        wr = (wr[0], wr[1])  # (1, 0.5, ..., 0.5, 1)
+        # the adjoints' bin weights as (edge, interior) scalars: the irfft
+        # adjoint rfft(g, n) * (1, 2, ..., 2, 1) / n, the rfft adjoint's
+        # (1, 0.5, ..., 0.5, 1) (_irfft_backward_weights, _rfft_backward_weights;
+        # at n = 2 both bins are edges and the interior value is unused)
+        gs = functional.rfft_mul(g, n, (1.0 / float(n), 2.0 / float(n)))
+        wr = (1.0, 0.5)
         gx = gh = None
         if self.needs_input_grad[0]:
             # the rfft adjoint of gs * conj(H): irfft(gs conj(H) w_rfft) * n
