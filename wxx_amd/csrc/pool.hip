@@ -287,9 +287,27 @@ __global__ __launch_bounds__(kBlock) void causal_conv1d_tiled_kernel(
     const float* __restrict__ x, View3 v, const float* __restrict__ w,
     const float* __restrict__ bias, float* __restrict__ y, int D, int L, int KS) {
   __shared__ float xs[kCT][kCW];
+  // the tile's weights and biases, staged with the window: a channel index
+  // formed from threadIdx.x is not known to be wave-uniform, so reading them
+  // from global memory in the loop below would be one vector load (and one
+  // wait behind the streaming loads) per tap and channel
+  __shared__ float ws[kCT][kCMaxKS + 1];  // [dd][k], k == kCMaxKS: bias
   const int n0 = blockIdx.x * kCT, d0 = blockIdx.y * kCT;
   const int64_t b = blockIdx.z;
+  float wr[(kCT * (kCMaxKS + 1) + kBlock - 1) / kBlock];
+#pragma unroll
+  for (int it = 0; it < (kCT * (kCMaxKS + 1) + kBlock - 1) / kBlock; ++it) {
+    const int i = threadIdx.x + it * kBlock;
+    const int c = i / (kCMaxKS + 1), k = i % (kCMaxKS + 1);
+    const bool in = i < kCT * (kCMaxKS + 1) && d0 + c < D && (k < KS || k == kCMaxKS);
+    wr[it] = in ? (k == kCMaxKS ? bias[d0 + c] : w[(d0 + c) * KS + k]) : 0.f;
+  }
   conv_stage_x(xs, x, v, b, d0, n0, D, L, KS);
+#pragma unroll
+  for (int it = 0; it < (kCT * (kCMaxKS + 1) + kBlock - 1) / kBlock; ++it) {
+    const int i = threadIdx.x + it * kBlock;
+    if (i < kCT * (kCMaxKS + 1)) ws[i / (kCMaxKS + 1)][i % (kCMaxKS + 1)] = wr[it];
+  }
   __syncthreads();
   const int nn = threadIdx.x % kCT;
   const int n = n0 + nn;
@@ -298,9 +316,9 @@ __global__ __launch_bounds__(kBlock) void causal_conv1d_tiled_kernel(
   for (int dd = threadIdx.x / kCT; dd < kCT; dd += kBlock / kCT) {
     const int d = d0 + dd;
     if (d >= D) break;
-    float acc = bias[d];
+    float acc = ws[dd][kCMaxKS];
     for (int k = 0; k < KS; ++k)  // same order and terms as the untiled kernel
-      if (n >= k) acc = fmaf(w[d * KS + k], xs[dd][nn + KS - 1 - k], acc);
+      if (n >= k) acc = fmaf(ws[dd][k], xs[dd][nn + KS - 1 - k], acc);
     y[(b * D + d) * (int64_t)L + n] = acc;
   }
 }
