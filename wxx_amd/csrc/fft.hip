@@ -104,15 +104,19 @@ struct SpecMul {
   int nyq;
 };
 
-// hr: this row's h row, or null.
+// OPS (fixed at compile time, so no bin's loads sit behind a branch of its
+// own): bit 0 the h factor (hr: this row's h row), bit 1 the bin weight.
+constexpr int kOpH = 1, kOpW = 2;
+template <int OPS>
 __device__ __forceinline__ float2 spec_mul(float2 v, const SpecMul& m,
                                            const float2* __restrict__ hr, int64_t j) {
-  if (hr) {
+  if constexpr ((OPS & kOpH) != 0) {
     float2 b = hr[j];
     if (m.conj_h) b.y = -b.y;
     v = cmul_op(v, b);
   }
-  if (m.weighted) v = cmul_op(v, make_float2(j == 0 || j == m.nyq ? m.w_edge : m.w_mid, 0.f));
+  if constexpr ((OPS & kOpW) != 0)
+    v = cmul_op(v, make_float2(j == 0 || j == m.nyq ? m.w_edge : m.w_mid, 0.f));
   return v;
 }
 
@@ -327,13 +331,13 @@ __global__ __launch_bounds__(Geo<LOGM>::NT) void rfft_kernel(const float* __rest
     const float2 o = make_float2(0.5f * (a.y + b.y), 0.5f * (b.x - a.x));
     const float2 w = wu[k];
     const float2 z = make_float2(e.x + (w.x * o.x - w.y * o.y), e.y + (w.x * o.y + w.y * o.x));
-    Xr[k] = MUL ? spec_mul(z, sm, nullptr, k) : z;
+    Xr[k] = MUL ? spec_mul<kOpW>(z, sm, nullptr, k) : z;
   }
 }
 
 // X: rows x in_len c64 one-sided spectrum; x: rows x n f32 (n = 2M).
-// MUL: input bins multiplied by sm's operands (spec_mul) as they load.
-template <int LOGM, int CROP, bool MUL>
+// MUL: the spec_mul operand mask applied to the input bins as they load (0: none).
+template <int LOGM, int CROP, int MUL>
 __global__ __launch_bounds__(Geo<LOGM>::NT) void irfft_kernel(const float2* __restrict__ X,
                                                               float* __restrict__ x,
                                                               const float2* __restrict__ tw,
@@ -349,7 +353,7 @@ __global__ __launch_bounds__(Geo<LOGM>::NT) void irfft_kernel(const float2* __re
   float2* buf = lds + rb * G::PM;
   const float2* Xr = X + (live ? row : 0) * in_len;
   const float2* wu = tw + pl.offset(pl.npass());
-  const float2* hr = MUL && sm.h ? sm.h + ((live ? row : 0) % sm.hrows) * in_len : nullptr;
+  const float2* hr = (MUL & kOpH) ? sm.h + ((live ? row : 0) % sm.hrows) * in_len : nullptr;
 
   // Pack the Hermitian spectrum into Z = E + i O (E, O: spectra of the even
   // and odd samples).  Bins at or above in_len are zero; the imaginary parts
@@ -364,8 +368,8 @@ __global__ __launch_bounds__(Geo<LOGM>::NT) void irfft_kernel(const float2* __re
       const int jj = G::M - j;
       float2 a = make_float2(0.f, 0.f), b = make_float2(0.f, 0.f);
       if (live) {
-        if (j < in_len) a = MUL ? spec_mul(Xr[j], sm, hr, j) : Xr[j];
-        if (jj < in_len) b = MUL ? spec_mul(Xr[jj], sm, hr, jj) : Xr[jj];
+        if (j < in_len) a = MUL ? spec_mul<MUL>(Xr[j], sm, hr, j) : Xr[j];
+        if (jj < in_len) b = MUL ? spec_mul<MUL>(Xr[jj], sm, hr, jj) : Xr[jj];
       }
       if (j == 0) a.y = 0.f;
       if (jj == G::M) b.y = 0.f;
@@ -672,8 +676,8 @@ __global__ __launch_bounds__(Big<LOGM>::T, Big<LOGM>::MIN_WAVES) void rfft_big_k
       const float2 wo = cmul(w, o);
       const float2 lo = make_float2(e.x + wo.x, e.y + wo.y);
       const float2 hi = make_float2(e.x - wo.x, wo.y - e.y);
-      Xr[k] = MUL ? spec_mul(lo, sm, nullptr, k) : lo;
-      if (k != G::M / 2) Xr[G::M - k] = MUL ? spec_mul(hi, sm, nullptr, G::M - k) : hi;
+      Xr[k] = MUL ? spec_mul<kOpW>(lo, sm, nullptr, k) : lo;
+      if (k != G::M / 2) Xr[G::M - k] = MUL ? spec_mul<kOpW>(hi, sm, nullptr, G::M - k) : hi;
     }
     __syncthreads();  // the row buffer is free for the next row
   }
@@ -689,7 +693,7 @@ __host__ __device__ constexpr int big_pos0(int e) {
 }
 
 // Spectrum bins of one irfft row at this thread's pass-0 positions.
-template <int LOGM, bool FULL, bool MUL>
+template <int LOGM, bool FULL, int MUL>
 __device__ __forceinline__ void irfft_big_load(float2* a, const float2* __restrict__ Xr, int t,
                                                int64_t in_len, const SpecMul& sm,
                                                const float2* __restrict__ hr) {
@@ -697,12 +701,12 @@ __device__ __forceinline__ void irfft_big_load(float2* a, const float2* __restri
 #pragma unroll
   for (int e = 0; e < G::E; ++e) {
     const int j = t + big_pos0<LOGM>(e);
-    a[e] = (FULL || j < in_len) ? (MUL ? spec_mul(Xr[j], sm, hr, j) : Xr[j])
+    a[e] = (FULL || j < in_len) ? (MUL ? spec_mul<MUL>(Xr[j], sm, hr, j) : Xr[j])
                                 : make_float2(0.f, 0.f);  // FULL: in_len >= M
   }
 }
 
-template <int LOGM, int CROP, bool MUL>
+template <int LOGM, int CROP, int MUL>
 __global__ __launch_bounds__(Big<LOGM>::T, Big<LOGM>::MIN_WAVES) void irfft_big_kernel(
     const float2* __restrict__ X, float* __restrict__ x, const float2* __restrict__ tw,
     int64_t rows, int64_t in_len, RowOut ro, SpecMul sm) {
@@ -721,12 +725,12 @@ __global__ __launch_bounds__(Big<LOGM>::T, Big<LOGM>::MIN_WAVES) void irfft_big_
     WXX_OPAQUE(wtr.x);
     WXX_OPAQUE(wtr.y);
     const float2* Xr = X + row * in_len;
-    const float2* hr = MUL && sm.h ? sm.h + (row % sm.hrows) * in_len : nullptr;
+    const float2* hr = (MUL & kOpH) ? sm.h + (row % sm.hrows) * in_len : nullptr;
     if (in_len >= G::M)
       irfft_big_load<LOGM, true, MUL>(v, Xr, t, in_len, sm, hr);
     else
       irfft_big_load<LOGM, false, MUL>(v, Xr, t, in_len, sm, hr);
-    const float2 nyq = G::M < in_len ? (MUL ? spec_mul(Xr[G::M], sm, hr, G::M) : Xr[G::M])
+    const float2 nyq = G::M < in_len ? (MUL ? spec_mul<MUL>(Xr[G::M], sm, hr, G::M) : Xr[G::M])
                                      : make_float2(0.f, 0.f);
     // exchange the bins through LDS to pair j with M - j
     const int tb = bpad(t), nb = -t + ((-t) >> 5);  // bpad(t), and bpad(a - t) - bpad_c(a)
@@ -890,7 +894,7 @@ void launch_rfft(const float* x, float2* X, const float2* tw, int64_t rows, int6
   }
 }
 
-template <int LOGM, int CROP, bool MUL>
+template <int LOGM, int CROP, int MUL>
 void launch_irfft_mode(const float2* X, float* x, const float2* tw, int64_t rows, int64_t in_len,
                        RowOut ro, const SpecMul& sm) {
   ro.scale = 1.0f / (float)(1 << LOGM);
@@ -912,7 +916,7 @@ void launch_irfft_mode(const float2* X, float* x, const float2* tw, int64_t rows
                      tw, rows, in_len, ro, sm);
 }
 
-template <int LOGM, bool MUL>
+template <int LOGM, int MUL>
 void launch_irfft_m(const float2* X, float* x, const float2* tw, int64_t rows, int64_t in_len,
                     const RowOut& ro, const SpecMul& sm) {
   if (ro.mode == 0)
@@ -926,10 +930,15 @@ void launch_irfft_m(const float2* X, float* x, const float2* tw, int64_t rows, i
 template <int LOGM>
 void launch_irfft(const float2* X, float* x, const float2* tw, int64_t rows, int64_t in_len,
                   const RowOut& ro, const SpecMul* sm) {
-  if (sm)
-    launch_irfft_m<LOGM, true>(X, x, tw, rows, in_len, ro, *sm);
+  const int ops = sm ? (sm->h ? kOpH : 0) | (sm->weighted ? kOpW : 0) : 0;
+  if (ops == kOpH)
+    launch_irfft_m<LOGM, kOpH>(X, x, tw, rows, in_len, ro, *sm);
+  else if (ops == kOpW)
+    launch_irfft_m<LOGM, kOpW>(X, x, tw, rows, in_len, ro, *sm);
+  else if (ops == (kOpH | kOpW))
+    launch_irfft_m<LOGM, kOpH | kOpW>(X, x, tw, rows, in_len, ro, *sm);
   else
-    launch_irfft_m<LOGM, false>(X, x, tw, rows, in_len, ro, SpecMul{});
+    launch_irfft_m<LOGM, 0>(X, x, tw, rows, in_len, ro, SpecMul{});
 }
 
 template <int L = 0>
