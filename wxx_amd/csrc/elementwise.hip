@@ -135,18 +135,32 @@ __global__ __launch_bounds__(kBlock) void binary_transposed_kernel(
   const int64_t tsn = tr == 1 ? sa2 : sb2;
   const float* R = tr == 1 ? b + bt * sb0 : a + bt * sa0;  // row-major: unit stride along N
   const int64_t rsm = tr == 1 ? sb1 : sa1;
+  // Indices past the edge are clamped into the tensor rather than guarded, so
+  // every load is unconditional and all of a thread's loads (both operands)
+  // issue before the first wait; a guarded load sits behind a branch of its
+  // own and waits alone.  Clamped values reach no stored output.
+  float tl[16], rv[16];
 #pragma unroll
-  for (int r = ty; r < 64; r += 4) {
-    const int n = n0 + r, m = m0 + tx;
-    if (n < N && m < M) t[r][tx] = T[(int64_t)n * tsn + m];
+  for (int i = 0; i < 16; ++i) {
+    const int n = min(n0 + ty + 4 * i, N - 1), m = min(m0 + tx, M - 1);
+    tl[i] = T[(int64_t)n * tsn + m];
   }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int m = min(m0 + ty + 4 * i, M - 1), n = min(n0 + tx, N - 1);
+    rv[i] = R[(int64_t)m * rsm + n];
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) t[ty + 4 * i][tx] = tl[i];
   __syncthreads();
 #pragma unroll
-  for (int r = ty; r < 64; r += 4) {
+  for (int i = 0; i < 16; ++i) {
+    const int r = ty + 4 * i;
     const int m = m0 + r, n = n0 + tx;
     if (m < M && n < N) {
-      const float tv = t[tx][r], rv = R[(int64_t)m * rsm + n];
-      out[bt * so0 + (int64_t)m * so1 + n] = tr == 1 ? binop(op, tv, rv) : binop(op, rv, tv);
+      const float tv = t[tx][r];
+      out[bt * so0 + (int64_t)m * so1 + n] =
+          tr == 1 ? binop(op, tv, rv[i]) : binop(op, rv[i], tv);
     }
   }
 }
