@@ -489,10 +489,17 @@ __global__ __launch_bounds__(kBlock) void transpose_tile_kernel(T* __restrict__ 
   const int64_t b = blockIdx.z;
   const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // 64 x 4
-  for (int k = ty; k < 64; k += 4) {
-    const int64_t c = c0 + k, r = r0 + tx;
-    if (c < cols && r < rows) tile[k][tx] = src[b * sb + r * sr + c * sc];
+  // edge indices clamped into the tensor instead of guarded: every load is
+  // unconditional and all 16 issue before the first wait (a guarded load sits
+  // behind a branch of its own and waits alone); clamped values reach no store
+  T tl[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t c = min(c0 + ty + 4 * i, cols - 1), r = min(r0 + tx, rows - 1);
+    tl[i] = src[b * sb + r * sr + c * sc];
   }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) tile[ty + 4 * i][tx] = tl[i];
   __syncthreads();
   for (int k = ty; k < 64; k += 4) {
     const int64_t r = r0 + k, c = c0 + tx;
